@@ -1,0 +1,105 @@
+/*
+ * ifx_qgemm.h -- C ABI of the MI355X (gfx950) quantized GEMV/GEMM path.
+ *
+ * Drop-in replacement for the fused GGUF dequant-GEMV/GEMM operators of
+ * InferFlux's native backend, class FusedQuantGemm
+ * (runtime/backends/cuda/native/fused_quant_gemm.h:47-398).  Plain pointers
+ * and sizes only; every device pointer is caller-owned device memory and
+ * every call is enqueued on the caller's HIP stream (passed as void*, a
+ * hipStream_t; NULL = the default stream).  Nothing here synchronises the
+ * host, and the GEMV/GEMM/quantize entry points allocate nothing.
+ *
+ * Layouts (as in the reference, weight_map.h:17-21 and
+ * quantized_weight_map.cpp:379-434):
+ *   W  raw GGUF blocks, row-major [N][K/QK]; row n starts at
+ *      W + n * (K/QK) * block_bytes.  QK = 256 for Q4_K/Q6_K, 32 for Q8_0.
+ *   A  Q8_1 activations [M][K/32], 36-byte blocks {f16 d, f16 s, i8 qs[32]}.
+ *   Y  [M][N] row-major, fp32 or fp16.
+ *
+ * Status codes: 0 = launched; > 0 = not handled, use a fallback (the
+ * reference's `false`); < 0 = -(hipError_t) reported by the launch.
+ */
+#ifndef IFX_QGEMM_H
+#define IFX_QGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type ids (runtime/backends/cuda/native/gguf_util.h:48-63). */
+enum ifx_quant_type {
+  IFX_TYPE_Q8_0 = 8,
+  IFX_TYPE_Q8_1 = 9,
+  IFX_TYPE_Q4_K = 12,
+  IFX_TYPE_Q6_K = 14
+};
+
+enum ifx_status {
+  IFX_OK = 0,
+  IFX_UNSUPPORTED_TYPE = 1, /* quant type has no kernel              */
+  IFX_BAD_GEOMETRY = 2,     /* M, N or K out of range / not a multiple */
+  IFX_NULL_POINTER = 3,     /* a required pointer is NULL            */
+  IFX_DISABLED = 4          /* policy disabled the fused path (C++ wrapper) */
+};
+
+enum ifx_out_dtype { IFX_OUT_F32 = 0, IFX_OUT_F16 = 1 };
+
+enum ifx_out_mode {
+  IFX_STORE = 0, /* Y  = W.a                         (GemvQ8_1)            */
+  IFX_ACCUM = 1, /* Y += W.a                         (GemvQ8_1Accum[F32])  */
+  IFX_BIAS = 2   /* Y  = W.a + bias[n], bias dtype = Y dtype (GemvQ8_1WithBias) */
+};
+
+/* Activation quantizer fp32 -> Q8_1, the BASELINE contract.
+ * Replaces FusedQuantGemm::QuantizeRowQ8_1 (fused_quant_gemm.h:118-119;
+ * kernel fused_dequant_gemv.cuh:597-655).  x [M][K] fp32, K % 32 == 0. */
+int ifx_q8_1_quantize_f32(const float *x, void *q8_1, int M, int K, void *stream);
+
+/* Same, fp16 input: the reference's own signature (const half* input). */
+int ifx_q8_1_quantize_f16(const uint16_t *x, void *q8_1, int M, int K, void *stream);
+
+/* Quantized GEMV/GEMM y[m][n] (op)= sum_k W[n][k] * a[m][k] for any M >= 1.
+ * Replaces FusedQuantGemm::GemvQ8_1 / GemvQ8_1Accum / GemvQ8_1AccumF32 /
+ * GemvQ8_1WithBias (fused_quant_gemm.h:171-173, 190-193, 202-205; .cu
+ * 2085-2260) and the dispatch DispatchQ8_1Gemv{Q4K,Q6K,Q8_0}
+ * (fused_quant_gemm.cu:1705-1738).  M <= 8 runs the weight-streaming GEMV,
+ * larger M the int8-MFMA GEMM (the reference returns false for M > 64 and
+ * falls back to FP16 cuBLAS; here every M is handled).
+ * out_dtype: ifx_out_dtype.  mode: ifx_out_mode.  bias may be NULL unless
+ * mode == IFX_BIAS. */
+int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
+              int mode, const void *bias, int M, int N, int K, void *stream);
+
+/* The prefill GEMM alone (int8 MFMA, fp32 accumulate), for any M >= 1.
+ * Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
+ * (quantized_weight_map.cpp:176-233, cublas_gemm.h:47, called at
+ * transformer_forward.cu:1479). */
+int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                      int out_dtype, int mode, const void *bias, int M, int N, int K,
+                      void *stream);
+
+/* Whole-tensor dequantization of n_rows x K weights to fp32 or fp16.
+ * Replaces dequantize_q4_k / dequantize_q6_k / dequantize_q8_0
+ * (kernels/dequantization.cuh:70-150). */
+int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows,
+                   int K, void *stream);
+
+/* 1 if ifx_qgemv handles (quant_type, M, N, K), else 0.
+ * Replaces FusedQuantGemm::SupportsQ8_1Activations (fused_quant_gemm.h:333)
+ * combined with ShouldUseFusedPath (fused_quant_gemm.h:388-391). */
+int ifx_supports(int quant_type, int M, int N, int K);
+
+/* Bytes per block / values per block of a quant type (0 if unknown). */
+int ifx_block_bytes(int quant_type);
+int ifx_block_elems(int quant_type);
+
+/* Human-readable name of a status code. */
+const char *ifx_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IFX_QGEMM_H */

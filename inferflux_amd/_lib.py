@@ -1,0 +1,48 @@
+"""Loads libifx_qgemm.so (the HIP kernels behind include/ifx_qgemm.h) with
+ctypes and declares every exported C entry point.
+
+There is no fallback: if the library is missing this raises, so nothing can
+silently run another implementation in its place.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libifx_qgemm.so")
+
+# Every symbol include/ifx_qgemm.h declares, with its ctypes signature.
+_vp, _i32, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+SIGNATURES = {
+    "ifx_q8_1_quantize_f32": ([_vp, _vp, _i32, _i32, _vp], _i32),
+    "ifx_q8_1_quantize_f16": ([_vp, _vp, _i32, _i32, _vp], _i32),
+    "ifx_qgemv": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
+    "ifx_supports": ([_i32, _i32, _i32, _i32], _i32),
+    "ifx_block_bytes": ([_i32], _i32),
+    "ifx_block_elems": ([_i32], _i32),
+    "ifx_status_string": ([_i32], ctypes.c_char_p),
+}
+
+_lib = None
+
+
+class IfxError(RuntimeError):
+    pass
+
+
+def load():
+    """Returns the loaded library; raises IfxError if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise IfxError(
+                "libifx_qgemm.so is not built (run `python -m inferflux_amd.build`); "
+                "the quantized GEMV/GEMM path has no other implementation")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib

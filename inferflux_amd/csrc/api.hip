@@ -1,0 +1,133 @@
+// api.hip -- the C ABI (include/ifx_qgemm.h): argument validation and
+// dispatch by quant type and batch size onto the gfx950 kernels.
+//
+// Validation mirrors FusedQuantGemm::GemvQ8_1
+// (runtime/backends/cuda/native/fused_quant_gemm.cu:2085-2117): a NULL
+// pointer, an unsupported type or a bad geometry is "not handled" (a positive
+// status, the reference's `false`) and launches nothing.  Unlike the
+// reference, launch errors are checked (hipGetLastError after each launch)
+// and returned as a negative status.
+#include "../../include/ifx_qgemm.h"
+#include "ifx_common.h"
+
+namespace ifx {
+hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
+                                hipStream_t stream);
+hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int64_t n_elems,
+                             hipStream_t stream);
+hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const void *bias,
+                       bool f16, int M, int N, int K, int mode, hipStream_t stream);
+hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
+                            bool f16, int M, int N, int K, int mode, hipStream_t stream);
+}  // namespace ifx
+
+namespace {
+
+constexpr int kMaxGemvM = 8;  // M <= 8: weight-streaming GEMV; larger: MFMA GEMM
+
+int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
+
+bool is_weight_type(int t) {
+  return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0;
+}
+
+int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int out_dtype,
+                    int mode, const void *bias, int M, int N, int K) {
+  if (!W || !A || !Y) return IFX_NULL_POINTER;
+  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (out_dtype != IFX_OUT_F32 && out_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (mode != IFX_STORE && mode != IFX_ACCUM && mode != IFX_BIAS) return IFX_BAD_GEOMETRY;
+  if (mode == IFX_BIAS && !bias) return IFX_NULL_POINTER;
+  if (M <= 0 || N <= 0 || K <= 0) return IFX_BAD_GEOMETRY;
+  if (K % ifx_block_elems(quant_type) != 0) return IFX_BAD_GEOMETRY;
+  // Row offsets are formed in 64-bit; the 32-bit grid limits N and M.
+  if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
+  return IFX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ifx_block_bytes(int quant_type) {
+  switch (quant_type) {
+  case IFX_TYPE_Q4_K: return ifx::kQ4KBytes;
+  case IFX_TYPE_Q6_K: return ifx::kQ6KBytes;
+  case IFX_TYPE_Q8_0: return ifx::kQ8_0Bytes;
+  case IFX_TYPE_Q8_1: return ifx::kQ8_1Bytes;
+  default: return 0;
+  }
+}
+
+int ifx_block_elems(int quant_type) {
+  switch (quant_type) {
+  case IFX_TYPE_Q4_K: case IFX_TYPE_Q6_K: return 256;
+  case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: return 32;
+  default: return 0;
+  }
+}
+
+const char *ifx_status_string(int status) {
+  switch (status) {
+  case IFX_OK: return "ok";
+  case IFX_UNSUPPORTED_TYPE: return "unsupported quant type";
+  case IFX_BAD_GEOMETRY: return "bad geometry or argument";
+  case IFX_NULL_POINTER: return "null pointer";
+  case IFX_DISABLED: return "fused path disabled by policy";
+  default: return status < 0 ? hipGetErrorString(static_cast<hipError_t>(-status)) : "unknown";
+  }
+}
+
+int ifx_supports(int quant_type, int M, int N, int K) {
+  if (!is_weight_type(quant_type)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
+  if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
+  return 1;
+}
+
+int ifx_q8_1_quantize_f32(const float *x, void *q8_1, int M, int K, void *stream) {
+  if (!x || !q8_1) return IFX_NULL_POINTER;
+  if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_quantize_q8_1(x, false, q8_1, M, K,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+int ifx_q8_1_quantize_f16(const uint16_t *x, void *q8_1, int M, int K, void *stream) {
+  if (!x || !q8_1) return IFX_NULL_POINTER;
+  if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_quantize_q8_1(x, true, q8_1, M, K,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,
+              const void *bias, int M, int N, int K, void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  if (M <= kMaxGemvM)
+    return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+}
+
+int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
+                      int mode, const void *bias, int M, int N, int K, void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias,
+                                         out_dtype == IFX_OUT_F16, M, N, K, mode,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,
+                   void *stream) {
+  if (!W || !out) return IFX_NULL_POINTER;
+  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (out_dtype != IFX_OUT_F32 && out_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_dequantize(quant_type, W, out, out_dtype == IFX_OUT_F16,
+                                          n_rows * static_cast<int64_t>(K),
+                                          static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

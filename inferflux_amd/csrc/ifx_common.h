@@ -1,0 +1,75 @@
+// ifx_common.h -- GGUF block formats and wave64 helpers shared by the gfx950
+// kernels of the quantized GEMV/GEMM path.
+//
+// Block layouts follow the reference's structs
+// (runtime/backends/cuda/native/kernels/dequantization.cuh:17-49,117-138):
+//   Q4_K 144 B : u16 d | u16 dmin | u8 scales[12] | u8 qs[128]
+//   Q6_K 210 B : u8 ql[128] | u8 qh[64] | i8 scales[16] | u16 d   (d last)
+//   Q8_0  34 B : u16 d | i8 qs[32]
+//   Q8_1  36 B : u16 d | u16 s (= d * sum(qs)) | i8 qs[32]
+// The kernels address blocks as raw bytes (no packed structs), so rows whose
+// byte stride is not a multiple of 16 (Q6_K, Q8_0) are read with plain
+// loads at their natural offsets; gfx950 serves unaligned dword loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifx {
+
+constexpr int kTypeQ8_0 = 8;
+constexpr int kTypeQ8_1 = 9;
+constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ6_K = 14;
+
+constexpr int kQ4KBytes = 144;
+constexpr int kQ6KBytes = 210;
+constexpr int kQ8_0Bytes = 34;
+constexpr int kQ8_1Bytes = 36;
+
+constexpr int kWave = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  _Float16 h;
+  uint16_t b = static_cast<uint16_t>(bits16);
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32 default mode).
+__device__ __forceinline__ uint32_t f2h_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Forces x to be rounded to an fp32 register value.  Without it the
+// compiler may fuse "fp32 multiply, then convert to fp16" into a single
+// mixed-precision FMA (one rounding instead of two), which changes results
+// that must match an fp32-then-fp16 evaluation bit for bit.
+__device__ __forceinline__ float materialize_f32(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg(const void *p) {
+  T v;
+  __builtin_memcpy(&v, p, sizeof(T));
+  return v;
+}
+
+// Signed int8x4 dot product with int32 accumulate: v_dot4_i32_i8.
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace ifx

@@ -1,0 +1,110 @@
+"""Torch-facing wrappers over the C ABI (include/ifx_qgemm.h).
+
+PyTorch only provides device memory and the current HIP stream here; every
+computation is a HIP kernel in libifx_qgemm.so, called through ctypes.
+Errors follow the reference's contract (fused_quant_gemm.cu:2085-2117):
+a positive status means "not handled" and is raised as NotHandled so the
+caller can pick a fallback; a negative status is a HIP launch error.
+"""
+import torch
+
+from . import _lib
+
+Q8_0, Q8_1, Q4_K, Q6_K = 8, 9, 12, 14
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34, Q8_1: 36}
+BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32}
+TYPE_NAMES = {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0", Q8_1: "Q8_1"}
+
+STORE, ACCUM, BIAS = 0, 1, 2
+OUT_F32, OUT_F16 = 0, 1
+
+
+class NotHandled(RuntimeError):
+    """Positive status: the call launched nothing (reference: `false`)."""
+
+    def __init__(self, status, what):
+        super().__init__(f"{what}: {_lib.load().ifx_status_string(status).decode()} ({status})")
+        self.status = status
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _check(rc, what):
+    if rc == 0:
+        return
+    if rc > 0:
+        raise NotHandled(rc, what)
+    raise HipError(f"{what}: HIP error {-rc}: {_lib.load().ifx_status_string(rc).decode()}")
+
+
+def _stream(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _dev(t, name):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def weight_bytes(qtype, n_rows, K):
+    return n_rows * (K // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+
+
+def quantize_q8_1(x, out=None, stream=None):
+    """fp32 or fp16 x [M, K] (device) -> uint8 Q8_1 blocks [M, K/32*36]."""
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, K // 32 * 36), dtype=torch.uint8, device=x.device)
+    L = _lib.load()
+    if x.dtype == torch.float32:
+        rc = L.ifx_q8_1_quantize_f32(_dev(x, "x"), _dev(out, "out"), M, K, _stream(stream))
+    elif x.dtype == torch.float16:
+        rc = L.ifx_q8_1_quantize_f16(_dev(x, "x"), _dev(out, "out"), M, K, _stream(stream))
+    else:
+        raise TypeError("x must be float32 or float16")
+    _check(rc, "ifx_q8_1_quantize")
+    return out
+
+
+def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, bias=None,
+          stream=None, prefill=False):
+    """y [M, N] (op)= W . a with raw GGUF W and Q8_1 A (all device tensors)."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if out.dtype not in (torch.float16, torch.float32):
+        raise TypeError("out must be float32 or float16")
+    if qtype in BLOCK_BYTES and W.numel() < weight_bytes(qtype, N, K):
+        raise ValueError("W is smaller than N x K blocks")
+    if A.numel() < M * (K // 32) * 36:
+        raise ValueError("A is smaller than M x K/32 Q8_1 blocks")
+    if out.numel() < M * N:
+        raise ValueError("out is smaller than M x N")
+    bptr = _dev(bias, "bias") if bias is not None else None
+    fn = _lib.load().ifx_qgemm_prefill if prefill else _lib.load().ifx_qgemv
+    rc = fn(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"), od, mode, bptr, M, N, K,
+            _stream(stream))
+    _check(rc, "ifx_qgemm_prefill" if prefill else "ifx_qgemv")
+    return out
+
+
+def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None):
+    out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, n_rows, K):
+        raise ValueError("W is smaller than n_rows x K blocks")
+    rc = _lib.load().ifx_dequantize(qtype, _dev(W, "W"), _dev(out, "out"), od, n_rows, K,
+                                    _stream(stream))
+    _check(rc, "ifx_dequantize")
+    return out
+
+
+def supports(qtype, M, N, K):
+    return bool(_lib.load().ifx_supports(qtype, M, N, K))

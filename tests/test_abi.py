@@ -1,0 +1,105 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point
+include/ifx_qgemm.h declares, and its host-side validation answers without
+touching a GPU (the reference's `false` = a positive status)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ifx_qgemm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ifx_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from inferflux_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for s in ("ifx_q8_1_quantize_f32", "ifx_q8_1_quantize_f16", "ifx_qgemv",
+              "ifx_qgemm_prefill", "ifx_dequantize", "ifx_supports"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from inferflux_amd import _lib
+    syms = declared_symbols()
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (ifx_\w+)", out))
+    assert set(syms) <= exported
+
+
+def test_library_has_gfx950_code_object():
+    """The fat binary embedded in our own build names its offload target."""
+    from inferflux_amd import _lib
+    data = open(_lib.LIB_PATH, "rb").read()
+    assert b"gfx950" in data
+
+
+def test_block_geometry(lib):
+    assert (lib.ifx_block_bytes(12), lib.ifx_block_elems(12)) == (144, 256)
+    assert (lib.ifx_block_bytes(14), lib.ifx_block_elems(14)) == (210, 256)
+    assert (lib.ifx_block_bytes(8), lib.ifx_block_elems(8)) == (34, 32)
+    assert (lib.ifx_block_bytes(9), lib.ifx_block_elems(9)) == (36, 32)
+    assert lib.ifx_block_bytes(0) == 0 and lib.ifx_block_elems(13) == 0
+
+
+def test_supports(lib):
+    assert lib.ifx_supports(12, 1, 11008, 2048) == 1
+    assert lib.ifx_supports(12, 512, 27648, 5120) == 1
+    assert lib.ifx_supports(14, 32, 5120, 13824) == 1
+    assert lib.ifx_supports(8, 8, 151936, 2048) == 1
+    assert lib.ifx_supports(8, 1, 16, 96) == 1        # Q8_0 needs K % 32 only
+    assert lib.ifx_supports(12, 1, 16, 96) == 0       # K-quants need K % 256
+    assert lib.ifx_supports(13, 1, 16, 256) == 0      # Q5_K: no kernel
+    assert lib.ifx_supports(12, 0, 16, 256) == 0
+
+
+def test_validation_without_launch(lib):
+    """Rejected calls return before any HIP call, so they run on the CPU."""
+    fake = ctypes.c_void_p(0x1000)
+    # NULL pointers
+    assert lib.ifx_qgemv(12, None, fake, fake, 0, 0, None, 1, 16, 256, None) == 3
+    assert lib.ifx_qgemv(12, fake, None, fake, 0, 0, None, 1, 16, 256, None) == 3
+    assert lib.ifx_qgemv(12, fake, fake, fake, 0, 2, None, 1, 16, 256, None) == 3  # bias mode
+    assert lib.ifx_q8_1_quantize_f32(None, fake, 1, 32, None) == 3
+    # unsupported type / geometry / mode / dtype
+    assert lib.ifx_qgemv(13, fake, fake, fake, 0, 0, None, 1, 16, 256, None) == 1
+    assert lib.ifx_qgemv(12, fake, fake, fake, 0, 0, None, 1, 16, 250, None) == 2
+    assert lib.ifx_qgemv(12, fake, fake, fake, 0, 0, None, 0, 16, 256, None) == 2
+    assert lib.ifx_qgemv(12, fake, fake, fake, 0, 7, None, 1, 16, 256, None) == 2
+    assert lib.ifx_qgemv(12, fake, fake, fake, 5, 0, None, 1, 16, 256, None) == 2
+    assert lib.ifx_qgemm_prefill(6, fake, fake, fake, 0, 0, None, 64, 16, 256, None) == 1
+    assert lib.ifx_q8_1_quantize_f32(fake, fake, 1, 33, None) == 2
+    assert lib.ifx_dequantize(12, fake, fake, 0, 4, 100, None) == 2
+    assert lib.ifx_status_string(3) == b"null pointer"
+
+
+def test_product_fails_loudly_without_library(monkeypatch):
+    from inferflux_amd import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libifx_qgemm.so")
+    with pytest.raises(_lib.IfxError):
+        _lib.load()
+
+
+def test_product_never_imports_oracle():
+    pkg = os.path.join(ROOT, "inferflux_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in re.sub(r"(#|//).*", "", text), f
