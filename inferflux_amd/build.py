@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libifx_qgemm.so")
+PROBE_LIB = os.path.join(HERE, "libifx_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = [
@@ -21,7 +22,7 @@ COMMON = [
 ]
 # Bit-exact kernels: no fp contraction anywhere in these translation units.
 EXACT = {"quantize.hip", "dequant.hip"}
-SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "gemm_mfma.hip"]
+SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "gemm_mfma.hip"]
 
 
 def _run(cmd):
@@ -55,6 +56,10 @@ def build(verbose=True):
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
     os.replace(tmp, LIB)
+    # bandwidth probes used only by the benchmark harness
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC] + COMMON + ["-shared", "-o", tmp, os.path.join(CSRC, "probe.hip")])
+    os.replace(tmp, PROBE_LIB)
     if verbose:
         print("built", LIB)
     return LIB

@@ -17,13 +17,21 @@ hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int6
                              hipStream_t stream);
 hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const void *bias,
                        bool f16, int M, int N, int K, int mode, hipStream_t stream);
+hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, const void *bias,
+                             bool f16, int M, int N, int K, int mode, hipStream_t stream);
 hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
                             bool f16, int M, int N, int K, int mode, hipStream_t stream);
 }  // namespace ifx
 
 namespace {
 
-constexpr int kMaxGemvM = 8;  // M <= 8: weight-streaming GEMV; larger: MFMA GEMM
+// Batch-size dispatch (the reference's MMVQ / MMQ / cuBLAS split,
+// fused_quant_gemm.cu:1697-1747, re-derived for gfx950):
+//   M <= 2       v_dot4 GEMV        (gemv.hip)
+//   3 <= M <= 32 skinny int8 MFMA   (mmq_skinny.hip), K % 256 == 0
+//   M > 32       tiled int8 MFMA    (gemm_mfma.hip)
+constexpr int kMaxGemvM = 2;
+constexpr int kMaxSkinnyM = 32;
 
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
 
@@ -40,8 +48,12 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   if (mode == IFX_BIAS && !bias) return IFX_NULL_POINTER;
   if (M <= 0 || N <= 0 || K <= 0) return IFX_BAD_GEOMETRY;
   if (K % ifx_block_elems(quant_type) != 0) return IFX_BAD_GEOMETRY;
-  // Row offsets are formed in 64-bit; the 32-bit grid limits N and M.
+  // Kernels address W and A with 32-bit byte offsets (buffer loads).
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
+  const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
+                           ifx_block_bytes(quant_type);
+  const uint64_t a_bytes = static_cast<uint64_t>(M) * (K / 32) * 36;
+  if (w_bytes >= (1ull << 32) || a_bytes >= (1ull << 32)) return IFX_BAD_GEOMETRY;
   return IFX_OK;
 }
 
@@ -82,6 +94,9 @@ int ifx_supports(int quant_type, int M, int N, int K) {
   if (!is_weight_type(quant_type)) return 0;
   if (M <= 0 || N <= 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
+  const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
+                           ifx_block_bytes(quant_type);
+  if (w_bytes >= (1ull << 32) || static_cast<uint64_t>(M) * (K / 32) * 36 >= (1ull << 32)) return 0;
   return 1;
 }
 
@@ -105,8 +120,10 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (M <= kMaxGemvM)
+  if (M <= kMaxGemvM || K % 256 != 0)
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  if (M <= kMaxSkinnyM)
+    return status_of(ifx::launch_mmq_skinny(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
 }
 

@@ -67,6 +67,29 @@ __device__ __forceinline__ T ldg(const void *p) {
   return v;
 }
 
+// Buffer resources: a 32-bit byte range over a tensor.  Loads take a
+// per-lane offset and a wave-uniform offset (scalar register), so address
+// arithmetic stays 32-bit, and reads past the range return zeros.  Word 3 is
+// the gfx9-family default (raw buffer, 32-bit dword format).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+template <typename T>
+__device__ __forceinline__ T bload(rsrc_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 16)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  else if constexpr (sizeof(T) == 8)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  else if constexpr (sizeof(T) == 4)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  else
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+}
+
 // Signed int8x4 dot product with int32 accumulate: v_dot4_i32_i8.
 __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
