@@ -14,19 +14,25 @@
 // and columns = weight rows n (B = unpacked weight codes).  Lane l supplies
 // A row l % 16 and B column l % 16 for the 8-value K chunk l / 16, and
 // receives column n = l % 16 and rows 4*(l/16) + i, i < 4, of the result.
-//  * A workgroup owns 16*NT weight rows and all (<= 32) batch rows; its KW
-//    waves split the super-blocks (256 values of K) round-robin, so small-N
-//    projections still fill the chip, and add their partial sums in LDS in
-//    a fixed order (deterministic results).
-//  * Per super-block each wave copies its W rows and A rows into its own
-//    LDS region with 16-byte loads whose lanes cover contiguous memory (the
-//    raw bytes: 144 B Q4_K, 210 B Q6_K, 8 x 34 B Q8_0 per row; 8 x 36 B
-//    Q8_1), then reads the MFMA operands from LDS.
+//  * A workgroup is 4 waves; each wave owns one n-tile of 16 weight rows and
+//    all MT m-tiles of 16 batch rows.  The workgroup walks a range of
+//    super-blocks (256 values of K).  Per super-block the four waves stage
+//    the batch rows' Q8_1 blocks once in LDS (shared) and each wave stages
+//    its own 16 weight rows (raw bytes: 144 B Q4_K, 210 B Q6_K, 8 x 34 B
+//    Q8_0) -- 16-byte buffer loads whose lanes cover contiguous memory --
+//    then reads the MFMA operands from LDS.  The next super-block's loads
+//    are issued before the current one is computed.
+//  * Small N cannot fill 256 CUs with 16-row tiles, so the super-blocks are
+//    split across gridDim.y workgroups whose fp32 partial sums are added to
+//    Y with atomics (Y is zeroed first for the store/bias modes).  Then the
+//    summation order, hence the last bits of y, can vary between runs, as
+//    in the reference's atomic fp32 accumulate kernels (mmvq.cuh:280-401).
+//    fp16 outputs never split.
 //  * Scaling: Q4_K and Q6_K sub-block scales are integers, so each block's
-//    int32 result is multiplied by its scale in the integer pipe and the
-//    fp32 sum is taken in units of the super-block d (one multiply by d per
-//    super-block).  The Q4_K min term sum_b (dmin*m_b) * s_b is a small
-//    fp32 GEMM done on the matrix cores (v_mfma_f32_16x16x4f32).
+//    int32 result is multiplied by its scale in the integer pipe (24-bit
+//    multiply) and the fp32 sum is taken in units of the super-block d (one
+//    multiply by d per super-block).  The Q4_K min term sum_b (dmin*m_b)*s_b
+//    is a small fp32 GEMM done on the matrix cores (v_mfma_f32_16x16x4f32).
 #include "ifx_common.h"
 
 #include <stdlib.h>
@@ -34,6 +40,8 @@
 namespace ifx {
 
 namespace {
+
+constexpr int kWaves = 4;
 
 __device__ __forceinline__ i32x4 mfma16x16x32(int64_t a, int64_t b) {
   const i32x4 z = {0, 0, 0, 0};
@@ -55,78 +63,70 @@ template <int QT>
 struct WFmt;
 template <>
 struct WFmt<kTypeQ4_K> {  // one super-block of a row: 144 raw bytes
-  static constexpr int kBytes = 144, kPitch = 144, kChunks = 9;
+  static constexpr int kSbBytes = 144, kPitch = 144, kChunks = 9;
 };
 template <>
 struct WFmt<kTypeQ6_K> {  // 210 raw bytes; the 14th chunk carries only d
-  static constexpr int kBytes = 210, kPitch = 224, kChunks = 14;
+  static constexpr int kSbBytes = 210, kPitch = 224, kChunks = 14;
 };
 template <>
 struct WFmt<kTypeQ8_0> {  // 8 blocks x 34 bytes
-  static constexpr int kBytes = 272, kPitch = 272, kChunks = 17;
+  static constexpr int kSbBytes = 272, kPitch = 272, kChunks = 17;
 };
 
-constexpr int kApitch = 288;  // 8 Q8_1 blocks x 36 bytes
+constexpr int kApitch = 288;  // 8 Q8_1 blocks x 36 bytes per batch row
 constexpr int kAChunks = 18;
 
-template <int QT, int MT, int NT>
+template <int QT, int MT>
 struct Stage {
-  static constexpr int kWBytes = 16 * NT * WFmt<QT>::kPitch;
-  static constexpr int kABytes = 16 * MT * kApitch;
-  static constexpr int kBytes = kWBytes + kABytes;
-  static constexpr int kWChunks = 16 * NT * WFmt<QT>::kChunks;
-  static constexpr int kAChunksAll = 16 * MT * kAChunks;
+  static constexpr int kABytes = 16 * MT * kApitch;              // shared
+  static constexpr int kWBytes = 16 * WFmt<QT>::kPitch;          // per wave
+  static constexpr int kBytes = kABytes + kWaves * kWBytes;
+  static constexpr int kWChunks = 16 * WFmt<QT>::kChunks;        // per wave
+  static constexpr int kAChunksAll = 16 * MT * kAChunks;         // per workgroup
   static constexpr int kWPerLane = (kWChunks + 63) / 64;
-  static constexpr int kAPerLane = (kAChunksAll + 63) / 64;
+  static constexpr int kAPerThread = (kAChunksAll + 64 * kWaves - 1) / (64 * kWaves);
 };
 
-// This lane's 16-byte chunks of one super-block's W rows and A rows.
-template <int QT, int MT, int NT>
+// One super-block's chunks held by this lane, and their loop-invariant
+// byte offsets (super-block sb adds sb * bytes-per-super-block).
+template <int QT, int MT>
 struct StageRegs {
-  u32x4 w[Stage<QT, MT, NT>::kWPerLane];
-  u32x4 a[Stage<QT, MT, NT>::kAPerLane];
+  u32x4 w[Stage<QT, MT>::kWPerLane];
+  u32x4 a[Stage<QT, MT>::kAPerThread];
 };
-
-// Per-lane byte offsets of this lane's 16-byte chunks within super-block 0
-// (loop invariant; super-block sb adds sb * bytes-per-super-block).  Rows
-// past N repeat row N-1; chunks of rows past M get offset -1 (zero fill).
-template <int QT, int MT, int NT>
+template <int QT, int MT>
 struct StageOffsets {
-  uint32_t w[Stage<QT, MT, NT>::kWPerLane];
-  int32_t a[Stage<QT, MT, NT>::kAPerLane];
+  uint32_t w[Stage<QT, MT>::kWPerLane];
+  int32_t a[Stage<QT, MT>::kAPerThread];  // -1: batch row past M (zero)
 };
 
-template <int QT, int MT, int NT>
-__device__ __forceinline__ void stage_offsets(StageOffsets<QT, MT, NT> &so, int n0, int N, int M,
-                                              int nsb, int nblk, int lane) {
-  using S = Stage<QT, MT, NT>;
+template <int QT, int MT>
+__device__ __forceinline__ void stage_offsets(StageOffsets<QT, MT> &so, int n0, int N, int M,
+                                              uint32_t w_row, uint32_t a_row, int lane, int tid) {
+  using S = Stage<QT, MT>;
   using F = WFmt<QT>;
-  const uint32_t wrow = (QT == kTypeQ8_0) ? static_cast<uint32_t>(nblk) * kQ8_0Bytes
-                                          : static_cast<uint32_t>(nsb) * F::kBytes;
 #pragma unroll
   for (int i = 0; i < S::kWPerLane; ++i) {
     const int c = min(lane + 64 * i, S::kWChunks - 1);
     const int r = c / F::kChunks, part = c - r * F::kChunks;
-    so.w[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * wrow + part * 16;
+    so.w[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * w_row + part * 16;
   }
 #pragma unroll
-  for (int i = 0; i < S::kAPerLane; ++i) {
-    const int c = min(lane + 64 * i, S::kAChunksAll - 1);
+  for (int i = 0; i < S::kAPerThread; ++i) {
+    const int c = min(tid + 64 * kWaves * i, S::kAChunksAll - 1);
     const int r = c / kAChunks, part = c - r * kAChunks;
-    so.a[i] = (r < M) ? r * nblk * kQ8_1Bytes + part * 16 : -1;
+    so.a[i] = (r < M) ? static_cast<int32_t>(r * a_row + part * 16) : -1;
   }
 }
 
-// Global -> registers: this lane's chunks of super-block sb, as buffer
-// loads (per-lane 32-bit offset + wave-uniform super-block offset).
-template <int QT, int MT, int NT>
-__device__ __forceinline__ void load_stage(StageRegs<QT, MT, NT> &rg,
-                                           const StageOffsets<QT, MT, NT> &so, rsrc_t Wr,
-                                           rsrc_t Ar, int sb, int lane) {
-  using S = Stage<QT, MT, NT>;
+template <int QT, int MT>
+__device__ __forceinline__ void load_stage(StageRegs<QT, MT> &rg, const StageOffsets<QT, MT> &so,
+                                           rsrc_t Wr, rsrc_t Ar, int sb, int lane, int tid) {
+  using S = Stage<QT, MT>;
   using F = WFmt<QT>;
-  const uint32_t wsb = sb * (QT == kTypeQ8_0 ? 8 * kQ8_0Bytes : F::kBytes);
-  const uint32_t asb = sb * (8 * kQ8_1Bytes);
+  const uint32_t wsb = sb * F::kSbBytes;
+  const uint32_t asb = sb * kApitch;
 #pragma unroll
   for (int i = 0; i < S::kWPerLane; ++i) {
     const int c = lane + 64 * i;
@@ -137,125 +137,124 @@ __device__ __forceinline__ void load_stage(StageRegs<QT, MT, NT> &rg,
     }
   }
 #pragma unroll
-  for (int i = 0; i < S::kAPerLane; ++i) {
-    const int c = lane + 64 * i;
+  for (int i = 0; i < S::kAPerThread; ++i) {
+    const int c = tid + 64 * kWaves * i;
     rg.a[i] = u32x4{0, 0, 0, 0};
-    if ((S::kAChunksAll % 64 == 0 || i + 1 < S::kAPerLane || c < S::kAChunksAll) && so.a[i] >= 0)
+    if ((S::kAChunksAll % (64 * kWaves) == 0 || i + 1 < S::kAPerThread || c < S::kAChunksAll) &&
+        so.a[i] >= 0)
       rg.a[i] = bload<u32x4>(Ar, static_cast<uint32_t>(so.a[i]), asb);
   }
 }
 
-template <int QT, int MT, int NT>
-__device__ __forceinline__ void store_stage(uint8_t *st, const StageRegs<QT, MT, NT> &rg,
-                                            int lane) {
-  using S = Stage<QT, MT, NT>;
+template <int QT, int MT>
+__device__ __forceinline__ void store_stage(uint8_t *as, uint8_t *ws, const StageRegs<QT, MT> &rg,
+                                            int lane, int tid) {
+  using S = Stage<QT, MT>;
   using F = WFmt<QT>;
 #pragma unroll
   for (int i = 0; i < S::kWPerLane; ++i) {
     const int c = lane + 64 * i;
-    if (c < S::kWChunks) {
+    if (S::kWChunks % 64 == 0 || i + 1 < S::kWPerLane || c < S::kWChunks) {
       const int r = c / F::kChunks, part = c - r * F::kChunks;
-      *reinterpret_cast<u32x4 *>(st + r * F::kPitch + part * 16) = rg.w[i];
+      *reinterpret_cast<u32x4 *>(ws + r * F::kPitch + part * 16) = rg.w[i];
     }
   }
-  uint8_t *as = st + S::kWBytes;
 #pragma unroll
-  for (int i = 0; i < S::kAPerLane; ++i) {
-    const int c = lane + 64 * i;
-    if (c < S::kAChunksAll) *reinterpret_cast<u32x4 *>(as + c * 16) = rg.a[i];
+  for (int i = 0; i < S::kAPerThread; ++i) {
+    const int c = tid + 64 * kWaves * i;
+    if (S::kAChunksAll % (64 * kWaves) == 0 || i + 1 < S::kAPerThread || c < S::kAChunksAll)
+      *reinterpret_cast<u32x4 *>(as + c * 16) = rg.a[i];
   }
 }
 
 }  // namespace
 
-template <int QT, int MT, int NT, int KW, bool F16OUT>
-__global__ __launch_bounds__(64 * KW, 4) void k_mmq_skinny(const uint8_t *__restrict__ W,
-                                                        const uint8_t *__restrict__ A,
-                                                        void *__restrict__ Y,
-                                                        const void *__restrict__ bias, int M,
-                                                        int N, int K, int mode) {
-  using S = Stage<QT, MT, NT>;
+__global__ __launch_bounds__(256) void k_fill_zero(float *__restrict__ y, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) y[i] = 0.0f;
+}
+
+// grid: x = ceil(N / 64) row groups, y = super-block splits (sb_per ranges)
+template <int QT, int MT, bool F16OUT, bool ATOMIC>
+__global__ __launch_bounds__(64 * kWaves, 2) void k_mmq_skinny(const uint8_t *__restrict__ W,
+                                                               const uint8_t *__restrict__ A,
+                                                               void *__restrict__ Y,
+                                                               const void *__restrict__ bias,
+                                                               int M, int N, int K, int mode,
+                                                               int sb_per) {
+  using S = Stage<QT, MT>;
   using F = WFmt<QT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int lane = threadIdx.x & 63;
-  // wave-uniform values kept in scalar registers
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int l16 = lane & 15, kq = lane >> 4;
-  const int n0 = blockIdx.x * 16 * NT;
-  const int m0 = 0;
+  const int n0 = (blockIdx.x * kWaves + wave) * 16;
   const int nblk = K >> 5;  // Q8_1 blocks per activation row
   const int nsb = K >> 8;   // super-blocks of 256 values
-  uint8_t *st = smem + wave * S::kBytes;       // this wave's W rows
-  const uint8_t *as = st + S::kWBytes;         // this wave's A rows
+  const int sb0 = blockIdx.y * sb_per;
+  const int sb1 = min(nsb, sb0 + sb_per);
+  uint8_t *as = smem;                                  // shared batch rows
+  uint8_t *ws = smem + S::kABytes + wave * S::kWBytes; // this wave's weight rows
 
-  f32x4 acc[MT][NT];   // result, rows 4*kq + i, column l16
-  f32x4 accm[MT][NT];  // Q4_K: sum of (dmin*m) * s, subtracted at the end
-#pragma unroll
-  for (int a = 0; a < MT; ++a)
-#pragma unroll
-    for (int b = 0; b < NT; ++b) acc[a][b] = accm[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t w_row = static_cast<uint32_t>(QT == kTypeQ8_0 ? nblk * kQ8_0Bytes : nsb * F::kSbBytes);
+  const uint32_t a_row = static_cast<uint32_t>(nblk) * kQ8_1Bytes;
+  const rsrc_t Wr = make_rsrc(W, w_row * static_cast<uint32_t>(N));
+  const rsrc_t Ar = make_rsrc(A, a_row * static_cast<uint32_t>(M));
+  StageOffsets<QT, MT> so;
+  stage_offsets<QT, MT>(so, n0, N, M, w_row, a_row, lane, tid);
 
-  StageOffsets<QT, MT, NT> so;
-  stage_offsets<QT, MT, NT>(so, n0, N, M, nsb, nblk, lane);
-  const uint32_t w_bytes = static_cast<uint32_t>(N) *
-      (QT == kTypeQ8_0 ? static_cast<uint32_t>(nblk) * kQ8_0Bytes : static_cast<uint32_t>(nsb) * F::kBytes);
-  const rsrc_t Wr = make_rsrc(W, w_bytes);
-  const rsrc_t Ar = make_rsrc(A, static_cast<uint32_t>(M) * nblk * kQ8_1Bytes);
-  // every wave runs the same number of iterations (the barriers need it);
-  // the other waves on the CU cover each wave's load latency
-  const int iters = (nsb + KW - 1) / KW;
-  for (int it = 0; it < iters; ++it) {
-    const int sb = it * KW + wave;
-    {
-      StageRegs<QT, MT, NT> rg;
-      if (sb < nsb) load_stage<QT, MT, NT>(rg, so, Wr, Ar, sb, lane);
-      __syncthreads();  // previous iteration's LDS reads are done
-      if (sb < nsb) store_stage<QT, MT, NT>(st, rg, lane);
-      __syncthreads();
-    }
-    if (sb >= nsb) continue;
+  f32x4 acc[MT];   // result, rows 4*kq + i, column l16
+  f32x4 accm[MT];  // Q4_K: sum of (dmin*m) * s, subtracted at the end
+#pragma unroll
+  for (int a = 0; a < MT; ++a) acc[a] = accm[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // weight scales of this lane's column (row l16 of each n-tile)
-    float dsup[NT];
-    uint32_t scw[NT][4];
+  StageRegs<QT, MT> rg;  // the next super-block's chunks, loaded a step ahead
+  if (sb0 < sb1) load_stage<QT, MT>(rg, so, Wr, Ar, sb0, lane, tid);
+  for (int sb = sb0; sb < sb1; ++sb) {
+    __syncthreads();  // previous super-block's LDS reads are done
+    store_stage<QT, MT>(as, ws, rg, lane, tid);
+    __syncthreads();
+    if (sb + 1 < sb1) load_stage<QT, MT>(rg, so, Wr, Ar, sb + 1, lane, tid);  // in flight below
+
+    // weight scales of this lane's column (row l16 of the n-tile)
+    const uint8_t *row = ws + l16 * F::kPitch;
+    float dsup = 0.0f;
+    uint32_t scw[4] = {0, 0, 0, 0};
+    if constexpr (QT == kTypeQ4_K) {
+      const u32x4 hdr = *reinterpret_cast<const u32x4 *>(row);
+      dsup = h2f(hdr.x & 0xFFFFu);
+      scw[0] = hdr.y & 0x3F3F3F3Fu;                                          // sc 0-3
+      scw[1] = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);         // sc 4-7
+      scw[2] = hdr.z & 0x3F3F3F3Fu;                                          // m 0-3
+      scw[3] = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);  // m 4-7
+      // min term: sum over the 8 blocks of (dmin*m)[n] * s[m], as two fp32
+      // MFMA 16x16x4 steps (K = blocks 4j..4j+3; this lane supplies k = kq)
+      const float dmin = h2f(hdr.x >> 16);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const uint8_t *row = st + (16 * t + l16) * F::kPitch;
-      if constexpr (QT == kTypeQ4_K) {
-        const u32x4 hdr = *reinterpret_cast<const u32x4 *>(row);
-        dsup[t] = h2f(hdr.x & 0xFFFFu);
-        scw[t][0] = hdr.y & 0x3F3F3F3Fu;                                            // sc 0-3
-        scw[t][1] = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);           // sc 4-7
-        scw[t][2] = hdr.z & 0x3F3F3F3Fu;                                            // m 0-3
-        scw[t][3] = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);    // m 4-7
-        // min term: sum over the 8 blocks of (dmin*m)[n] * s[m], as two fp32
-        // MFMA 16x16x4 steps (K = blocks 4j..4j+3; this lane supplies k = kq)
-        const float dmin = h2f(hdr.x >> 16);
+      for (int j = 0; j < 2; ++j) {
+        const float fm = dmin * static_cast<float>((scw[2 + j] >> (8 * kq)) & 0xFFu);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float fm = dmin * static_cast<float>((scw[t][2 + j] >> (8 * kq)) & 0xFFu);
-#pragma unroll
-          for (int s = 0; s < MT; ++s) {
-            const uint32_t ds = *reinterpret_cast<const uint32_t *>(
-                as + (16 * s + l16) * kApitch + (4 * j + kq) * kQ8_1Bytes);
-            accm[s][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(h2f(ds >> 16), fm, accm[s][t], 0, 0, 0);
-          }
+        for (int s = 0; s < MT; ++s) {
+          const uint32_t ds = *reinterpret_cast<const uint32_t *>(
+              as + (16 * s + l16) * kApitch + (4 * j + kq) * kQ8_1Bytes);
+          accm[s] = __builtin_amdgcn_mfma_f32_16x16x4f32(h2f(ds >> 16), fm, accm[s], 0, 0, 0);
         }
-      } else if constexpr (QT == kTypeQ6_K) {
-        dsup[t] = h2f(*reinterpret_cast<const uint16_t *>(row + 208));
-        const u32x4 sc = *reinterpret_cast<const u32x4 *>(row + 192);
-        scw[t][0] = sc.x; scw[t][1] = sc.y; scw[t][2] = sc.z; scw[t][3] = sc.w;
       }
+    } else if constexpr (QT == kTypeQ6_K) {
+      dsup = h2f(*reinterpret_cast<const uint16_t *>(row + 208));
+      const u32x4 sc = *reinterpret_cast<const u32x4 *>(row + 192);
+      scw[0] = sc.x; scw[1] = sc.y; scw[2] = sc.z; scw[3] = sc.w;
     }
+    // 64-bit views of the scale bytes: byte selects become shifts, not
+    // indexed loads (keeps them in registers)
+    const uint64_t sc8lo = static_cast<uint64_t>(scw[0]) | (static_cast<uint64_t>(scw[1]) << 32);
+    const uint64_t sc8hi = static_cast<uint64_t>(scw[2]) | (static_cast<uint64_t>(scw[3]) << 32);
 
-    f32x4 P[MT][NT];  // super-block partial in units of the super-block d
+    f32x4 P[MT];  // super-block partial in units of the super-block d
 #pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int b = 0; b < NT; ++b) P[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < MT; ++a) P[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // two blocks per step: enough independent MFMAs to hide their latency
-    // without hoisting all eight blocks' operands into registers
 #pragma unroll 2
     for (int b = 0; b < 8; ++b) {
       int64_t av[MT];
@@ -268,177 +267,129 @@ __global__ __launch_bounds__(64 * KW, 4) void k_mmq_skinny(const uint8_t *__rest
           fa[s][i] = h2f(*reinterpret_cast<const uint16_t *>(
               as + (16 * s + 4 * kq + i) * kApitch + b * kQ8_1Bytes));
       }
+      if constexpr (QT == kTypeQ4_K) {
+        const u32x2 q = *reinterpret_cast<const u32x2 *>(row + 16 + 32 * (b >> 1) + 8 * kq);
+        const int sh = (b & 1) * 4;
+        const int64_t bw = pack64((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
+        const int sc = static_cast<int>((sc8lo >> (8 * b)) & 0xFFu);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const uint8_t *row = st + (16 * t + l16) * F::kPitch;
-        if constexpr (QT == kTypeQ4_K) {
-          const u32x2 q = *reinterpret_cast<const u32x2 *>(row + 16 + 32 * (b >> 1) + 8 * kq);
-          const int sh = (b & 1) * 4;
-          const int64_t bw = pack64((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
-          const int sc = static_cast<int>((scw[t][b >> 2] >> (8 * (b & 3))) & 0xFFu);
+        for (int s = 0; s < MT; ++s) {
+          const i32x4 c = mfma16x16x32(av[s], bw);
 #pragma unroll
-          for (int s = 0; s < MT; ++s) {
-            const i32x4 c = mfma16x16x32(av[s], bw);
+          for (int i = 0; i < 4; ++i) P[s][i] += static_cast<float>(__mul24(c[i], sc)) * fa[s][i];
+        }
+      } else if constexpr (QT == kTypeQ6_K) {
+        const int g = b >> 2, sub = b & 3;
+        const u32x2 ql = *reinterpret_cast<const u32x2 *>(row + 64 * g + 32 * (sub & 1) + 8 * kq);
+        const u32x2 qh = *reinterpret_cast<const u32x2 *>(row + 128 + 32 * g + 8 * kq);
+        const int lsh = (sub >= 2) ? 4 : 0, hsh = 2 * sub;
+        const uint32_t v0 = q6_minus32(((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qh.x >> hsh) & 0x03030303u) << 4));
+        const uint32_t v1 = q6_minus32(((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qh.y >> hsh) & 0x03030303u) << 4));
+        // values 0-15 come from lanes kq 0, 1; 16-31 from kq 2, 3: two MFMAs
+        // so each half gets its own int8 scale (scales[g*8 + 2*sub + 0/1])
+        const bool first = kq < 2;
+        const int64_t bw0 = first ? pack64(v0, v1) : 0, bw1 = first ? 0 : pack64(v0, v1);
+        const uint32_t two = static_cast<uint32_t>((g == 0 ? sc8lo : sc8hi) >> (16 * sub));
+        const int sc0 = static_cast<int8_t>(two & 0xFFu);
+        const int sc1 = static_cast<int8_t>((two >> 8) & 0xFFu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) P[s][t][i] += static_cast<float>(c[i] * sc) * fa[s][i];
-          }
-        } else if constexpr (QT == kTypeQ6_K) {
-          const int g = b >> 2, sub = b & 3;
-          const u32x2 ql = *reinterpret_cast<const u32x2 *>(row + 64 * g + 32 * (sub & 1) + 8 * kq);
-          const u32x2 qh = *reinterpret_cast<const u32x2 *>(row + 128 + 32 * g + 8 * kq);
-          const int lsh = (sub >= 2) ? 4 : 0, hsh = 2 * sub;
-          const uint32_t v0 = q6_minus32(((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qh.x >> hsh) & 0x03030303u) << 4));
-          const uint32_t v1 = q6_minus32(((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qh.y >> hsh) & 0x03030303u) << 4));
-          // values 0-15 come from lanes kq 0, 1; 16-31 from kq 2, 3: two
-          // MFMAs so each half gets its own int8 scale
-          const bool first = kq < 2;
-          const int64_t bw0 = first ? pack64(v0, v1) : 0, bw1 = first ? 0 : pack64(v0, v1);
-          const int si = g * 8 + 2 * sub;  // even: both halves' scales in one dword
-          const uint32_t hw = scw[t][si >> 2];
-          const int sc0 = static_cast<int8_t>((hw >> (8 * (si & 3))) & 0xFFu);
-          const int sc1 = static_cast<int8_t>((hw >> (8 * ((si & 3) + 1))) & 0xFFu);
+        for (int s = 0; s < MT; ++s) {
+          const i32x4 c0 = mfma16x16x32(av[s], bw0);
+          const i32x4 c1 = mfma16x16x32(av[s], bw1);
 #pragma unroll
-          for (int s = 0; s < MT; ++s) {
-            const i32x4 c0 = mfma16x16x32(av[s], bw0);
-            const i32x4 c1 = mfma16x16x32(av[s], bw1);
+          for (int i = 0; i < 4; ++i)
+            P[s][i] += static_cast<float>(__mul24(c0[i], sc0) + __mul24(c1[i], sc1)) * fa[s][i];
+        }
+      } else {
+        const uint8_t *blk = row + 34 * b;
+        const float dw = h2f(ldg<uint16_t>(blk));
+        const int64_t bw = ldg<int64_t>(blk + 2 + 8 * kq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              P[s][t][i] += static_cast<float>(c0[i] * sc0 + c1[i] * sc1) * fa[s][i];
-          }
-        } else {
-          const uint8_t *blk = row + 34 * b;
-          const float dw = h2f(ldg<uint16_t>(blk));
-          const int64_t bw = ldg<int64_t>(blk + 2 + 8 * kq);
+        for (int s = 0; s < MT; ++s) {
+          const i32x4 c = mfma16x16x32(av[s], bw);
 #pragma unroll
-          for (int s = 0; s < MT; ++s) {
-            const i32x4 c = mfma16x16x32(av[s], bw);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) P[s][t][i] += static_cast<float>(c[i]) * (dw * fa[s][i]);
-          }
+          for (int i = 0; i < 4; ++i) P[s][i] += static_cast<float>(c[i]) * (dw * fa[s][i]);
         }
       }
     }
 #pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        if constexpr (QT == kTypeQ8_0) acc[a][t] += P[a][t];
-        else acc[a][t] += dsup[t] * P[a][t];
-      }
+    for (int a = 0; a < MT; ++a) {
+      if constexpr (QT == kTypeQ8_0) acc[a] += P[a];
+      else acc[a] += dsup * P[a];
+    }
   }
+#pragma unroll
+  for (int a = 0; a < MT; ++a) acc[a] -= accm[a];
+
+  // ---- epilogue: lane holds column n and rows 4*kq + i of each m-tile
+  const int n = n0 + l16;
+  if (n >= N) return;
 #pragma unroll
   for (int a = 0; a < MT; ++a)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[a][t] -= accm[a][t];
-
-  // ---- combine the KW waves' partial sums in a fixed order (LDS reused)
-  if constexpr (KW > 1) {
-    constexpr int NACC = MT * NT * 4;
-    float *red = reinterpret_cast<float *>(smem);
-    __syncthreads();
-    if (wave > 0) {
-      float *dst = red + ((wave - 1) * NACC) * 64 + lane;
-#pragma unroll
-      for (int a = 0; a < MT; ++a)
-#pragma unroll
-        for (int b = 0; b < NT; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) dst[((a * NT + b) * 4 + i) * 64] = acc[a][b][i];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-#pragma unroll
-    for (int w = 0; w < KW - 1; ++w) {
-      const float *src = red + (w * NACC) * 64 + lane;
-#pragma unroll
-      for (int a = 0; a < MT; ++a)
-#pragma unroll
-        for (int b = 0; b < NT; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[a][b][i] += src[((a * NT + b) * 4 + i) * 64];
-    }
-  }
-
-  // ---- epilogue: lane holds column n and rows 4*kq + i of each tile
-#pragma unroll
-  for (int b = 0; b < NT; ++b) {
-    const int n = n0 + 16 * b + l16;
-    if (n >= N) continue;
-#pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 16 * a + 4 * kq + i;
-        if (m >= M) continue;
-        const int64_t o = static_cast<int64_t>(m) * N + n;
-        float y = acc[a][b][i];
-        if constexpr (F16OUT) {
-          uint16_t *Yh = static_cast<uint16_t *>(Y);
-          if (mode == 1) y += h2f(Yh[o]);
-          else if (mode == 2) y += h2f(static_cast<const uint16_t *>(bias)[n]);
-          Yh[o] = static_cast<uint16_t>(f2h_bits(y));
-        } else {
-          float *Yf = static_cast<float *>(Y);
-          if (mode == 1) y += Yf[o];
-          else if (mode == 2) y += static_cast<const float *>(bias)[n];
-          Yf[o] = y;
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * a + 4 * kq + i;
+      if (m >= M) continue;
+      const int64_t o = static_cast<int64_t>(m) * N + n;
+      float y = acc[a][i];
+      if constexpr (ATOMIC) {
+        // Y was zeroed (store/bias) or holds the accumulate base
+        if (mode == 2 && blockIdx.y == 0) y += static_cast<const float *>(bias)[n];
+        atomicAdd(static_cast<float *>(Y) + o, y);
+      } else if constexpr (F16OUT) {
+        uint16_t *Yh = static_cast<uint16_t *>(Y);
+        if (mode == 1) y += h2f(Yh[o]);
+        else if (mode == 2) y += h2f(static_cast<const uint16_t *>(bias)[n]);
+        Yh[o] = static_cast<uint16_t>(f2h_bits(y));
+      } else {
+        float *Yf = static_cast<float *>(Y);
+        if (mode == 1) y += Yf[o];
+        else if (mode == 2) y += static_cast<const float *>(bias)[n];
+        Yf[o] = y;
       }
-  }
+    }
 }
 
 namespace {
 
-constexpr int kMaxLds = 160 * 1024;
-
-template <int QT, int MT, int NT, int KW>
-hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16, int M,
-                    int N, int K, int mode, hipStream_t s) {
-  using St = Stage<QT, MT, NT>;
-  constexpr int stage = KW * St::kBytes;
-  constexpr int red = (KW > 1) ? (KW - 1) * MT * NT * 4 * 64 * 4 : 0;
-  constexpr int shm = stage > red ? stage : red;
-  static_assert(shm <= kMaxLds, "LDS budget");
-  auto kern = f16 ? k_mmq_skinny<QT, MT, NT, KW, true> : k_mmq_skinny<QT, MT, NT, KW, false>;
-  static bool attr_set[2] = {false, false};
-  if (shm > 64 * 1024 && !attr_set[f16]) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, shm);
-    if (e != hipSuccess) return e;
-    attr_set[f16] = true;
-  }
-  const dim3 grid((N + 16 * NT - 1) / (16 * NT));
-  hipLaunchKernelGGL(kern, grid, dim3(64 * KW), shm, s, W, A, Y, bias, M, N, K, mode);
-  return hipGetLastError();
-}
-
-template <int QT, int MT, int NT>
-hipError_t launch_kw(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                     int M, int N, int K, int mode, hipStream_t s) {
-  // enough waves to cover the chip (~16 per CU) without splitting K finer
-  // than one super-block per wave, within the LDS budget
-  using St = Stage<QT, MT, NT>;
-  const int tiles = (N + 16 * NT - 1) / (16 * NT);
-  const int nsb = K >> 8;
-  int kw = 1;
-  while (kw < 16 && kw * 2 <= nsb && tiles * kw < 4096 && (2 * kw) * St::kBytes <= kMaxLds)
-    kw *= 2;
-  static const int kw_env = [] {
-    const char *e = getenv("IFX_SKINNY_KW");
+// Super-block splits: enough workgroups for ~16 waves per CU, at least two
+// super-blocks per split.  IFX_SKINNY_SPLIT overrides (tuning; read once).
+int choose_splits(int row_groups, int nsb) {
+  static const int env = [] {
+    const char *e = getenv("IFX_SKINNY_SPLIT");
     return e ? atoi(e) : 0;
   }();
-  if (kw_env > 0 && kw_env <= nsb && kw_env * St::kBytes <= kMaxLds) kw = kw_env;
-  switch (kw) {
-  case 1: return launch_k<QT, MT, NT, 1>(W, A, Y, bias, f16, M, N, K, mode, s);
-  case 2: return launch_k<QT, MT, NT, 2>(W, A, Y, bias, f16, M, N, K, mode, s);
-  case 4: return launch_k<QT, MT, NT, 4>(W, A, Y, bias, f16, M, N, K, mode, s);
-  case 8: return launch_k<QT, MT, NT, 8>(W, A, Y, bias, f16, M, N, K, mode, s);
-  default:
-    if constexpr (16 * St::kBytes <= kMaxLds)
-      return launch_k<QT, MT, NT, 16>(W, A, Y, bias, f16, M, N, K, mode, s);
-    else
-      return launch_k<QT, MT, NT, 8>(W, A, Y, bias, f16, M, N, K, mode, s);
+  int ks = env > 0 ? env : (1024 + row_groups - 1) / row_groups;
+  ks = max(1, min(ks, nsb / 2 > 0 ? nsb / 2 : 1));
+  return ks;
+}
+
+template <int QT, int MT>
+hipError_t launch_mt(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16, int M,
+                     int N, int K, int mode, hipStream_t s) {
+  constexpr int shm = Stage<QT, MT>::kBytes;
+  const int groups = (N + 16 * kWaves - 1) / (16 * kWaves);
+  const int nsb = K >> 8;
+  int ks = f16 ? 1 : choose_splits(groups, nsb);
+  const int sb_per = (nsb + ks - 1) / ks;
+  ks = (nsb + sb_per - 1) / sb_per;
+  const dim3 grid(groups, ks);
+  if (f16) {
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, true, false>), grid, dim3(64 * kWaves), shm, s, W, A,
+                       Y, bias, M, N, K, mode, sb_per);
+  } else if (ks == 1) {
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, false>), grid, dim3(64 * kWaves), shm, s, W, A,
+                       Y, bias, M, N, K, mode, sb_per);
+  } else {
+    if (mode != 1) {  // store / bias: the splits add into a zeroed Y
+      const int64_t n = static_cast<int64_t>(M) * N;
+      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                         static_cast<float *>(Y), n);
+    }
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, true>), grid, dim3(64 * kWaves), shm, s, W, A,
+                       Y, bias, M, N, K, mode, sb_per);
   }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -452,14 +403,14 @@ hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, c
   const bool two = M > 16;  // two m-tiles of 16
   switch (qtype) {
   case kTypeQ4_K:
-    return two ? launch_kw<kTypeQ4_K, 2, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_kw<kTypeQ4_K, 1, 2>(w, a, Y, bias, f16, M, N, K, mode, stream);
+    return two ? launch_mt<kTypeQ4_K, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
+               : launch_mt<kTypeQ4_K, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
   case kTypeQ6_K:
-    return two ? launch_kw<kTypeQ6_K, 2, 1>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_kw<kTypeQ6_K, 1, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
+    return two ? launch_mt<kTypeQ6_K, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
+               : launch_mt<kTypeQ6_K, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
   case kTypeQ8_0:
-    return two ? launch_kw<kTypeQ8_0, 2, 1>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_kw<kTypeQ8_0, 1, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
+    return two ? launch_mt<kTypeQ8_0, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
+               : launch_mt<kTypeQ8_0, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
   default: return hipErrorInvalidValue;
   }
 }
