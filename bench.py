@@ -26,6 +26,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 ROTATE_BYTES = 512 << 20
+# HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
+# (FETCH_SIZE, WRITE_SIZE), each scaled by what the counter reads for a copy
+# of exactly 64 MiB; summary and commands in profiles/k_gemv_q4k_11008x2048_m1.md.
+DOMINANT_TRAFFIC_BYTES = 12785755
 
 
 def parse():
@@ -36,6 +40,9 @@ def parse():
     p.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--profile", action="store_true",
+                   help="profiling run: only the dominant GEMV (eager launches), the HBM "
+                        "read probe and a copy of known size for counter calibration")
     return p.parse_args()
 
 
@@ -53,6 +60,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.profile:
+        profile_run(args, dev)
+        return
 
     def ev():
         return torch.cuda.Event(enable_timing=True)
@@ -173,7 +183,7 @@ def main():
     achieved = dom_bytes / dom_us / 1e3
     result["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
         "kernel": f"k_gemv<Q4_K,MC=1> N={N} K={K} M=1", "bytes_per_launch": dom_bytes,
         "us_per_launch": round(dom_us, 3),
     }
@@ -282,6 +292,63 @@ def main():
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
+
+
+def probe_lib():
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "inferflux_amd", "libifx_probe.so"))
+    for fn in (lib.ifx_probe_read, lib.ifx_probe_copy):
+        fn.restype = ctypes.c_int
+    lib.ifx_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                   ctypes.c_int, ctypes.c_void_p]
+    lib.ifx_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                   ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def profile_run(args, dev):
+    """Eager launches for rocprofv3: `steps` launches of the dominant GEMV
+    (Q4_K 11008 x 2048, M = 1, rotating weight replicas), 20 copies of
+    exactly 64 MiB (k_probe_copy: FETCH_SIZE and WRITE_SIZE per dispatch of
+    a known 64 MiB read and 64 MiB write calibrate the counters), and 20
+    streaming reads of the GEMV's weight bytes (k_probe_read: the HBM read
+    rate at this transfer size).  Prints one JSON line of event timings."""
+    import torch
+
+    from inferflux_amd import ops, synth
+
+    stream = torch.cuda.current_stream()
+    qt, N, K = ops.Q4_K, 11008, 2048
+    w = torch.from_numpy(synth.blocks(qt, N, K, seed=0)).to(dev)
+    R = max(2, -(-ROTATE_BYTES // w.numel()))
+    reps = [w] + [w.clone() for _ in range(R - 1)]
+    A = ops.quantize_q8_1(torch.from_numpy(synth.activations(1, K, seed=0)).to(dev))
+    Y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    for i in range(args.warmup):
+        ops.qgemv(qt, reps[i % R], A, 1, N, K, out=Y)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
+        ops.qgemv(qt, reps[i % R], A, 1, N, K, out=Y)
+    b.record(stream)
+    torch.cuda.synchronize()
+    gemv_us = a.elapsed_time(b) * 1e3 / args.steps
+
+    lib = probe_lib()
+    sp = stream.cuda_stream
+    big = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(big)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    for _ in range(20):
+        assert lib.ifx_probe_copy(dst.data_ptr(), big.data_ptr(), big.numel(), 8192, sp) == 0
+    nbytes = w.numel()
+    for i in range(20):
+        assert lib.ifx_probe_read(reps[i % R].data_ptr(), nbytes, sink.data_ptr(), 16384, sp) == 0
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "dominant gemv", "kernel": "k_gemv Q4_K N=11008 K=2048 M=1",
+                      "launches": args.steps, "event_us_per_launch": round(gemv_us, 3),
+                      "copy_bytes": big.numel(), "read_probe_bytes": nbytes}), flush=True)
 
 
 def cpu_baseline(budget_s):
