@@ -72,6 +72,18 @@ int ifx_q8_1_quantize_f16(const uint16_t *x, void *q8_1, int M, int K, void *str
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
               int mode, const void *bias, int M, int N, int K, void *stream);
 
+/* count (1..3) sibling projections of one quant type that read the same
+ * Q8_1 activations, e.g. gate + up or Q + K + V: y_i (op)= W_i . a with
+ * W_i [N[i]][K] and Y_i [M][N[i]].  For M <= 2 this is one launch whose
+ * workgroups walk the rows of all projections; larger M runs one MFMA
+ * launch per projection.  mode: IFX_STORE or IFX_ACCUM (no bias).  W, Y and
+ * N are host arrays of count entries.
+ * Replaces FusedQuantGemm::GemvQ8_1Pair / GemvQ8_1Triple
+ * (fused_quant_gemm.h:272-276, 309-313; kernels mmvq.cuh:1197-1448). */
+int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *const *Y,
+                      const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
+                      void *stream);
+
 /* The prefill GEMM alone (int8 MFMA, fp32 accumulate), for any M >= 1.
  * Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
  * (quantized_weight_map.cpp:176-233, cublas_gemm.h:47, called at
@@ -90,6 +102,12 @@ int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int6
  * Replaces FusedQuantGemm::SupportsQ8_1Activations (fused_quant_gemm.h:333)
  * combined with ShouldUseFusedPath (fused_quant_gemm.h:388-391). */
 int ifx_supports(int quant_type, int M, int N, int K);
+
+/* Kernel family ifx_qgemv runs (quant_type, M, N, K) on: 0 = not supported,
+ * 1 = v_dot4 GEMV, 2 = skinny int8 MFMA (decode batches), 3 = tiled int8
+ * MFMA (prefill).  No reference counterpart (the reference logs the choice,
+ * fused_quant_gemm.cu:2104-2117). */
+int ifx_kernel_family(int quant_type, int M, int N, int K);
 
 /* Bytes per block / values per block of a quant type (0 if unknown). */
 int ifx_block_bytes(int quant_type);

@@ -16,8 +16,10 @@ SIGNATURES = {
     "ifx_q8_1_quantize_f32": ([_vp, _vp, _i32, _i32, _vp], _i32),
     "ifx_q8_1_quantize_f16": ([_vp, _vp, _i32, _i32, _vp], _i32),
     "ifx_qgemv": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_qgemv_grouped": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
+    "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_supports": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_block_bytes": ([_i32], _i32),
     "ifx_block_elems": ([_i32], _i32),

@@ -22,7 +22,8 @@ COMMON = [
 ]
 # Bit-exact kernels: no fp contraction anywhere in these translation units.
 EXACT = {"quantize.hip", "dequant.hip"}
-SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "gemm_mfma.hip"]
+SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "gemm_mfma.hip",
+           "../host/fused_quant_gemm.cpp"]
 
 
 def _run(cmd):
@@ -40,9 +41,11 @@ def build(verbose=True):
     objs = []
     procs = []
     for src in SOURCES:
-        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        obj = os.path.join(OBJ, os.path.basename(src).rsplit(".", 1)[0] + ".o")
         flags = COMMON + (["-ffp-contract=off"] if src in EXACT else [])
-        cmd = [HIPCC] + flags + ["-c", os.path.join(CSRC, src), "-o", obj]
+        path = os.path.normpath(os.path.join(CSRC, src))
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        cmd = [HIPCC] + flags + ["-c"] + lang + [path, "-o", obj]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
                                             stderr=subprocess.PIPE, text=True)))
         objs.append(obj)

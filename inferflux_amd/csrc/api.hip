@@ -17,6 +17,9 @@ hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int6
                              hipStream_t stream);
 hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const void *bias,
                        bool f16, int M, int N, int K, int mode, hipStream_t stream);
+hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void *const *Y,
+                               const int *N, const void *A, bool f16, int M, int K, int mode,
+                               hipStream_t stream);
 hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, const void *bias,
                              bool f16, int M, int N, int K, int mode, hipStream_t stream);
 hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
@@ -100,6 +103,12 @@ int ifx_supports(int quant_type, int M, int N, int K) {
   return 1;
 }
 
+int ifx_kernel_family(int quant_type, int M, int N, int K) {
+  if (!ifx_supports(quant_type, M, N, K)) return 0;
+  if (M <= kMaxGemvM || K % 256 != 0) return 1;
+  return M <= kMaxSkinnyM ? 2 : 3;
+}
+
 int ifx_q8_1_quantize_f32(const float *x, void *q8_1, int M, int K, void *stream) {
   if (!x || !q8_1) return IFX_NULL_POINTER;
   if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
@@ -125,6 +134,31 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (M <= kMaxSkinnyM)
     return status_of(ifx::launch_mmq_skinny(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+}
+
+int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *const *Y,
+                      const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
+                      void *stream) {
+  if (!W || !Y || !N) return IFX_NULL_POINTER;
+  if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
+  if (mode == IFX_BIAS) return IFX_BAD_GEOMETRY;
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_gemm_args(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M,
+                                   N[i], K);
+    if (rc != IFX_OK) return rc;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  if (M <= kMaxGemvM || K % 256 != 0)
+    return status_of(
+        ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
+  // batched decode and prefill: one launch per projection (each fills the chip)
+  for (int i = 0; i < count; ++i) {
+    const int rc = ifx_qgemv(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],
+                             K, stream);
+    if (rc != IFX_OK) return rc;
+  }
+  return IFX_OK;
 }
 
 int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,

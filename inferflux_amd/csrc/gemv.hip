@@ -233,21 +233,43 @@ __device__ __forceinline__ void q8_0_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t 
 
 // ---------------------------------------------------------------------------
 // Kernel.  blockDim = 64 * G * P: P row groups of G waves.  blockIdx.y
-// selects the group of MC batch columns.
+// selects the group of MC batch columns.  blockIdx.x walks the row groups of
+// up to kMaxSeg projections that share the activations A (the reference's
+// grouped pair/triple launches, mmvq.cuh:1197-1448): workgroups
+// [seg[i].blk_begin, seg[i + 1].blk_begin) belong to projection i.
 // ---------------------------------------------------------------------------
+constexpr int kMaxSeg = 3;
+
+struct GemvSeg {
+  const uint8_t *W;
+  void *Y;
+  const void *bias;
+  int N;
+  int blk_begin;
+};
+
+struct GemvArgs {
+  GemvSeg seg[kMaxSeg];
+  int nseg;
+  const uint8_t *A;
+  int M, K, mode;
+};
+
 template <int QT, int MC, int R, int G, int P, bool F16OUT>
-__global__ __launch_bounds__(64 * G * P) void k_gemv(const uint8_t *__restrict__ W,
-                                                     const uint8_t *__restrict__ A,
-                                                     void *__restrict__ Y,
-                                                     const void *__restrict__ bias, int M, int N,
-                                                     int K, int mode) {
+__global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   constexpr int V = R * MC;  // partial sums per lane; a power of two <= 64
   __shared__ float red[(G > 1) ? P * G * V : 1];
+  const int bx = blockIdx.x;
+  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+                 : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
+  const GemvSeg &sg = args.seg[si];
+  const uint8_t *__restrict__ W = sg.W;
+  const int N = sg.N, M = args.M, K = args.K, mode = args.mode;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int gw = wave % G;   // wave within its row group
   const int grp = wave / G;  // row group within the workgroup
-  const int row0 = (blockIdx.x * P + grp) * R;
+  const int row0 = ((bx - sg.blk_begin) * P + grp) * R;
   const int col0 = blockIdx.y * MC;
   const int mvalid = min(MC, M - col0);
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
@@ -256,7 +278,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const uint8_t *__restrict__
                                              : static_cast<uint32_t>(K >> 5) * kQ8_0Bytes;
   // 32-bit ranges (the launcher checks the tensors are below 4 GiB)
   const rsrc_t Wr = make_rsrc(W, w_row * static_cast<uint32_t>(N));
-  const rsrc_t Ar = make_rsrc(A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
+  const rsrc_t Ar = make_rsrc(args.A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
 
   uint32_t rows[R];  // byte offset of each row (rows past N repeat row N-1)
 #pragma unroll
@@ -316,41 +338,44 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const uint8_t *__restrict__
   if (row >= N || c >= mvalid) return;
   const int64_t o_idx = static_cast<int64_t>(col0 + c) * N + row;
   if constexpr (F16OUT) {
-    uint16_t *Yh = static_cast<uint16_t *>(Y);
+    uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
     if (mode == kOutAccum) y += h2f(Yh[o_idx]);
-    else if (mode == kOutBias) y += h2f(static_cast<const uint16_t *>(bias)[row]);
+    else if (mode == kOutBias) y += h2f(static_cast<const uint16_t *>(sg.bias)[row]);
     Yh[o_idx] = static_cast<uint16_t>(f2h_bits(y));
   } else {
-    float *Yf = static_cast<float *>(Y);
+    float *Yf = static_cast<float *>(sg.Y);
     if (mode == kOutAccum) y += Yf[o_idx];
-    else if (mode == kOutBias) y += static_cast<const float *>(bias)[row];
+    else if (mode == kOutBias) y += static_cast<const float *>(sg.bias)[row];
     Yf[o_idx] = y;
   }
 }
 
 template <int QT, int MC, int R, int G>
-static void launch_t(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                     int M, int N, int K, int mode, hipStream_t s) {
+static void launch_t(GemvArgs args, bool f16, hipStream_t s) {
   constexpr int P = (G >= 3) ? 1 : 4 / G;
-  const int groups = (N + R - 1) / R;
-  const dim3 grid((groups + P - 1) / P, (M + MC - 1) / MC);
+  int blocks = 0;
+  for (int i = 0; i < args.nseg; ++i) {
+    args.seg[i].blk_begin = blocks;
+    const int groups = (args.seg[i].N + R - 1) / R;
+    blocks += (groups + P - 1) / P;
+  }
+  const dim3 grid(blocks, (args.M + MC - 1) / MC);
   const dim3 block(64 * G * P);
   if (f16)
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, true>), grid, block, 0, s, W, A, Y, bias, M, N, K, mode);
+    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, true>), grid, block, 0, s, args);
   else
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false>), grid, block, 0, s, W, A, Y, bias, M, N, K, mode);
+    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false>), grid, block, 0, s, args);
 }
 
 template <int QT, int MC, int R>
-static void launch_g(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                     int M, int N, int K, int mode, hipStream_t s) {
+static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
   // waves per row group: enough lanes to cover the K/32 slices, at most 4
-  const int nslice = K >> 5;
+  const int nslice = args.K >> 5;
   const int g = (nslice + 63) / 64;
-  if (g <= 1) launch_t<QT, MC, R, 1>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else if (g == 2) launch_t<QT, MC, R, 2>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else if (g == 3) launch_t<QT, MC, R, 3>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else launch_t<QT, MC, R, 4>(W, A, Y, bias, f16, M, N, K, mode, s);
+  if (g <= 1) launch_t<QT, MC, R, 1>(args, f16, s);
+  else if (g == 2) launch_t<QT, MC, R, 2>(args, f16, s);
+  else if (g == 3) launch_t<QT, MC, R, 3>(args, f16, s);
+  else launch_t<QT, MC, R, 4>(args, f16, s);
 }
 
 // Rows per wave: enough waves to keep ~4 per SIMD in flight on small N, more
@@ -368,23 +393,33 @@ static int rows_per_wave(int N) {
 }
 
 template <int QT, int MC>
-static void launch_r(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                     int M, int N, int K, int mode, hipStream_t s) {
-  switch (rows_per_wave(N)) {
-  case 1: launch_g<QT, MC, 1>(W, A, Y, bias, f16, M, N, K, mode, s); break;
-  case 2: launch_g<QT, MC, 2>(W, A, Y, bias, f16, M, N, K, mode, s); break;
-  case 8: launch_g<QT, MC, 8>(W, A, Y, bias, f16, M, N, K, mode, s); break;
-  default: launch_g<QT, MC, 4>(W, A, Y, bias, f16, M, N, K, mode, s); break;
+static void launch_r(const GemvArgs &args, bool f16, hipStream_t s) {
+  int n_total = 0;
+  for (int i = 0; i < args.nseg; ++i) n_total += args.seg[i].N;
+  switch (rows_per_wave(n_total)) {
+  case 1: launch_g<QT, MC, 1>(args, f16, s); break;
+  case 2: launch_g<QT, MC, 2>(args, f16, s); break;
+  case 8: launch_g<QT, MC, 8>(args, f16, s); break;
+  default: launch_g<QT, MC, 4>(args, f16, s); break;
   }
 }
 
 template <int QT>
-static void launch_type(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                        int M, int N, int K, int mode, hipStream_t s) {
-  if (M == 1) launch_r<QT, 1>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else if (M == 2) launch_r<QT, 2>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else if (M <= 4) launch_g<QT, 4, 4>(W, A, Y, bias, f16, M, N, K, mode, s);
-  else launch_g<QT, 8, 4>(W, A, Y, bias, f16, M, N, K, mode, s);
+static void launch_type(const GemvArgs &args, bool f16, hipStream_t s) {
+  if (args.M == 1) launch_r<QT, 1>(args, f16, s);
+  else if (args.M == 2) launch_r<QT, 2>(args, f16, s);
+  else if (args.M <= 4) launch_g<QT, 4, 4>(args, f16, s);
+  else launch_g<QT, 8, 4>(args, f16, s);
+}
+
+static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStream_t stream) {
+  switch (qtype) {
+  case kTypeQ4_K: launch_type<kTypeQ4_K>(args, f16, stream); break;
+  case kTypeQ6_K: launch_type<kTypeQ6_K>(args, f16, stream); break;
+  case kTypeQ8_0: launch_type<kTypeQ8_0>(args, f16, stream); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // Geometry is validated by the caller: K % 256 == 0 for Q4_K/Q6_K,
@@ -392,15 +427,30 @@ static void launch_type(const uint8_t *W, const uint8_t *A, void *Y, const void 
 // (gridDim.y); the MFMA kernel covers large M.
 hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const void *bias,
                        bool f16, int M, int N, int K, int mode, hipStream_t stream) {
-  const uint8_t *w = static_cast<const uint8_t *>(W);
-  const uint8_t *a = static_cast<const uint8_t *>(A);
-  switch (qtype) {
-  case kTypeQ4_K: launch_type<kTypeQ4_K>(w, a, Y, bias, f16, M, N, K, mode, stream); break;
-  case kTypeQ6_K: launch_type<kTypeQ6_K>(w, a, Y, bias, f16, M, N, K, mode, stream); break;
-  case kTypeQ8_0: launch_type<kTypeQ8_0>(w, a, Y, bias, f16, M, N, K, mode, stream); break;
-  default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  GemvArgs args{};
+  args.seg[0] = GemvSeg{static_cast<const uint8_t *>(W), Y, bias, N, 0};
+  args.nseg = 1;
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = mode;
+  return launch_args(qtype, args, f16, stream);
+}
+
+// count (1..3) projections of one quant type over the same A, one launch.
+hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void *const *Y,
+                               const int *N, const void *A, bool f16, int M, int K, int mode,
+                               hipStream_t stream) {
+  if (count < 1 || count > kMaxSeg) return hipErrorInvalidValue;
+  GemvArgs args{};
+  for (int i = 0; i < count; ++i)
+    args.seg[i] = GemvSeg{static_cast<const uint8_t *>(W[i]), Y[i], nullptr, N[i], 0};
+  args.nseg = count;
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = mode;
+  return launch_args(qtype, args, f16, stream);
 }
 
 }  // namespace ifx

@@ -1,0 +1,199 @@
+// fused_quant_gemm.cpp -- C++ host mirror of InferFlux's FusedQuantGemm
+// (runtime/backends/cuda/native/fused_quant_gemm.cu) over the gfx950 C ABI
+// (include/ifx_qgemm.h).  It carries the reference's host conventions --
+// bool "launched" results, QuantizedWeightInfo views, the
+// INFERFLUX_DISABLE_FUSED_GEMV policy switch -- and leaves every launch to
+// the C ABI, which validates arguments and reports HIP errors.
+#include "../../include/ifx_fused_quant_gemm.h"
+
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/ifx_qgemm.h"
+
+namespace inferflux {
+namespace rocm {
+
+namespace {
+
+// Policy resolution (fused_quant_gemm.cu:28-42): an explicit policy wins,
+// else the environment, read on each call as the reference does.
+NativeExecutionPolicy Resolve(const NativeExecutionPolicy *policy) {
+  return policy ? *policy : NativeExecutionPolicy::FromEnv();
+}
+
+bool ParseBoolEnv(const char *name, bool fallback) {
+  const char *v = std::getenv(name);
+  if (!v || !*v) return fallback;
+  if (!std::strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes") ||
+      !strcasecmp(v, "on"))
+    return true;
+  if (!std::strcmp(v, "0") || !strcasecmp(v, "false") || !strcasecmp(v, "no") ||
+      !strcasecmp(v, "off"))
+    return false;
+  return fallback;
+}
+
+bool Usable(const QuantizedWeightInfo &w, const void *act, const void *out) {
+  return w.data && w.quant_type >= 0 && act && out;
+}
+
+// The view must hold at least N x K elements when its size is known.
+bool ViewCovers(const QuantizedWeightInfo &w, int N, int K) {
+  return w.num_elements <= 0 ||
+         w.num_elements >= static_cast<int64_t>(N) * static_cast<int64_t>(K);
+}
+
+bool Launch(const QuantizedWeightInfo &w, const void *act, void *out, int out_dtype, int mode,
+            const void *bias, int M, int N, int K, hipStream_t stream,
+            const NativeExecutionPolicy *policy) {
+  if (!Usable(w, act, out)) return false;
+  if (Resolve(policy).disable_fused_gemv) return false;
+  if (!ViewCovers(w, N, K)) return false;
+  const FusedDispatchGeometry g{M, N, K, 1, true, false};
+  if (!FusedQuantGemm::ShouldUseFusedPath(w.quant_type, g)) return false;
+  return ifx_qgemv(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K, stream) ==
+         IFX_OK;
+}
+
+template <size_t C>
+bool LaunchGroup(const std::array<PackedProjectionSpec, C> &p, const void *act, int M, int K,
+                 hipStream_t stream, const NativeExecutionPolicy *policy) {
+  if (!act || Resolve(policy).disable_fused_gemv) return false;
+  const void *W[C];
+  void *Y[C];
+  int N[C];
+  for (size_t i = 0; i < C; ++i) {
+    if (!Usable(p[i].weight, act, p[i].output)) return false;
+    if (p[i].weight.quant_type != p[0].weight.quant_type) return false;
+    if (!ViewCovers(p[i].weight, p[i].output_cols, K)) return false;
+    W[i] = p[i].weight.data;
+    Y[i] = p[i].output;
+    N[i] = p[i].output_cols;
+  }
+  const FusedDispatchGeometry g{M, N[0], K, static_cast<int>(C), true, false};
+  if (!FusedQuantGemm::ShouldUseFusedPath(p[0].weight.quant_type, g)) return false;
+  return ifx_qgemv_grouped(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
+                           IFX_OUT_F16, IFX_STORE, M, K, stream) == IFX_OK;
+}
+
+}  // namespace
+
+NativeExecutionPolicy NativeExecutionPolicy::FromEnv() {
+  NativeExecutionPolicy p;
+  p.disable_fused_gemv = ParseBoolEnv("INFERFLUX_DISABLE_FUSED_GEMV", false);
+  return p;
+}
+
+void FusedQuantGemm::QuantizeRowQ8_1(const uint16_t *input, void *output_q8_1, int M, int K,
+                                     hipStream_t stream) {
+  ifx_q8_1_quantize_f16(input, output_q8_1, M, K, stream);
+}
+
+void FusedQuantGemm::QuantizeRowQ8_1(const float *input, void *output_q8_1, int M, int K,
+                                     hipStream_t stream) {
+  ifx_q8_1_quantize_f32(input, output_q8_1, M, K, stream);
+}
+
+bool FusedQuantGemm::GemvQ8_1(const QuantizedWeightInfo &weight, const void *act_q8_1,
+                              uint16_t *output, int M, int N, int K, hipStream_t stream,
+                              const NativeExecutionPolicy *policy) {
+  return Launch(weight, act_q8_1, output, IFX_OUT_F16, IFX_STORE, nullptr, M, N, K, stream,
+                policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1F32(const QuantizedWeightInfo &weight, const void *act_q8_1,
+                                 float *output, int M, int N, int K, hipStream_t stream,
+                                 const NativeExecutionPolicy *policy) {
+  return Launch(weight, act_q8_1, output, IFX_OUT_F32, IFX_STORE, nullptr, M, N, K, stream,
+                policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1Accum(const QuantizedWeightInfo &weight, const void *act_q8_1,
+                                   uint16_t *output, int M, int N, int K, hipStream_t stream,
+                                   const NativeExecutionPolicy *policy) {
+  return Launch(weight, act_q8_1, output, IFX_OUT_F16, IFX_ACCUM, nullptr, M, N, K, stream,
+                policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1AccumF32(const QuantizedWeightInfo &weight, const void *act_q8_1,
+                                      float *output, int M, int N, int K, hipStream_t stream,
+                                      const NativeExecutionPolicy *policy) {
+  return Launch(weight, act_q8_1, output, IFX_OUT_F32, IFX_ACCUM, nullptr, M, N, K, stream,
+                policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1WithBias(const QuantizedWeightInfo &weight, const void *act_q8_1,
+                                      uint16_t *output, const uint16_t *bias, int M, int N,
+                                      int K, hipStream_t stream,
+                                      const NativeExecutionPolicy *policy) {
+  return Launch(weight, act_q8_1, output, IFX_OUT_F16, bias ? IFX_BIAS : IFX_STORE, bias, M, N,
+                K, stream, policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1Pair(const std::array<PackedProjectionSpec, 2> &projections,
+                                  const void *act_q8_1, int M, int K, hipStream_t stream,
+                                  const NativeExecutionPolicy *policy) {
+  return LaunchGroup(projections, act_q8_1, M, K, stream, policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1Triple(const std::array<PackedProjectionSpec, 3> &projections,
+                                    const void *act_q8_1, int M, int K, hipStream_t stream,
+                                    const NativeExecutionPolicy *policy) {
+  return LaunchGroup(projections, act_q8_1, M, K, stream, policy);
+}
+
+bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
+  return quant_type == static_cast<int>(TensorType::Q4_K) ||
+         quant_type == static_cast<int>(TensorType::Q6_K) ||
+         quant_type == static_cast<int>(TensorType::Q8_0);
+}
+
+// The reference scales a per-GPU-generation base by 16/bpw and clamps to
+// [4, 64] (fused_quant_gemm.cu:62-184, 830-880): above it, dequantize +
+// FP16 cuBLAS wins on its tensor cores.  On gfx950 the quantized path has
+// an int8 MFMA GEMM at every M >= 33 that reads the raw blocks (3.6x fewer
+// bytes than an FP16 copy for Q4_K) and runs at twice the FP16 MFMA rate,
+// so the fallback never wins: the threshold is the path's M limit.
+int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
+  return SupportsQ8_1Activations(quant_type) ? kMaxFusedM : 0;
+}
+
+int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,
+                                              const FusedDispatchGeometry &geometry) {
+  if (geometry.M <= 0) return 0;
+  return GetAdaptiveThreshold(quant_type);
+}
+
+bool FusedQuantGemm::ShouldUseFusedPath(int quant_type, int M) {
+  const FusedDispatchGeometry geometry{M, 0, 0, 1, false, false};
+  return ShouldUseFusedPath(quant_type, geometry);
+}
+
+bool FusedQuantGemm::ShouldUseFusedPath(int quant_type, const FusedDispatchGeometry &geometry) {
+  if (geometry.M <= 0) return false;
+  if (geometry.grouped_outputs < 1 || geometry.grouped_outputs > 3) return false;
+  if (!SupportsQ8_1Activations(quant_type)) return false;
+  if (geometry.M > GetGeometryAwareThreshold(quant_type, geometry)) return false;
+  // Known N and K must fit the kernels (K a whole number of blocks, 32-bit
+  // byte offsets); unknown (0) ones are decided at launch.
+  if (geometry.N > 0 && geometry.K > 0)
+    return ifx_supports(quant_type, geometry.M, geometry.N, geometry.K) != 0;
+  return true;
+}
+
+KernelFamily FusedQuantGemm::SelectKernel(int quant_type, int M, int N, int K) {
+  return static_cast<KernelFamily>(ifx_kernel_family(quant_type, M, N, K));
+}
+
+const char *FusedQuantGemm::KernelFamilyName(KernelFamily family) {
+  switch (family) {
+  case KernelFamily::kGemv: return "v_dot4 GEMV";
+  case KernelFamily::kSkinnyMfma: return "skinny int8 MFMA";
+  case KernelFamily::kTiledMfma: return "tiled int8 MFMA";
+  default: return "none";
+  }
+}
+
+}  // namespace rocm
+}  // namespace inferflux

@@ -95,6 +95,33 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     return out
 
 
+def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mode=STORE,
+                  stream=None):
+    """Sibling projections over one Q8_1 A: [W_i . a for W_i in Ws], one launch
+    for M <= 2.  Returns the list of outputs [M, N_i]."""
+    import ctypes
+    count = len(Ws)
+    if not 1 <= count <= 3 or len(Ns) != count:
+        raise ValueError("1..3 projections with one N each")
+    if outs is None:
+        outs = [torch.empty((M, n), dtype=out_dtype, device=A.device) for n in Ns]
+    for W, n, out in zip(Ws, Ns, outs):
+        if W.numel() < weight_bytes(qtype, n, K):
+            raise ValueError("W is smaller than N x K blocks")
+        if out.numel() < M * n or out.dtype != outs[0].dtype:
+            raise ValueError("bad output tensor")
+    if A.numel() < M * (K // 32) * 36:
+        raise ValueError("A is smaller than M x K/32 Q8_1 blocks")
+    od = OUT_F16 if outs[0].dtype == torch.float16 else OUT_F32
+    wp = (ctypes.c_void_p * count)(*[_dev(w, "W") for w in Ws])
+    yp = (ctypes.c_void_p * count)(*[_dev(y, "out") for y in outs])
+    nn = (ctypes.c_int * count)(*Ns)
+    rc = _lib.load().ifx_qgemv_grouped(qtype, count, wp, yp, nn, _dev(A, "A"), od, mode, M, K,
+                                       _stream(stream))
+    _check(rc, "ifx_qgemv_grouped")
+    return outs
+
+
 def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None):
     out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)
     od = OUT_F16 if out_dtype == torch.float16 else OUT_F32

@@ -1,0 +1,346 @@
+// test_fused_quant_gemm.cpp -- tests of the C++ FusedQuantGemm mirror
+// (include/ifx_fused_quant_gemm.h), in the manner of the reference's
+// tests/unit/test_native_forward.cpp: the policy cases (thresholds,
+// argument rejection, the disable switch) run without a GPU; the GPU cases
+// run each entry point on seeded blocks and compare with the CPU oracle
+// (oracle/ifx_oracle.c, linked as the checker).
+//
+//   test_fused_quant_gemm policy   host-only cases
+//   test_fused_quant_gemm gpu      device cases (needs a GPU)
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cmath>
+#include <memory>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ifx_fused_quant_gemm.h"
+#include "../../include/ifx_qgemm.h"
+
+extern "C" {
+int orc_block_bytes(int qtype);
+int orc_block_elems(int qtype);
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+int orc_quantize_q8_1_f32(const float *x, void *out, int64_t M, int64_t K);
+int orc_gemv_exact(int qtype, const void *W, const void *A, double *y, int M, int N, int K,
+                   int threads);
+}
+
+using inferflux::rocm::FusedDispatchGeometry;
+using inferflux::rocm::FusedQuantGemm;
+using inferflux::rocm::KernelFamily;
+using inferflux::rocm::NativeExecutionPolicy;
+using inferflux::rocm::PackedProjectionSpec;
+using inferflux::rocm::QuantizedWeightInfo;
+
+namespace {
+
+int g_failures = 0;
+
+#define EXPECT(cond)                                                            \
+  do {                                                                          \
+    if (!(cond)) {                                                              \
+      std::printf("  FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);           \
+      ++g_failures;                                                             \
+    }                                                                           \
+  } while (0)
+
+#define HIP_OK(x)                                                               \
+  do {                                                                          \
+    hipError_t e_ = (x);                                                        \
+    if (e_ != hipSuccess) {                                                     \
+      std::printf("  HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, \
+                  __LINE__);                                                    \
+      std::exit(2);                                                             \
+    }                                                                           \
+  } while (0)
+
+constexpr int Q8_0 = 8, Q8_1 = 9, Q4_K = 12, Q6_K = 14;
+
+// xorshift64*: the test's own seeded generator.
+struct Rng {
+  uint64_t s;
+  explicit Rng(uint64_t seed) : s(seed * 0x9E3779B97F4A7C15ull + 1) {}
+  uint64_t next() {
+    s ^= s >> 12;
+    s ^= s << 25;
+    s ^= s >> 27;
+    return s * 0x2545F4914F6CDD1Dull;
+  }
+  float uniform() { return (next() >> 40) * (1.0f / 16777216.0f); }
+  float normal() {
+    const float u1 = uniform() + 1e-7f, u2 = uniform();
+    return std::sqrt(-2.0f * std::log(u1)) * std::cos(6.2831853f * u2);
+  }
+};
+
+// Random blocks with finite fp16 scales: d, dmin = |N(0,1)| * 0.01.
+std::vector<uint8_t> MakeBlocks(int qtype, int N, int K, uint64_t seed) {
+  Rng r(seed);
+  const int bb = orc_block_bytes(qtype), be = orc_block_elems(qtype);
+  const int64_t nb = static_cast<int64_t>(N) * (K / be);
+  std::vector<uint8_t> w(nb * bb);
+  for (auto &b : w) b = static_cast<uint8_t>(r.next() >> 56);
+  for (int64_t i = 0; i < nb; ++i) {
+    uint8_t *blk = w.data() + i * bb;
+    auto put = [&](int off) {
+      const uint16_t h = orc_f32_to_f16(std::fabs(r.normal()) * 0.01f);
+      std::memcpy(blk + off, &h, 2);
+    };
+    if (qtype == Q4_K) { put(0); put(2); }
+    else if (qtype == Q6_K) {
+      for (int j = 0; j < 16; ++j) blk[192 + j] = static_cast<uint8_t>(static_cast<int8_t>(r.next() % 128) - 64);
+      put(208);
+    } else {
+      put(0);
+      for (int j = 0; j < 32; ++j) blk[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(r.next() % 255) - 127);
+    }
+  }
+  return w;
+}
+
+struct Dev {
+  void *p = nullptr;
+  explicit Dev(size_t n) { HIP_OK(hipMalloc(&p, n ? n : 1)); }
+  ~Dev() { (void)hipFree(p); }
+  template <typename T> T *as() { return static_cast<T *>(p); }
+};
+
+// max_row |y - ye| <= rel * ||ye_row|| (+ fp16 output rounding when half).
+bool RowsClose(const std::vector<float> &y, const std::vector<double> &ye, int M, int N,
+               double rel, bool half_out) {
+  for (int m = 0; m < M; ++m) {
+    double nrm = 0, err = 0, mag = 0;
+    for (int n = 0; n < N; ++n) {
+      const double e = ye[static_cast<size_t>(m) * N + n];
+      nrm += e * e;
+      mag = std::fmax(mag, std::fabs(e));
+      err = std::fmax(err, std::fabs(y[static_cast<size_t>(m) * N + n] - e));
+    }
+    const double lim = rel * std::sqrt(nrm) + (half_out ? mag * (1.0 / 1024) : 0.0);
+    if (!(err <= lim)) {
+      std::printf("  row %d: max err %.3e > %.3e\n", m, err, lim);
+      return false;
+    }
+  }
+  return true;
+}
+
+std::vector<float> HalfToFloat(const std::vector<uint16_t> &h) {
+  std::vector<float> f(h.size());
+  for (size_t i = 0; i < h.size(); ++i) f[i] = orc_f16_to_f32(h[i]);
+  return f;
+}
+
+// ---------------------------------------------------------------- policy
+void TestPolicy() {
+  std::printf("[policy]\n");
+  EXPECT(FusedQuantGemm::SupportsQ8_1Activations(Q4_K));
+  EXPECT(FusedQuantGemm::SupportsQ8_1Activations(Q6_K));
+  EXPECT(FusedQuantGemm::SupportsQ8_1Activations(Q8_0));
+  EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(Q8_1));
+  EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(0));
+  EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(15));
+
+  // thresholds: no crossover to a fallback on gfx950
+  EXPECT(FusedQuantGemm::GetAdaptiveThreshold(Q4_K) == FusedQuantGemm::kMaxFusedM);
+  EXPECT(FusedQuantGemm::GetAdaptiveThreshold(1) == 0);
+  EXPECT(!FusedQuantGemm::ShouldUseFusedPath(Q4_K, 0));
+  EXPECT(FusedQuantGemm::ShouldUseFusedPath(Q4_K, 1));
+  EXPECT(FusedQuantGemm::ShouldUseFusedPath(Q6_K, 64));
+  EXPECT(FusedQuantGemm::ShouldUseFusedPath(Q8_0, 512));
+  EXPECT(!FusedQuantGemm::ShouldUseFusedPath(Q8_1, 1));
+  {
+    FusedDispatchGeometry g{8, 4096, 2048, 4, true, false};
+    EXPECT(!FusedQuantGemm::ShouldUseFusedPath(Q4_K, g));  // no 4-way group
+    g.grouped_outputs = 3;
+    EXPECT(FusedQuantGemm::ShouldUseFusedPath(Q4_K, g));
+    g.K = 2080;  // not a whole number of Q4_K super-blocks
+    EXPECT(!FusedQuantGemm::ShouldUseFusedPath(Q4_K, g));
+    EXPECT(FusedQuantGemm::ShouldUseFusedPath(Q8_0, g));  // 65 Q8_0 blocks
+  }
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 1, 11008, 2048) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 2, 11008, 2048) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 8, 11008, 2048) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kTiledMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 1, 64, 100) == KernelFamily::kNone);
+  EXPECT(std::string(FusedQuantGemm::KernelFamilyName(KernelFamily::kTiledMfma)) ==
+         "tiled int8 MFMA");
+
+  // rejected calls return false before any launch (no GPU needed)
+  uint16_t dummy_out[4];
+  const uint8_t dummy[64] = {};
+  QuantizedWeightInfo w{dummy, Q4_K, 256};
+  EXPECT(!FusedQuantGemm::GemvQ8_1(QuantizedWeightInfo{}, dummy, dummy_out, 1, 1, 256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, nullptr, dummy_out, 1, 1, 256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, dummy, nullptr, 1, 1, 256, nullptr));
+  QuantizedWeightInfo bad_type{dummy, Q8_1, 256};
+  EXPECT(!FusedQuantGemm::GemvQ8_1(bad_type, dummy, dummy_out, 1, 1, 256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, dummy, dummy_out, 0, 1, 256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, dummy, dummy_out, 1, 1, 100, nullptr));
+  QuantizedWeightInfo small{dummy, Q4_K, 255};  // view smaller than N x K
+  EXPECT(!FusedQuantGemm::GemvQ8_1(small, dummy, dummy_out, 1, 1, 256, nullptr));
+  NativeExecutionPolicy off;
+  off.disable_fused_gemv = true;
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, dummy, dummy_out, 1, 1, 256, nullptr, &off));
+  EXPECT(!FusedQuantGemm::GemvQ8_1AccumF32(w, dummy, reinterpret_cast<float *>(dummy_out), 1, 1,
+                                           256, nullptr, &off));
+  setenv("INFERFLUX_DISABLE_FUSED_GEMV", "1", 1);
+  EXPECT(NativeExecutionPolicy::FromEnv().disable_fused_gemv);
+  EXPECT(!FusedQuantGemm::GemvQ8_1(w, dummy, dummy_out, 1, 1, 256, nullptr));
+  setenv("INFERFLUX_DISABLE_FUSED_GEMV", "off", 1);
+  EXPECT(!NativeExecutionPolicy::FromEnv().disable_fused_gemv);
+  unsetenv("INFERFLUX_DISABLE_FUSED_GEMV");
+  // grouped: mixed quant types or a null output are not handled
+  std::array<PackedProjectionSpec, 2> mixed{
+      PackedProjectionSpec{QuantizedWeightInfo{dummy, Q4_K, 256}, dummy_out, 1},
+      PackedProjectionSpec{QuantizedWeightInfo{dummy, Q6_K, 256}, dummy_out, 1}};
+  EXPECT(!FusedQuantGemm::GemvQ8_1Pair(mixed, dummy, 1, 256, nullptr));
+  mixed[1].weight.quant_type = Q4_K;
+  mixed[1].output = nullptr;
+  EXPECT(!FusedQuantGemm::GemvQ8_1Pair(mixed, dummy, 1, 256, nullptr));
+}
+
+// ------------------------------------------------------------------- gpu
+struct Problem {
+  int qtype, M, N, K;
+  std::vector<uint8_t> w;
+  std::vector<float> x;
+  std::vector<uint8_t> a;  // oracle Q8_1
+  std::vector<double> ye;  // oracle fp64 product
+};
+
+Problem MakeProblem(int qtype, int M, int N, int K, uint64_t seed) {
+  Problem p{qtype, M, N, K, MakeBlocks(qtype, N, K, seed), {}, {}, {}};
+  Rng r(seed + 1000);
+  p.x.resize(static_cast<size_t>(M) * K);
+  for (auto &v : p.x) v = r.normal();
+  p.a.resize(static_cast<size_t>(M) * (K / 32) * 36);
+  orc_quantize_q8_1_f32(p.x.data(), p.a.data(), M, K);
+  p.ye.resize(static_cast<size_t>(M) * N);
+  orc_gemv_exact(qtype, p.w.data(), p.a.data(), p.ye.data(), M, N, K, 8);
+  return p;
+}
+
+void TestGpuCase(int qtype, int M, int N, int K) {
+  std::printf("[gpu] qtype=%d M=%d N=%d K=%d\n", qtype, M, N, K);
+  std::fflush(stdout);
+  Problem p = MakeProblem(qtype, M, N, K, 7 * qtype + M);
+  hipStream_t s;
+  HIP_OK(hipStreamCreate(&s));
+  Dev dw(p.w.size()), dx(p.x.size() * 4), da(p.a.size()), dy(static_cast<size_t>(M) * N * 4),
+      dh(static_cast<size_t>(M) * N * 2), db(static_cast<size_t>(N) * 2);
+  HIP_OK(hipMemcpy(dw.p, p.w.data(), p.w.size(), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dx.p, p.x.data(), p.x.size() * 4, hipMemcpyHostToDevice));
+  FusedQuantGemm::QuantizeRowQ8_1(dx.as<float>(), da.p, M, K, s);
+  HIP_OK(hipStreamSynchronize(s));
+  std::vector<uint8_t> a(p.a.size());
+  HIP_OK(hipMemcpy(a.data(), da.p, a.size(), hipMemcpyDeviceToHost));
+  EXPECT(a == p.a);  // Q8_1 codes and scales bit-exact
+
+  const QuantizedWeightInfo w{dw.p, qtype, static_cast<int64_t>(N) * K};
+  std::vector<float> y(static_cast<size_t>(M) * N);
+  // fp32 store
+  EXPECT(FusedQuantGemm::GemvQ8_1F32(w, da.p, dy.as<float>(), M, N, K, s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipMemcpy(y.data(), dy.p, y.size() * 4, hipMemcpyDeviceToHost));
+  EXPECT(RowsClose(y, p.ye, M, N, 1e-3, false));
+  // fp32 accumulate onto 0.5
+  std::vector<float> base(y.size(), 0.5f);
+  HIP_OK(hipMemcpy(dy.p, base.data(), base.size() * 4, hipMemcpyHostToDevice));
+  EXPECT(FusedQuantGemm::GemvQ8_1AccumF32(w, da.p, dy.as<float>(), M, N, K, s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipMemcpy(y.data(), dy.p, y.size() * 4, hipMemcpyDeviceToHost));
+  for (auto &v : y) v -= 0.5f;
+  EXPECT(RowsClose(y, p.ye, M, N, 1e-3, false));
+  // fp16 store
+  std::vector<uint16_t> h(y.size());
+  EXPECT(FusedQuantGemm::GemvQ8_1(w, da.p, dh.as<uint16_t>(), M, N, K, s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipMemcpy(h.data(), dh.p, h.size() * 2, hipMemcpyDeviceToHost));
+  EXPECT(RowsClose(HalfToFloat(h), p.ye, M, N, 1e-3, true));
+  // fp16 with bias, then fp16 accumulate of the same product
+  std::vector<uint16_t> bias(N);
+  std::vector<double> ye_b(p.ye);
+  for (int n = 0; n < N; ++n) {
+    bias[n] = orc_f32_to_f16(0.25f * static_cast<float>(n % 7) - 0.5f);
+    for (int m = 0; m < M; ++m) ye_b[static_cast<size_t>(m) * N + n] += orc_f16_to_f32(bias[n]);
+  }
+  HIP_OK(hipMemcpy(db.p, bias.data(), bias.size() * 2, hipMemcpyHostToDevice));
+  EXPECT(FusedQuantGemm::GemvQ8_1WithBias(w, da.p, dh.as<uint16_t>(), db.as<uint16_t>(), M, N, K,
+                                          s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipMemcpy(h.data(), dh.p, h.size() * 2, hipMemcpyDeviceToHost));
+  EXPECT(RowsClose(HalfToFloat(h), ye_b, M, N, 1e-3, true));
+  EXPECT(FusedQuantGemm::GemvQ8_1Accum(w, da.p, dh.as<uint16_t>(), M, N, K, s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipMemcpy(h.data(), dh.p, h.size() * 2, hipMemcpyDeviceToHost));
+  std::vector<double> ye_2(ye_b);
+  for (size_t i = 0; i < ye_2.size(); ++i) ye_2[i] += p.ye[i];
+  EXPECT(RowsClose(HalfToFloat(h), ye_2, M, N, 2e-3, true));
+  HIP_OK(hipStreamDestroy(s));
+}
+
+template <size_t C>
+void TestGrouped(int qtype, int M, int K, const std::array<int, C> &Ns) {
+  std::printf("[gpu grouped x%zu] qtype=%d M=%d K=%d\n", C, qtype, M, K);
+  std::fflush(stdout);
+  std::vector<Problem> ps;
+  for (size_t i = 0; i < C; ++i) ps.push_back(MakeProblem(qtype, M, Ns[i], K, 100 + i));
+  // all projections read projection 0's activations
+  std::vector<std::unique_ptr<Dev>> dws, dys;
+  Dev da(ps[0].a.size());
+  HIP_OK(hipMemcpy(da.p, ps[0].a.data(), ps[0].a.size(), hipMemcpyHostToDevice));
+  std::array<PackedProjectionSpec, C> spec{};
+  for (size_t i = 0; i < C; ++i) {
+    dws.emplace_back(new Dev(ps[i].w.size()));
+    dys.emplace_back(new Dev(static_cast<size_t>(M) * Ns[i] * 2));
+    HIP_OK(hipMemcpy(dws[i]->p, ps[i].w.data(), ps[i].w.size(), hipMemcpyHostToDevice));
+    spec[i] = PackedProjectionSpec{QuantizedWeightInfo{dws[i]->p, qtype, int64_t{Ns[i]} * K},
+                                   dys[i]->template as<uint16_t>(), Ns[i]};
+  }
+  bool ok;
+  if constexpr (C == 2) ok = FusedQuantGemm::GemvQ8_1Pair(spec, da.p, M, K, nullptr);
+  else ok = FusedQuantGemm::GemvQ8_1Triple(spec, da.p, M, K, nullptr);
+  EXPECT(ok);
+  HIP_OK(hipDeviceSynchronize());
+  for (size_t i = 0; i < C; ++i) {
+    std::vector<double> ye(static_cast<size_t>(M) * Ns[i]);
+    orc_gemv_exact(qtype, ps[i].w.data(), ps[0].a.data(), ye.data(), M, Ns[i], K, 8);
+    std::vector<uint16_t> h(ye.size());
+    HIP_OK(hipMemcpy(h.data(), dys[i]->p, h.size() * 2, hipMemcpyDeviceToHost));
+    EXPECT(RowsClose(HalfToFloat(h), ye, M, Ns[i], 1e-3, true));
+  }
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const std::string mode = argc > 1 ? argv[1] : "policy";
+  if (mode == "policy") {
+    TestPolicy();
+  } else if (mode == "gpu") {
+    TestGpuCase(Q4_K, 1, 300, 2048);
+    TestGpuCase(Q6_K, 2, 129, 1024);
+    TestGpuCase(Q8_0, 1, 77, 2080);
+    TestGpuCase(Q4_K, 5, 200, 1024);
+    TestGpuCase(Q6_K, 24, 96, 2048);
+    TestGpuCase(Q8_0, 40, 160, 512);
+    TestGrouped<2>(Q4_K, 1, 2048, {300, 173});
+    TestGrouped<3>(Q4_K, 2, 1024, {128, 64, 65});
+    TestGrouped<3>(Q6_K, 1, 512, {33, 1, 250});
+    TestGrouped<2>(Q8_0, 4, 256, {70, 90});
+  } else {
+    std::printf("usage: %s policy|gpu\n", argv[0]);
+    return 2;
+  }
+  std::printf("%s: %d failure(s)\n", mode.c_str(), g_failures);
+  return g_failures ? 1 : 0;
+}

@@ -232,3 +232,39 @@ def test_config4_14b_down_and_gate(orc, dev, M):
 @pytest.mark.parametrize("qtype,N,K", [(Q4_K, 27648, 5120), (Q6_K, 5120, 27648)])
 def test_config5_prefill(orc, dev, qtype, N, K):
     _sampled(orc, dev, qtype, 512, N, K, seed=5, outl=0.01, rows=96)
+
+
+# ------------------------------------- grouped sibling projections (pair/triple)
+@pytest.mark.parametrize("qtype,M,K,Ns", [
+    (Q4_K, 1, 2048, (2560, 11008)),        # 3B QKV-sized + gate-sized
+    (Q4_K, 2, 2048, (11008, 11008)),       # gate + up
+    (Q6_K, 1, 1024, (33, 1, 250)),         # ragged row counts
+    (Q8_0, 2, 2080, (7, 129, 64)),         # K not a multiple of 256
+    (Q4_K, 8, 2048, (300, 173)),           # M > 2: one MFMA launch per projection
+])
+def test_grouped_parity(orc, dev, qtype, M, K, Ns):
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"grouped type={qtype} M={M} K={K} N={Ns}")
+    ws = [synth.blocks(qtype, n, K, seed=11 * i + n) for i, n in enumerate(Ns)]
+    x = synth.activations(M, K, seed=K + M, outlier_frac=0.01)
+    a = orc.quantize_q8_1(x)
+    outs = ops.qgemv_grouped(qtype, [up(w, dev) for w in ws], up(a, dev), M, list(Ns), K)
+    for w, n, y in zip(ws, Ns, outs):
+        check_rows(down(y), orc.gemv_exact(qtype, w, a, M, n, K))
+    # accumulate mode adds onto what the outputs hold
+    base = [torch.full_like(y, 0.25) for y in outs]
+    ops.qgemv_grouped(qtype, [up(w, dev) for w in ws], up(a, dev), M, list(Ns), K,
+                      outs=base, mode=ops.ACCUM)
+    for w, n, y in zip(ws, Ns, base):
+        check_rows(down(y) - 0.25, orc.gemv_exact(qtype, w, a, M, n, K))
+
+
+def test_host_cpp_gpu():
+    """The C++ FusedQuantGemm mirror on the GPU (tests/cpp, vs the oracle)."""
+    import subprocess
+    from tests.test_host_cpp import binary
+    note("host cpp gpu cases")
+    r = subprocess.run([binary(), "gpu"], capture_output=True, text=True, timeout=100)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
