@@ -10,6 +10,8 @@
 #include "../../include/ifx_qgemm.h"
 #include "ifx_common.h"
 
+#include <stdlib.h>
+
 namespace ifx {
 hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
                                 hipStream_t stream);
@@ -20,6 +22,9 @@ hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const v
 hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void *const *Y,
                                const int *N, const void *A, bool f16, int M, int K, int mode,
                                hipStream_t stream);
+hipError_t launch_mmvq(int qtype, int count, const void *const *W, void *const *Y,
+                       const int *N, const void *bias, const void *A, bool f16, int M, int K,
+                       int mode, hipStream_t stream);
 hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, const void *bias,
                              bool f16, int M, int N, int K, int mode, hipStream_t stream);
 hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
@@ -33,8 +38,31 @@ namespace {
 //   M <= 2       v_dot4 GEMV        (gemv.hip)
 //   3 <= M <= 32 skinny int8 MFMA   (mmq_skinny.hip), K % 256 == 0
 //   M > 32       tiled int8 MFMA    (gemm_mfma.hip)
-constexpr int kMaxGemvM = 2;
+constexpr int kMaxGemvMDefault = 2;
 constexpr int kMaxSkinnyM = 32;
+
+// Largest M the v_dot4 GEMV takes; IFX_GEMV_MAX_M in 0..8 overrides it
+// (tuning; read once).
+int max_gemv_m() {
+  static const int v = [] {
+    const char *e = getenv("IFX_GEMV_MAX_M");
+    const int n = e ? atoi(e) : 0;
+    return (n >= 0 && n <= 8 && e) ? n : kMaxGemvMDefault;
+  }();
+  return v;
+}
+
+// Decode-batch kernel for 3 <= M <= 32 (measured on MI355X): the MFMA GEMV
+// with a per-workgroup K split (mmvq.hip) up to M = 16; above it the
+// workgroup-shared activation tile of mmq_skinny.hip reads fewer bytes per
+// weight byte.  IFX_DECODE=skinny|mmvq forces one (tuning; read once).
+bool use_skinny(int M) {
+  static const int v = [] {
+    const char *e = getenv("IFX_DECODE");
+    return e ? (e[0] == 's' ? 1 : e[0] == 'm' ? 2 : 0) : 0;
+  }();
+  return v == 1 || (v == 0 && M > 16);
+}
 
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
 
@@ -105,7 +133,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
-  if (M <= kMaxGemvM || K % 256 != 0) return 1;
+  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   return M <= kMaxSkinnyM ? 2 : 3;
 }
 
@@ -129,10 +157,13 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (M <= kMaxGemvM || K % 256 != 0)
+  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
-  if (M <= kMaxSkinnyM)
-    return status_of(ifx::launch_mmq_skinny(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  if (M <= kMaxSkinnyM) {
+    if (use_skinny(M) && K % 256 == 0)
+      return status_of(ifx::launch_mmq_skinny(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+    return status_of(ifx::launch_mmvq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  }
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
 }
 
@@ -149,9 +180,12 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (M <= kMaxGemvM || K % 256 != 0)
+  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
         ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
+  if (M <= kMaxSkinnyM && !(use_skinny(M) && K % 256 == 0))
+    return status_of(ifx::launch_mmvq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                      mode, s));
   // batched decode and prefill: one launch per projection (each fills the chip)
   for (int i = 0; i < count; ++i) {
     const int rc = ifx_qgemv(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],

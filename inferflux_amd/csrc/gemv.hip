@@ -47,8 +47,8 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
   const uint32_t wo = b * kQ4KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    hdr[r] = bload<u32x4>(Wr, wo, rows[r]);
-    q[r] = bload<u32x4>(Wr, wo + 16 + 16 * j, rows[r]);
+    hdr[r] = wload<u32x4>(Wr, wo, rows[r]);
+    q[r] = wload<u32x4>(Wr, wo + 16 + 16 * j, rows[r]);
   }
   // activations: Q8_1 blocks (b*8 + 2p) and (b*8 + 2p + 1), bytes 16h..16h+15
   i32x4 xa[MC], xb[MC];
@@ -121,10 +121,10 @@ __device__ __forceinline__ void q6k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
   const uint32_t wo = b * kQ6KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    ql[r] = bload<u32x4>(Wr, wo + g * 64 + cc * 32 + 16 * h, rows[r]);
-    qh[r] = bload<u32x4>(Wr, wo + 128 + g * 32 + 16 * h, rows[r]);
-    scw[r] = bload<u32x2>(Wr, wo + 192 + g * 8, rows[r]);
-    dbits[r] = bload<uint16_t>(Wr, wo + 208, rows[r]);
+    ql[r] = wload<u32x4>(Wr, wo + g * 64 + cc * 32 + 16 * h, rows[r]);
+    qh[r] = wload<u32x4>(Wr, wo + 128 + g * 32 + 16 * h, rows[r]);
+    scw[r] = wload<u32x2>(Wr, wo + 192 + g * 8, rows[r]);
+    dbits[r] = wload<uint16_t>(Wr, wo + 208, rows[r]);
   }
   i32x4 xa[MC], xb[MC];
   float da[MC], db[MC];
@@ -195,9 +195,9 @@ __device__ __forceinline__ void q8_0_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t 
   const uint32_t wo = s * kQ8_0Bytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    dbits[r] = bload<uint16_t>(Wr, wo, rows[r]);
-    w0[r] = bload<i32x4>(Wr, wo + 2, rows[r]);
-    w1[r] = bload<i32x4>(Wr, wo + 18, rows[r]);
+    dbits[r] = wload<uint16_t>(Wr, wo, rows[r]);
+    w0[r] = wload<i32x4>(Wr, wo + 2, rows[r]);
+    w1[r] = wload<i32x4>(Wr, wo + 18, rows[r]);
   }
   i32x4 x0[MC], x1[MC];
   float da[MC];

@@ -90,6 +90,22 @@ __device__ __forceinline__ T bload(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
 }
 
+// Cache policy of the weight-stream loads (buffer instruction aux bits).
+#ifndef IFX_WAUX
+#define IFX_WAUX 0
+#endif
+template <typename T>
+__device__ __forceinline__ T wload(rsrc_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 16)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, IFX_WAUX));
+  else if constexpr (sizeof(T) == 8)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, IFX_WAUX));
+  else if constexpr (sizeof(T) == 4)
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, IFX_WAUX));
+  else
+    return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, IFX_WAUX));
+}
+
 // Signed int8x4 dot product with int32 accumulate: v_dot4_i32_i8.
 __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);

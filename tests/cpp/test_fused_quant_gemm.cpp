@@ -169,7 +169,8 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 8, 11008, 2048) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kTiledMfma);
-  EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 40, 64, 2080) == KernelFamily::kGemv);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 1, 64, 100) == KernelFamily::kNone);
   EXPECT(std::string(FusedQuantGemm::KernelFamilyName(KernelFamily::kTiledMfma)) ==
          "tiled int8 MFMA");
