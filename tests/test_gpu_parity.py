@@ -212,6 +212,13 @@ def _sampled(orc, dev, qtype, M, N, K, seed, outl=0.0, rows=256):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0])
+def test_gemm_large_tiles(orc, dev, qtype):
+    """A grid of >= 512 128x128 tiles takes the large-tile GEMM (the small
+    parity cases above all run 64x64 tiles); ragged M and N edges."""
+    _sampled(orc, dev, qtype, 1000, 8190, 512, seed=21, outl=0.01, rows=128)
+
+
 @pytest.mark.parametrize("M", [1, 8])
 def test_config1_q4k_gemv(orc, dev, M):
     _sampled(orc, dev, Q4_K, M, 11008, 2048, seed=0, rows=11008)
