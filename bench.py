@@ -1,18 +1,24 @@
 """Benchmark of the quantized GEMV/GEMM path on one MI355X.
 
 Workload: one Qwen2.5-3B Q4_K_M decode layer through
-the quantized path -- Q8_1 quantize of the layer input, QKV / O / gate / up
-Q4_K GEMVs, Q8_1 quantize of the FFN activation, Q6_K down GEMV -- at
-M = 1 (the unified decode batch size of the headline).  A step is one such
-layer.  Weights rotate through replicas totalling >= 512 MB so every step
-streams from HBM, not the 256 MB Infinity Cache.
+the quantized path, launched as the reference's forward pass launches it
+(inferflux_amd/workloads.py DECODE_LAUNCHES): Q8_1 quantize of the four
+activation inputs, one grouped Q/K/V GEMV, O accumulated into an fp32
+residual, one grouped gate/up GEMV, the Q6_K down projection accumulated
+into the residual.  A step is one such layer at M = 1 (the unified decode
+batch of the headline).  Weights rotate through replicas totalling >= 512
+MB so every step streams from HBM, not the 256 MB Infinity Cache.
 
 Headline `value`: HBM GB/s of the layer's Q4_K GEMVs at M = 1 (algorithmic
 bytes: weights + Q8_1 activations + fp32 outputs, each counted once, over
 the summed kernel time).  The JSON line also carries the roofline of the
-dominant kernel (the 11008 x 2048 Q4_K GEMV), us per layer at M = 1/4/8,
-the other configs (config 1 at M = 1/8, LM head, 14B layer at M = 16/32,
-32B prefill GEMMs) and a CPU baseline timed on this host.
+dominant kernel (the grouped gate/up Q4_K GEMV, 2 x 11008 x 2048), us per
+layer at M = 1/4/8, an HBM read probe at the same transfer size, the other
+configs (config 1 at M = 1/8, LM head, 14B layer at M = 16/32, 32B prefill
+GEMMs) and a CPU baseline timed on this host.
+
+`python bench.py --profile` runs only the dominant kernel and the counter
+calibration kernels, for rocprofv3.
 """
 import argparse
 import json
@@ -28,8 +34,9 @@ INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE), each scaled by what the counter reads for a copy
-# of exactly 64 MiB; summary and commands in profiles/k_gemv_q4k_11008x2048_m1.md.
-DOMINANT_TRAFFIC_BYTES = 12785755
+# of exactly 64 MiB; the summary and commands are in
+# profiles/k_gemv_q4k_gate_up_2x11008x2048_m1.md.
+DOMINANT_TRAFFIC_BYTES = 25510080
 
 
 def parse():
@@ -44,6 +51,12 @@ def parse():
                    help="profiling run: only the dominant GEMV (eager launches), the HBM "
                         "read probe and a copy of known size for counter calibration")
     return p.parse_args()
+
+
+def gemv_bytes(ops, qt, M, Ns, K):
+    """Algorithmic bytes of one launch: weights, one read of the Q8_1
+    activations, fp32 outputs."""
+    return sum(ops.weight_bytes(qt, N, K) for N in Ns) + M * (K // 32) * 36 + M * sum(Ns) * 4
 
 
 def main():
@@ -69,12 +82,11 @@ def main():
 
     # ------------------------------------------------------------ inputs
     def make_layer(projs, seed, replicas):
-        """Per projection: list of replicated device weight tensors."""
-        out = []
+        """name -> (quant type, N, K, [replicated device weight tensors])."""
+        out = {}
         for i, (name, qt, N, K) in enumerate(projs):
             w = torch.from_numpy(synth.blocks(qt, N, K, seed=seed * 100 + i)).to(dev)
-            reps = [w] + [w.clone() for _ in range(replicas - 1)]
-            out.append((name, qt, N, K, reps))
+            out[name] = (qt, N, K, [w] + [w.clone() for _ in range(replicas - 1)])
         return out
 
     def layer_bytes(projs):
@@ -86,7 +98,9 @@ def main():
     def time_loop(fn, steps, warmup):
         """us per fn call.  The calls are captured once into a HIP graph
         (fn(0) .. fn(steps-1), so weight replicas rotate) and the graph is
-        replayed, so host launch latency does not leave the GPU idle."""
+        replayed, so host launch latency does not leave the GPU idle.  The
+        events are recorded on torch's current stream, the stream every
+        kernel here is launched on."""
         for i in range(min(warmup, 3)):
             fn(i)  # eager first calls: one-time kernel attribute set-up
         torch.cuda.synchronize()
@@ -107,31 +121,40 @@ def main():
         return a.elapsed_time(b) * 1e3 / steps  # us per call
 
     def decode_layer_runner(layer, M, seed):
-        """One decode layer at batch M: 4 quantizes + 5 GEMVs."""
-        hidden = layer[0][3]
-        ffn = layer[2][2]
-        xs = {k: torch.from_numpy(synth.activations(M, K, seed=seed + j, outlier_frac=0.0)).to(dev)
-              for j, (k, K) in enumerate((("in", hidden), ("o", layer[1][3]),
-                                          ("ffn", hidden), ("down", ffn)))}
-        A = {k: torch.empty((M, v.shape[1] // 32 * 36), dtype=torch.uint8, device=dev)
-             for k, v in xs.items()}
-        Y = {name: torch.empty((M, N), dtype=torch.float32, device=dev)
-             for name, _, N, _, _ in layer}
-        src = {"qkv": "in", "o": "o", "gate": "ffn", "up": "ffn", "down": "down"}
-        R = len(layer[0][4])
+        """One decode layer at batch M: 4 quantizes + 4 GEMV launches."""
+        K_of = {"attn_in": layer["q"][2], "attn_out": layer["o"][2],
+                "ffn_in": layer["gate"][2], "ffn_act": layer["down"][2]}
+        xs = {k: torch.from_numpy(synth.activations(M, K, seed=seed + j)).to(dev)
+              for j, (k, K) in enumerate(K_of.items())}
+        A = {k: torch.empty((M, K // 32 * 36), dtype=torch.uint8, device=dev)
+             for k, K in K_of.items()}
+        Y = {name: torch.zeros((M, v[1]), dtype=torch.float32, device=dev)
+             for name, v in layer.items()}
+        R = len(layer["q"][3])
 
         def run(i, which=None):
             r = i % R
-            for k in ("in", "o", "ffn", "down"):
-                if which is None or which == "quant":
+            if which is None or which == "quant":
+                for k in K_of:
                     ops.quantize_q8_1(xs[k], out=A[k])
-            for name, qt, N, K, reps in layer:
-                if which is None or which == name:
-                    ops.qgemv(qt, reps[r], A[src[name]], M, N, K, out=Y[name])
+            for lname, projs, src, accum in workloads.DECODE_LAUNCHES:
+                if which is not None and which != lname:
+                    continue
+                qt, _, K, _ = layer[projs[0]]
+                mode = ops.ACCUM if accum else ops.STORE
+                if len(projs) == 1:
+                    p = layer[projs[0]]
+                    ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode)
+                else:
+                    ops.qgemv_grouped(qt, [layer[p][3][r] for p in projs], A[src], M,
+                                      [layer[p][1] for p in projs], K,
+                                      outs=[Y[p] for p in projs], mode=mode)
         return run
 
-    def gemv_bytes(qt, M, N, K):
-        return ops.weight_bytes(qt, N, K) + M * (K // 32) * 36 + M * N * 4
+    def launch_bytes(layer, lname, M):
+        projs = dict((l[0], l[1]) for l in workloads.DECODE_LAUNCHES)[lname]
+        qt, _, K, _ = layer[projs[0]]
+        return qt, gemv_bytes(ops, qt, M, [layer[p][1] for p in projs], K)
 
     result = {}
     extras = {}
@@ -140,7 +163,6 @@ def main():
     projs3b = workloads.QWEN3B_LAYER
     R3 = n_replicas(layer_bytes(projs3b))
     layer3b = make_layer(projs3b, seed=1, replicas=R3)
-    q4k_names = [p[0] for p in projs3b if p[1] == ops.Q4_K]
     per_m = {}
     for M in (1, 4, 8):
         run = decode_layer_runner(layer3b, M, seed=10 + M)
@@ -148,19 +170,20 @@ def main():
         # whole layer: `steps` layers captured in one graph, replayed between
         # synchronisations (the K timed steps of the contract)
         us_layer = time_loop(run, steps, args.warmup)
-        # each kernel alone (same rotation), for per-kernel GB/s
-        kern = {}
-        for name, qt, N, K, _ in layer3b:
-            kern[name] = time_loop(lambda i, n=name: run(i, n), steps, args.warmup)
-        kern["quant"] = time_loop(lambda i: run(i, "quant"), steps, args.warmup)
-        q4_bytes = sum(gemv_bytes(qt, M, N, K) for name, qt, N, K, _ in layer3b if qt == ops.Q4_K)
-        q4_us = sum(kern[n] for n in q4k_names)
-        all_bytes = sum(gemv_bytes(qt, M, N, K) for _, qt, N, K, _ in layer3b)
+        # each launch alone (same rotation), for per-kernel GB/s
+        kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, args.warmup)
+                for l in workloads.DECODE_LAUNCHES}
+        kern["quant_x4"] = time_loop(lambda i: run(i, "quant"), steps, args.warmup)
+        q4 = [l[0] for l in workloads.DECODE_LAUNCHES if launch_bytes(layer3b, l[0], M)[0] == ops.Q4_K]
+        q4_bytes = sum(launch_bytes(layer3b, n, M)[1] for n in q4)
+        q4_us = sum(kern[n] for n in q4)
+        all_bytes = sum(launch_bytes(layer3b, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
+        gemv_us = sum(kern[l[0]] for l in workloads.DECODE_LAUNCHES)
         per_m[M] = {
             "us_per_layer": round(us_layer, 2),
             "us_sum_kernels": round(sum(kern.values()), 2),
             "q4k_gemv_GBs": round(q4_bytes / q4_us / 1e3, 1),
-            "layer_gemv_GBs": round(all_bytes / sum(kern[n] for n, *_ in layer3b) / 1e3, 1),
+            "layer_gemv_GBs": round(all_bytes / gemv_us / 1e3, 1),
             "kernel_us": {k: round(v, 2) for k, v in kern.items()},
             "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_layer * 1e-6), 1),
         }
@@ -170,23 +193,41 @@ def main():
     extras["qwen3b_layer"] = per_m
 
     # --------------------------------------- dominant kernel: roofline
-    # the 11008 x 2048 Q4_K GEMV (gate), M = 1: events around back-to-back
-    # launches on the stream the kernel runs on (torch's current stream)
-    name, qt, N, K, reps = layer3b[2]
+    # the grouped gate/up Q4_K GEMV (2 x 11008 x 2048), M = 1: events
+    # around graph-replayed launches on the stream the kernel runs on
     M = 1
+    qt, N, K, _ = layer3b["gate"]
     x = torch.from_numpy(synth.activations(M, K, seed=0)).to(dev)
     A1 = ops.quantize_q8_1(x)
-    Y1 = torch.empty((M, N), dtype=torch.float32, device=dev)
-    dom_us = time_loop(lambda i: ops.qgemv(qt, reps[i % len(reps)], A1, M, N, K, out=Y1),
+    Yg = [torch.empty((M, N), dtype=torch.float32, device=dev) for _ in range(2)]
+    gate, up = layer3b["gate"][3], layer3b["up"][3]
+    dom_us = time_loop(lambda i: ops.qgemv_grouped(qt, [gate[i % R3], up[i % R3]], A1, M, [N, N],
+                                                   K, outs=Yg),
                        max(args.steps, 200), args.warmup)
-    dom_bytes = gemv_bytes(qt, M, N, K)
+    dom_bytes = gemv_bytes(ops, qt, M, [N, N], K)
     achieved = dom_bytes / dom_us / 1e3
     result["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
-        "kernel": f"k_gemv<Q4_K,MC=1> N={N} K={K} M=1", "bytes_per_launch": dom_bytes,
-        "us_per_launch": round(dom_us, 3),
+        "kernel": "k_gemv<Q4_K,MC=1,R=2> grouped gate+up, N=2x11008 K=2048 M=1",
+        "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3),
     }
+    # what a plain streaming read of the same number of bytes achieves
+    # (the size-dependent ceiling: launch ramp and drain are fixed costs)
+    probe = probe_lib()
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    wbytes = gate[0].numel() * 2
+    big = torch.empty(max(ROTATE_BYTES * 2, 8 * wbytes), dtype=torch.uint8, device=dev)
+    nrot = big.numel() // wbytes
+
+    def probe_step(i, nbytes=wbytes):
+        off = (i % nrot) * nbytes
+        rc = probe.ifx_probe_read(big.data_ptr() + off, nbytes, sink.data_ptr(), 1 << 20,
+                                  torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    p_us = time_loop(probe_step, 200, 10)
+    result["roofline"]["read_probe_same_bytes_GBs"] = round(wbytes / p_us / 1e3, 1)
+    del big
     del layer3b
     torch.cuda.empty_cache()
 
@@ -201,7 +242,7 @@ def main():
             Y = torch.empty((M, N), dtype=torch.float32, device=dev)
             us = time_loop(lambda i: ops.qgemv(qt, reps[i % len(reps)], A, M, N, K, out=Y),
                            max(args.steps, 200), args.warmup)
-            gb = gemv_bytes(qt, M, N, K) / us / 1e3
+            gb = gemv_bytes(ops, qt, M, [N], K) / us / 1e3
             c1[f"M{M}"] = {"us": round(us, 3), "GBs": round(gb, 1),
                            "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
         extras["config1_q4k_11008x2048"] = c1
@@ -219,7 +260,7 @@ def main():
                 Y = torch.empty((M, N), dtype=torch.float32, device=dev)
                 us = time_loop(lambda i: ops.qgemv(qt, reps[i % 2], A, M, N, K, out=Y),
                                max(20, args.steps // 4), 5)
-                gb = gemv_bytes(qt, M, N, K) / us / 1e3
+                gb = gemv_bytes(ops, qt, M, [N], K) / us / 1e3
                 c3[f"{key}_M{M}"] = {"us": round(us, 2), "GBs": round(gb, 1),
                                      "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
             del reps, w
@@ -232,14 +273,15 @@ def main():
         c4 = {}
         for M in (16, 32):
             run = decode_layer_runner(layer14, M, seed=40 + M)
-            us_layer = time_loop(run, max(20, args.steps // 4), 5)
-            kern = {}
-            for name, qt, N, K, _ in layer14:
-                kern[name] = time_loop(lambda i, n=name: run(i, n), max(20, args.steps // 4), 5)
-            all_bytes = sum(gemv_bytes(qt, M, N, K) for _, qt, N, K, _ in layer14)
+            steps = max(20, args.steps // 4)
+            us_layer = time_loop(run, steps, 5)
+            kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
+                    for l in workloads.DECODE_LAUNCHES}
+            all_bytes = sum(launch_bytes(layer14, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
             c4[f"M{M}"] = {
                 "us_per_layer": round(us_layer, 2),
                 "layer_GBs": round(all_bytes / us_layer / 1e3, 1),
+                "gemv_GBs": round(all_bytes / sum(kern.values()) / 1e3, 1),
                 "kernel_us": {k: round(v, 2) for k, v in kern.items()},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN14B_LAYERS * us_layer * 1e-6), 1),
             }
@@ -285,7 +327,8 @@ def main():
         "data": "synthetic (seeded GGUF blocks, N(0,1) activations)",
         "config": {"workload": "qwen2.5-3b Q4_K_M decode layer, M=1 (BASELINE config 2)",
                    "M": 1, "hidden": 2048, "ffn": 11008, "weight_replicas": R3,
-                   "value_is": "HBM GB/s of the layer's Q4_K GEMVs (QKV, O, gate, up)",
+                   "launches": [l[0] for l in workloads.DECODE_LAUNCHES],
+                   "value_is": "HBM GB/s of the layer's Q4_K GEMV launches (QKV, O, gate+up)",
                    "frac_of_hbm_peak": round(headline / HBM_PEAK_GBS, 4)},
         "roofline": result["roofline"],
         "cpu_baseline": cpu,
@@ -308,29 +351,31 @@ def probe_lib():
 
 def profile_run(args, dev):
     """Eager launches for rocprofv3: `steps` launches of the dominant GEMV
-    (Q4_K 11008 x 2048, M = 1, rotating weight replicas), 20 copies of
-    exactly 64 MiB (k_probe_copy: FETCH_SIZE and WRITE_SIZE per dispatch of
-    a known 64 MiB read and 64 MiB write calibrate the counters), and 20
-    streaming reads of the GEMV's weight bytes (k_probe_read: the HBM read
-    rate at this transfer size).  Prints one JSON line of event timings."""
+    (the grouped gate/up Q4_K GEMV, 2 x 11008 x 2048, M = 1, rotating weight
+    replicas), 20 copies of exactly 64 MiB (k_probe_copy: FETCH_SIZE and
+    WRITE_SIZE per dispatch of a known 64 MiB read and 64 MiB write
+    calibrate the counters), and 20 streaming reads of the dominant
+    launch's weight bytes (k_probe_read: the HBM read rate at this size).
+    Prints one JSON line of event timings."""
     import torch
 
     from inferflux_amd import ops, synth
 
     stream = torch.cuda.current_stream()
     qt, N, K = ops.Q4_K, 11008, 2048
-    w = torch.from_numpy(synth.blocks(qt, N, K, seed=0)).to(dev)
-    R = max(2, -(-ROTATE_BYTES // w.numel()))
-    reps = [w] + [w.clone() for _ in range(R - 1)]
+    g = torch.from_numpy(synth.blocks(qt, N, K, seed=0)).to(dev)
+    u = torch.from_numpy(synth.blocks(qt, N, K, seed=1)).to(dev)
+    R = max(2, -(-ROTATE_BYTES // (2 * g.numel())))
+    reps = [(g, u)] + [(g.clone(), u.clone()) for _ in range(R - 1)]
     A = ops.quantize_q8_1(torch.from_numpy(synth.activations(1, K, seed=0)).to(dev))
-    Y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    Y = [torch.empty((1, N), dtype=torch.float32, device=dev) for _ in range(2)]
     for i in range(args.warmup):
-        ops.qgemv(qt, reps[i % R], A, 1, N, K, out=Y)
+        ops.qgemv_grouped(qt, list(reps[i % R]), A, 1, [N, N], K, outs=Y)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(stream)
     for i in range(args.steps):
-        ops.qgemv(qt, reps[i % R], A, 1, N, K, out=Y)
+        ops.qgemv_grouped(qt, list(reps[i % R]), A, 1, [N, N], K, outs=Y)
     b.record(stream)
     torch.cuda.synchronize()
     gemv_us = a.elapsed_time(b) * 1e3 / args.steps
@@ -342,11 +387,13 @@ def profile_run(args, dev):
     sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
     for _ in range(20):
         assert lib.ifx_probe_copy(dst.data_ptr(), big.data_ptr(), big.numel(), 8192, sp) == 0
-    nbytes = w.numel()
+    nbytes = g.numel()
     for i in range(20):
-        assert lib.ifx_probe_read(reps[i % R].data_ptr(), nbytes, sink.data_ptr(), 16384, sp) == 0
+        assert lib.ifx_probe_read(reps[i % R][0].data_ptr(), nbytes, sink.data_ptr(), 1 << 20,
+                                  sp) == 0
     torch.cuda.synchronize()
-    print(json.dumps({"profile": "dominant gemv", "kernel": "k_gemv Q4_K N=11008 K=2048 M=1",
+    print(json.dumps({"profile": "dominant gemv",
+                      "kernel": "k_gemv Q4_K grouped gate+up N=2x11008 K=2048 M=1",
                       "launches": args.steps, "event_us_per_launch": round(gemv_us, 3),
                       "copy_bytes": big.numel(), "read_probe_bytes": nbytes}), flush=True)
 

@@ -9,15 +9,31 @@ SINGLE_Q4K = [("gate", Q4_K, 11008, 2048)]
 
 
 def decode_layer(hidden, q_heads, kv_heads, head_dim, ffn):
-    """Q4_K_M decode layer: QKV, O, gate, up in Q4_K; down in Q6_K."""
-    qkv = (q_heads + 2 * kv_heads) * head_dim
+    """Q4_K_M decode layer: Q, K, V, O, gate, up in Q4_K; down in Q6_K."""
     return [
-        ("qkv", Q4_K, qkv, hidden),
+        ("q", Q4_K, q_heads * head_dim, hidden),
+        ("k", Q4_K, kv_heads * head_dim, hidden),
+        ("v", Q4_K, kv_heads * head_dim, hidden),
         ("o", Q4_K, hidden, q_heads * head_dim),
         ("gate", Q4_K, ffn, hidden),
         ("up", Q4_K, ffn, hidden),
         ("down", Q6_K, hidden, ffn),
     ]
+
+
+# The launches of a decode layer, as the reference's forward pass issues
+# them (runtime/backends/cuda/native/transformer_forward.cu:474-980): one
+# grouped Q8_1 GEMV for Q/K/V (GemvQ8_1Triple, :542) over the quantized
+# attention-norm output, O accumulated into the fp32 residual
+# (GemvQ8_1AccumF32, :726), one grouped launch for gate/up (GemvQ8_1Pair,
+# :559) and down accumulated into the residual (:817).
+# (launch name, projections, activation input, accumulate into Y)
+DECODE_LAUNCHES = [
+    ("qkv", ("q", "k", "v"), "attn_in", False),
+    ("o", ("o",), "attn_out", True),
+    ("gate_up", ("gate", "up"), "ffn_in", False),
+    ("down", ("down",), "ffn_act", True),
+]
 
 
 # Config 2: Qwen2.5-3B layer (hidden 2048, 16/2 heads x 128, FFN 11008), M = 1, 4, 8.
