@@ -62,8 +62,8 @@ def gemv_bytes(ops, qt, M, Ns, K):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only; the path shards by weight rows "
-              "(see DESIGN.md) and no multi-GPU figure is produced", file=sys.stderr)
+        print("bench.py: this build measures one GPU only; the path would shard by weight rows "
+              "and no multi-GPU figure is produced", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -22,8 +22,10 @@
 //  * Rows past N are clamped (loaded but never stored), so no branch
 //    separates a lane's loads.
 //  * Partial sums acc[R*MC] are combined across the 64 lanes of a wave with
-//    a reduce-scatter butterfly (one shuffle per value per halving step),
-//    then across the G waves of the group through LDS.
+//    DPP adds (no LDS traffic; lane 63 ends with the totals), then across
+//    the G waves of the group through LDS.
+//  * Q4_K: the 16-byte super-block header is loaded by one of the eight
+//    lanes that share it and broadcast to the others with DPP.
 #include "ifx_common.h"
 
 #include <stdlib.h>
@@ -47,7 +49,10 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
   const uint32_t wo = b * kQ4KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    hdr[r] = wload<u32x4>(Wr, wo, rows[r]);
+    // the 16-byte header is loaded by one lane of the eight that share the
+    // super-block (lane & 7 == 0, i.e. j == 0) and broadcast to the others
+    hdr[r] = u32x4{0, 0, 0, 0};
+    if (j == 0) hdr[r] = wload<u32x4>(Wr, wo, rows[r]);
     q[r] = wload<u32x4>(Wr, wo + 16 + 16 * j, rows[r]);
   }
   // activations: Q8_1 blocks (b*8 + 2p) and (b*8 + 2p + 1), bytes 16h..16h+15
@@ -57,10 +62,16 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
   for (int c = 0; c < MC; ++c) {
     if (c < mvalid) {
       const uint32_t ao = (b * 8 + 2 * p) * kQ8_1Bytes;
+#ifdef IFX_EXP_NOA
+      const uint32_t dsa = 0x3C003C00u ^ ao, dsb = 0x3C003C00u ^ (ao << 3);
+      xa[c] = i32x4{static_cast<int>(ao), s, 3, 5};
+      xb[c] = i32x4{s, static_cast<int>(ao), 7, 1};
+#else
       const uint32_t dsa = bload<uint32_t>(Ar, ao, c * a_row);
       const uint32_t dsb = bload<uint32_t>(Ar, ao + kQ8_1Bytes, c * a_row);
       xa[c] = bload<i32x4>(Ar, ao + 4 + 16 * h, c * a_row);
       xb[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 4 + 16 * h, c * a_row);
+#endif
       da[c] = h2f(dsa & 0xFFFFu);
       db[c] = h2f(dsb & 0xFFFFu);
       // the min term is per 32-value sub-block: only the h == 0 lane adds it
@@ -72,6 +83,9 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
     }
   }
   const int shift = 8 * ((2 * p) & 3);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    hdr[r] = u32x4{bcast8(hdr[r].x), bcast8(hdr[r].y), bcast8(hdr[r].z), bcast8(hdr[r].w)};
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float d = h2f(hdr[r].x & 0xFFFFu);
@@ -300,53 +314,48 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       q8_0_slice<MC, R>(Wr, Ar, rows, a_row, mvalid, s, acc);
   }
 
-  // Reduce-scatter over the wave: after the step with lane offset o and
-  // length L, a lane with (lane & o) keeps the upper half of the values.
+  // Sum each partial over the wave (DPP adds, no LDS); lane 63 ends with
+  // all V totals, then across the G waves of the row group through LDS.
   float v[V];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int c = 0; c < MC; ++c) v[r * MC + c] = acc[r][c];
-  int o = 32;
-#pragma unroll
-  for (int L = V; L > 1; L >>= 1, o >>= 1) {
-    const bool up = (lane & o) != 0;
-#pragma unroll
-    for (int i = 0; i < L / 2; ++i) {
-      const float send = up ? v[i] : v[i + L / 2];
-      const float keep = up ? v[i + L / 2] : v[i];
-      v[i] = keep + __shfl_xor(send, o);
-    }
-  }
-  for (; o >= 1; o >>= 1) v[0] += __shfl_xor(v[0], o);
-  // Lane bits 5, 4, ... (high first) now spell the index of the value kept.
-  constexpr int kLowBits = 6 - __builtin_ctz(V);
-  const bool holder = (lane & ((1 << kLowBits) - 1)) == 0;
-  const int idx = lane >> kLowBits;
-  float y = v[0];
+    for (int c = 0; c < MC; ++c) v[r * MC + c] = wave_sum_to63(acc[r][c]);
   if constexpr (G > 1) {
-    if (holder) red[(grp * G + gw) * V + idx] = y;
-    __syncthreads();
-    if (gw != 0 || !holder) return;
+    if (lane == 63) {
 #pragma unroll
-    for (int w = 1; w < G; ++w) y += red[(grp * G + w) * V + idx];
+      for (int i = 0; i < V; ++i) red[(grp * G + gw) * V + i] = v[i];
+    }
+    __syncthreads();
+    if (gw != 0 || lane != 63) return;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < G; ++w) t += red[(grp * G + w) * V + i];
+      v[i] = t;
+    }
   } else {
-    if (!holder) return;
+    if (lane != 63) return;
   }
-  const int r = idx / MC, c = idx % MC;
-  const int row = row0 + r;
-  if (row >= N || c >= mvalid) return;
-  const int64_t o_idx = static_cast<int64_t>(col0 + c) * N + row;
-  if constexpr (F16OUT) {
-    uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
-    if (mode == kOutAccum) y += h2f(Yh[o_idx]);
-    else if (mode == kOutBias) y += h2f(static_cast<const uint16_t *>(sg.bias)[row]);
-    Yh[o_idx] = static_cast<uint16_t>(f2h_bits(y));
-  } else {
-    float *Yf = static_cast<float *>(sg.Y);
-    if (mode == kOutAccum) y += Yf[o_idx];
-    else if (mode == kOutBias) y += static_cast<const float *>(sg.bias)[row];
-    Yf[o_idx] = y;
+#pragma unroll
+  for (int idx = 0; idx < V; ++idx) {
+    float y = v[idx];
+    const int r = idx / MC, c = idx % MC;
+    const int row = row0 + r;
+    if (row >= N || c >= mvalid) continue;
+    const int64_t o_idx = static_cast<int64_t>(col0 + c) * N + row;
+    if constexpr (F16OUT) {
+      uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
+      if (mode == kOutAccum) y += h2f(Yh[o_idx]);
+      else if (mode == kOutBias) y += h2f(static_cast<const uint16_t *>(sg.bias)[row]);
+      Yh[o_idx] = static_cast<uint16_t>(f2h_bits(y));
+    } else {
+      float *Yf = static_cast<float *>(sg.Y);
+      if (mode == kOutAccum) y += Yf[o_idx];
+      else if (mode == kOutBias) y += static_cast<const float *>(sg.bias)[row];
+      Yf[o_idx] = y;
+    }
   }
 }
 

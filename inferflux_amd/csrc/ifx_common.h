@@ -106,6 +106,38 @@ __device__ __forceinline__ T wload(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, IFX_WAUX));
 }
 
+// DPP lane moves (VALU, no LDS): `old` is kept where the row/bank mask
+// disables the move.
+template <int CTRL, int ROWS = 0xF, int BANKS = 0xF>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      static_cast<int>(old), static_cast<int>(v), CTRL, ROWS, BANKS, false));
+}
+template <int CTRL, int ROWS = 0xF, int BANKS = 0xF>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, dpp<CTRL, ROWS, BANKS>(0u, __builtin_bit_cast(uint32_t, v)));
+}
+
+// Sum over the 64 lanes of a wave with DPP adds; the total is exact in lane
+// 63 (other lanes hold partial sums): quad swaps, half-row and row mirrors,
+// then row 15 -> rows 1 and 3, lane 31 -> rows 2 and 3.
+__device__ __forceinline__ float wave_sum_to63(float v) {
+  v += dppf<0xB1>(v);         // quad_perm [1,0,3,2]
+  v += dppf<0x4E>(v);         // quad_perm [2,3,0,1]
+  v += dppf<0x141>(v);        // row_half_mirror
+  v += dppf<0x140>(v);        // row_mirror
+  v += dppf<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+  v += dppf<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// Lane 8k's value in lanes 8k .. 8k+7 (row_newbcast of lanes 0 and 8 of
+// each 16-lane row into banks 0-1 and 2-3).
+__device__ __forceinline__ uint32_t bcast8(uint32_t v) {
+  uint32_t x = dpp<0x150, 0xF, 0x3>(0u, v);
+  return dpp<0x158, 0xF, 0xC>(x, v);
+}
+
 // Signed int8x4 dot product with int32 accumulate: v_dot4_i32_i8.
 __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
