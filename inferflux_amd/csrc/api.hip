@@ -25,8 +25,9 @@ hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void 
 hipError_t launch_mmvq(int qtype, int count, const void *const *W, void *const *Y,
                        const int *N, const void *bias, const void *A, bool f16, int M, int K,
                        int mode, hipStream_t stream);
-hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, const void *bias,
-                             bool f16, int M, int N, int K, int mode, hipStream_t stream);
+hipError_t launch_mmq_skinny(int qtype, int count, const void *const *W, void *const *Y,
+                             const int *N, const void *bias, const void *A, bool f16, int M,
+                             int K, int mode, hipStream_t stream);
 hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
                             bool f16, int M, int N, int K, int mode, hipStream_t stream);
 }  // namespace ifx
@@ -161,7 +162,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
-      return status_of(ifx::launch_mmq_skinny(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+      return status_of(
+          ifx::launch_mmq_skinny(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
     return status_of(ifx::launch_mmvq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   }
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
@@ -183,9 +185,13 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
         ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
-  if (M <= kMaxSkinnyM && !(use_skinny(M) && K % 256 == 0))
+  if (M <= kMaxSkinnyM) {
+    if (use_skinny(M) && K % 256 == 0)
+      return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16,
+                                              M, K, mode, s));
     return status_of(ifx::launch_mmvq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                       mode, s));
+  }
   // batched decode and prefill: one launch per projection (each fills the chip)
   for (int i = 0; i < count; ++i) {
     const int rc = ifx_qgemv(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],

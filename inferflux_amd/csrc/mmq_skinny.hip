@@ -174,28 +174,62 @@ __global__ __launch_bounds__(256) void k_fill_zero(float *__restrict__ y, int64_
   if (i < n) y[i] = 0.0f;
 }
 
-// grid: x = ceil(N / 64) row groups, y = super-block splits (sb_per ranges)
+// Up to three projections over the same activations (grouped launches):
+// workgroups [seg[i].blk_begin, seg[i + 1].blk_begin) belong to projection i.
+struct SkSeg {
+  const uint8_t *W;
+  void *Y;
+  const void *bias;
+  int N;
+  int blk_begin;
+};
+struct SkArgs {
+  SkSeg seg[3];
+  int nseg;
+  const uint8_t *A;
+  int M, K, mode, sb_per;
+};
+
+// Zeroes up to three fp32 outputs (the split-K kernel adds into them);
+// blockIdx.y selects the output.
+struct FillArgs {
+  float *y[3];
+  int64_t n[3];
+};
+__global__ __launch_bounds__(256) void k_fill_zero(const FillArgs f) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < f.n[blockIdx.y]) f.y[blockIdx.y][i] = 0.0f;
+}
+
+// grid: x = row groups of 64 (all projections), y = super-block splits.
+// Pipeline: the LDS stage is double-buffered and two super-blocks are in
+// flight in registers, so a step has one barrier and its loads were issued
+// two steps earlier.
 template <int QT, int MT, bool F16OUT, bool ATOMIC>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_mmq_skinny(const uint8_t *__restrict__ W,
-                                                               const uint8_t *__restrict__ A,
-                                                               void *__restrict__ Y,
-                                                               const void *__restrict__ bias,
-                                                               int M, int N, int K, int mode,
-                                                               int sb_per) {
+__global__ __launch_bounds__(64 * kWaves, 2) void k_mmq_skinny(const SkArgs args) {
   using S = Stage<QT, MT>;
   using F = WFmt<QT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int bx = blockIdx.x;
+  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+                 : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
+  const SkSeg &sg = args.seg[si];
+  const uint8_t *__restrict__ W = sg.W;
+  const uint8_t *__restrict__ A = args.A;
+  void *__restrict__ Y = sg.Y;
+  const void *__restrict__ bias = sg.bias;
+  const int N = sg.N, M = args.M, K = args.K, mode = args.mode, sb_per = args.sb_per;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int l16 = lane & 15, kq = lane >> 4;
-  const int n0 = (blockIdx.x * kWaves + wave) * 16;
+  const int n0 = ((bx - sg.blk_begin) * kWaves + wave) * 16;
   const int nblk = K >> 5;  // Q8_1 blocks per activation row
   const int nsb = K >> 8;   // super-blocks of 256 values
   const int sb0 = blockIdx.y * sb_per;
   const int sb1 = min(nsb, sb0 + sb_per);
-  uint8_t *as = smem;                                  // shared batch rows
-  uint8_t *ws = smem + S::kABytes + wave * S::kWBytes; // this wave's weight rows
+  // two stage buffers: shared batch rows, then each wave's weight rows
+  uint8_t *const buf[2] = {smem, smem + S::kBytes};
 
   const uint32_t w_row = static_cast<uint32_t>(QT == kTypeQ8_0 ? nblk * kQ8_0Bytes : nsb * F::kSbBytes);
   const uint32_t a_row = static_cast<uint32_t>(nblk) * kQ8_1Bytes;
@@ -209,14 +243,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_mmq_skinny(const uint8_t *__
 #pragma unroll
   for (int a = 0; a < MT; ++a) acc[a] = accm[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  StageRegs<QT, MT> rg;  // the next super-block's chunks, loaded a step ahead
-  if (sb0 < sb1) load_stage<QT, MT>(rg, so, Wr, Ar, sb0, lane, tid);
-  for (int sb = sb0; sb < sb1; ++sb) {
-    __syncthreads();  // previous super-block's LDS reads are done
-    store_stage<QT, MT>(as, ws, rg, lane, tid);
-    __syncthreads();
-    if (sb + 1 < sb1) load_stage<QT, MT>(rg, so, Wr, Ar, sb + 1, lane, tid);  // in flight below
-
+  // compute one super-block from the stage buffer at `as`
+  auto compute = [&](const uint8_t *as) {
+    const uint8_t *ws = as + S::kABytes + wave * S::kWBytes;
     // weight scales of this lane's column (row l16 of the n-tile)
     const uint8_t *row = ws + l16 * F::kPitch;
     float dsup = 0.0f;
@@ -317,6 +346,30 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_mmq_skinny(const uint8_t *__
       if constexpr (QT == kTypeQ8_0) acc[a] += P[a];
       else acc[a] += dsup * P[a];
     }
+    };
+
+  // r1 / r2: the two super-blocks in flight.  Before step s, super-block s
+  // is committed to buf[s & 1] (visible after the step's barrier), s + 1 is
+  // in one register set and s + 2 in the other, alternating.
+  StageRegs<QT, MT> r1, r2;
+  if (sb0 < sb1) {
+    load_stage<QT, MT>(r1, so, Wr, Ar, sb0, lane, tid);
+    if (sb0 + 1 < sb1) load_stage<QT, MT>(r2, so, Wr, Ar, sb0 + 1, lane, tid);
+    store_stage<QT, MT>(buf[0], buf[0] + S::kABytes + wave * S::kWBytes, r1, lane, tid);
+    if (sb0 + 2 < sb1) load_stage<QT, MT>(r1, so, Wr, Ar, sb0 + 2, lane, tid);
+  }
+  auto step = [&](int sb, int k, StageRegs<QT, MT> &rc) {
+    __syncthreads();  // buf[k] complete; buf[k ^ 1] no longer read
+    if (sb + 1 < sb1) {
+      uint8_t *b = buf[k ^ 1];
+      store_stage<QT, MT>(b, b + S::kABytes + wave * S::kWBytes, rc, lane, tid);
+      if (sb + 3 < sb1) load_stage<QT, MT>(rc, so, Wr, Ar, sb + 3, lane, tid);
+    }
+    compute(buf[k]);
+  };
+  for (int sb = sb0; sb < sb1; sb += 2) {
+    step(sb, 0, r2);
+    if (sb + 1 < sb1) step(sb + 1, 1, r1);
   }
 #pragma unroll
   for (int a = 0; a < MT; ++a) acc[a] -= accm[a];
@@ -365,52 +418,60 @@ int choose_splits(int row_groups, int nsb) {
 }
 
 template <int QT, int MT>
-hipError_t launch_mt(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16, int M,
-                     int N, int K, int mode, hipStream_t s) {
-  constexpr int shm = Stage<QT, MT>::kBytes;
-  const int groups = (N + 16 * kWaves - 1) / (16 * kWaves);
-  const int nsb = K >> 8;
+hipError_t launch_mt(SkArgs args, bool f16, hipStream_t s) {
+  constexpr int shm = 2 * Stage<QT, MT>::kBytes;
+  int groups = 0;
+  for (int i = 0; i < args.nseg; ++i) {
+    args.seg[i].blk_begin = groups;
+    groups += (args.seg[i].N + 16 * kWaves - 1) / (16 * kWaves);
+  }
+  const int nsb = args.K >> 8;
   int ks = f16 ? 1 : choose_splits(groups, nsb);
-  const int sb_per = (nsb + ks - 1) / ks;
-  ks = (nsb + sb_per - 1) / sb_per;
+  args.sb_per = (nsb + ks - 1) / ks;
+  ks = (nsb + args.sb_per - 1) / args.sb_per;
   const dim3 grid(groups, ks);
   if (f16) {
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, true, false>), grid, dim3(64 * kWaves), shm, s, W, A,
-                       Y, bias, M, N, K, mode, sb_per);
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, true, false>), grid, dim3(64 * kWaves), shm, s, args);
   } else if (ks == 1) {
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, false>), grid, dim3(64 * kWaves), shm, s, W, A,
-                       Y, bias, M, N, K, mode, sb_per);
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, false>), grid, dim3(64 * kWaves), shm, s, args);
   } else {
-    if (mode != 1) {  // store / bias: the splits add into a zeroed Y
-      const int64_t n = static_cast<int64_t>(M) * N;
-      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                         static_cast<float *>(Y), n);
+    if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
+      FillArgs f{};
+      int64_t nmax = 0;
+      for (int i = 0; i < args.nseg; ++i) {
+        f.y[i] = static_cast<float *>(args.seg[i].Y);
+        f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
+        nmax = max(nmax, f.n[i]);
+      }
+      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 255) / 256), args.nseg),
+                         dim3(256), 0, s, f);
     }
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, true>), grid, dim3(64 * kWaves), shm, s, W, A,
-                       Y, bias, M, N, K, mode, sb_per);
+    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, true>), grid, dim3(64 * kWaves), shm, s, args);
   }
   return hipGetLastError();
 }
 
 }  // namespace
 
-// Requires K % 256 == 0 and 1 <= M <= 32 (checked by the caller).
-hipError_t launch_mmq_skinny(int qtype, const void *W, const void *A, void *Y, const void *bias,
-                             bool f16, int M, int N, int K, int mode, hipStream_t stream) {
-  const uint8_t *w = static_cast<const uint8_t *>(W);
-  const uint8_t *a = static_cast<const uint8_t *>(A);
-  if (M > 32) return hipErrorInvalidValue;
+// Requires K % 256 == 0 and 1 <= M <= 32 (checked by the caller).  count
+// projections (1..3) of one quant type share A; bias only with count == 1.
+hipError_t launch_mmq_skinny(int qtype, int count, const void *const *W, void *const *Y,
+                             const int *N, const void *bias, const void *A, bool f16, int M,
+                             int K, int mode, hipStream_t stream) {
+  if (M > 32 || count < 1 || count > 3) return hipErrorInvalidValue;
+  SkArgs args{};
+  for (int i = 0; i < count; ++i)
+    args.seg[i] = SkSeg{static_cast<const uint8_t *>(W[i]), Y[i], i == 0 ? bias : nullptr, N[i], 0};
+  args.nseg = count;
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = mode;
   const bool two = M > 16;  // two m-tiles of 16
   switch (qtype) {
-  case kTypeQ4_K:
-    return two ? launch_mt<kTypeQ4_K, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_mt<kTypeQ4_K, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
-  case kTypeQ6_K:
-    return two ? launch_mt<kTypeQ6_K, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_mt<kTypeQ6_K, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
-  case kTypeQ8_0:
-    return two ? launch_mt<kTypeQ8_0, 2>(w, a, Y, bias, f16, M, N, K, mode, stream)
-               : launch_mt<kTypeQ8_0, 1>(w, a, Y, bias, f16, M, N, K, mode, stream);
+  case kTypeQ4_K: return two ? launch_mt<kTypeQ4_K, 2>(args, f16, stream) : launch_mt<kTypeQ4_K, 1>(args, f16, stream);
+  case kTypeQ6_K: return two ? launch_mt<kTypeQ6_K, 2>(args, f16, stream) : launch_mt<kTypeQ6_K, 1>(args, f16, stream);
+  case kTypeQ8_0: return two ? launch_mt<kTypeQ8_0, 2>(args, f16, stream) : launch_mt<kTypeQ8_0, 1>(args, f16, stream);
   default: return hipErrorInvalidValue;
   }
 }
