@@ -2,10 +2,11 @@
 
 Workload: one Qwen2.5-3B Q4_K_M decode layer through
 the quantized path, launched as the reference's forward pass launches it
-(inferflux_amd/workloads.py DECODE_LAUNCHES): Q8_1 quantize of the four
-activation inputs, one grouped Q/K/V GEMV, O accumulated into an fp32
-residual, one grouped gate/up GEMV, the Q6_K down projection accumulated
-into the residual.  A step is one such layer at M = 1 (the unified decode
+(inferflux_amd/workloads.py DECODE_LAUNCHES), as a chain over an fp32
+residual stream: fused RMSNorm+Q8_1 -> one grouped Q/K/V GEMV -> Q8_1 of
+the attention output -> O accumulated into the residual -> fused
+RMSNorm+Q8_1 -> one grouped gate/up GEMV -> fused SiLU*up+Q8_1 -> the Q6_K
+down projection accumulated into the residual.  A step is one such layer at M = 1 (the unified decode
 batch of the headline).  Weights rotate through replicas totalling >= 512
 MB so every step streams from HBM, not the 256 MB Infinity Cache.
 
@@ -121,34 +122,58 @@ def main():
         return a.elapsed_time(b) * 1e3 / steps  # us per call
 
     def decode_layer_runner(layer, M, seed):
-        """One decode layer at batch M: 4 quantizes + 4 GEMV launches."""
-        K_of = {"attn_in": layer["q"][2], "attn_out": layer["o"][2],
-                "ffn_in": layer["gate"][2], "ffn_act": layer["down"][2]}
-        xs = {k: torch.from_numpy(synth.activations(M, K, seed=seed + j)).to(dev)
-              for j, (k, K) in enumerate(K_of.items())}
-        A = {k: torch.empty((M, K // 32 * 36), dtype=torch.uint8, device=dev)
-             for k, K in K_of.items()}
+        """One decode layer at batch M as a chain over an fp32 residual
+        stream: RMSNorm+Q8_1 -> grouped QKV -> Q8_1 of the attention output
+        (synthetic: attention itself is not on this path) -> O accumulated
+        into the residual -> RMSNorm+Q8_1 -> grouped gate/up -> SiLU*up+Q8_1
+        -> down accumulated into the residual.  4 producers + 4 GEMVs."""
+        hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
+        rng = np.random.default_rng(seed)
+        resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
+        attn = torch.from_numpy(synth.activations(M, q_dim, seed=seed + 1)).to(dev)
+        norm_w = {k: torch.from_numpy(rng.uniform(0.5, 1.5, hidden).astype(np.float16)).to(dev)
+                  for k in ("attn", "ffn")}
+        A = {"attn_in": (M, hidden), "attn_out": (M, q_dim), "ffn_in": (M, hidden),
+             "ffn_act": (M, ffn)}
+        A = {k: torch.empty((m, K // 32 * 36), dtype=torch.uint8, device=dev)
+             for k, (m, K) in A.items()}
         Y = {name: torch.zeros((M, v[1]), dtype=torch.float32, device=dev)
              for name, v in layer.items()}
+        Y["o"] = Y["down"] = resid  # O and down accumulate into the residual
         R = len(layer["q"][3])
+        launches = {l[0]: l for l in workloads.DECODE_LAUNCHES}
+
+        def gemv(lname, r):
+            _, projs, src, accum = launches[lname]
+            qt, _, K, _ = layer[projs[0]]
+            mode = ops.ACCUM if accum else ops.STORE
+            if len(projs) == 1:
+                p = layer[projs[0]]
+                ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode)
+            else:
+                ops.qgemv_grouped(qt, [layer[p][3][r] for p in projs], A[src], M,
+                                  [layer[p][1] for p in projs], K,
+                                  outs=[Y[p] for p in projs], mode=mode)
 
         def run(i, which=None):
             r = i % R
-            if which is None or which == "quant":
-                for k in K_of:
-                    ops.quantize_q8_1(xs[k], out=A[k])
-            for lname, projs, src, accum in workloads.DECODE_LAUNCHES:
-                if which is not None and which != lname:
-                    continue
-                qt, _, K, _ = layer[projs[0]]
-                mode = ops.ACCUM if accum else ops.STORE
-                if len(projs) == 1:
-                    p = layer[projs[0]]
-                    ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode)
-                else:
-                    ops.qgemv_grouped(qt, [layer[p][3][r] for p in projs], A[src], M,
-                                      [layer[p][1] for p in projs], K,
-                                      outs=[Y[p] for p in projs], mode=mode)
+            prod = which is None or which == "producers"
+            if prod:
+                ops.rmsnorm_quantize_q8_1(resid, norm_w["attn"], out=A["attn_in"])
+            if which is None or which == "qkv":
+                gemv("qkv", r)
+            if prod:
+                ops.quantize_q8_1(attn, out=A["attn_out"])
+            if which is None or which == "o":
+                gemv("o", r)
+            if prod:
+                ops.rmsnorm_quantize_q8_1(resid, norm_w["ffn"], out=A["ffn_in"])
+            if which is None or which == "gate_up":
+                gemv("gate_up", r)
+            if prod:
+                ops.silu_mul_quantize_q8_1(Y["gate"], Y["up"], out=A["ffn_act"])
+            if which is None or which == "down":
+                gemv("down", r)
         return run
 
     def launch_bytes(layer, lname, M):
@@ -173,7 +198,7 @@ def main():
         # each launch alone (same rotation), for per-kernel GB/s
         kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, args.warmup)
                 for l in workloads.DECODE_LAUNCHES}
-        kern["quant_x4"] = time_loop(lambda i: run(i, "quant"), steps, args.warmup)
+        kern["producers_x4"] = time_loop(lambda i: run(i, "producers"), steps, args.warmup)
         q4 = [l[0] for l in workloads.DECODE_LAUNCHES if launch_bytes(layer3b, l[0], M)[0] == ops.Q4_K]
         q4_bytes = sum(launch_bytes(layer3b, n, M)[1] for n in q4)
         q4_us = sum(kern[n] for n in q4)

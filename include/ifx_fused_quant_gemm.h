@@ -74,6 +74,21 @@ class FusedQuantGemm {
   static void QuantizeRowQ8_1(const float *input, void *output_q8_1, int M, int K,
                               hipStream_t stream);
 
+  // fused_quant_gemm.h:121-129: SiLU(gate) * up quantized to Q8_1 (fp16
+  // inputs), and the fp32 variant for fp32 gate/up outputs.
+  static void SiluMulQuantizeQ8_1(const uint16_t *gate, const uint16_t *up, void *output_q8_1,
+                                  int M, int K, hipStream_t stream);
+  static void SiluMulQuantizeQ8_1(const float *gate, const float *up, void *output_q8_1, int M,
+                                  int K, hipStream_t stream);
+  // fused_quant_gemm.h:131-150: RMSNorm (fp16 norm weights) then Q8_1, for
+  // an fp16 or an fp32 residual stream.
+  static void FusedRmsNormQuantizeQ8_1(const uint16_t *residual, const uint16_t *norm_weight,
+                                       void *output_q8_1, int M, int K, float rms_norm_eps,
+                                       hipStream_t stream);
+  static void FusedRmsNormQuantizeQ8_1(const float *residual, const uint16_t *norm_weight,
+                                       void *output_q8_1, int M, int K, float rms_norm_eps,
+                                       hipStream_t stream);
+
   // fused_quant_gemm.h:171-173: output = W . a, fp16 out.
   static bool GemvQ8_1(const QuantizedWeightInfo &weight, const void *act_q8_1,
                        uint16_t *output, int M, int N, int K, hipStream_t stream,

@@ -60,6 +60,24 @@ int ifx_q8_1_quantize_f32(const float *x, void *q8_1, int M, int K, void *stream
 /* Same, fp16 input: the reference's own signature (const half* input). */
 int ifx_q8_1_quantize_f16(const uint16_t *x, void *q8_1, int M, int K, void *stream);
 
+/* Fused RMSNorm then Q8_1: per row, rms = 1/sqrt(sum(x^2)/K + eps),
+ * y = (x * rms) * norm_weight, quantized as ifx_q8_1_quantize_f32 does.
+ * residual [M][K] fp32 or fp16 (residual_dtype: ifx_out_dtype),
+ * norm_weight fp16 [K].  Replaces FusedQuantGemm::FusedRmsNormQuantizeQ8_1
+ * (both overloads, fused_quant_gemm.h:131-150; kernels
+ * fused_dequant_gemv.cuh:736-904).  The square root and division are
+ * correctly rounded (the reference uses rsqrtf). */
+int ifx_rmsnorm_quantize_q8_1(const void *residual, int residual_dtype,
+                              const uint16_t *norm_weight, void *q8_1, int M, int K, float eps,
+                              void *stream);
+
+/* Fused SiLU(gate) * up then Q8_1: y = gate / (1 + exp(-gate)) * up.
+ * gate, up [M][K], fp32 or fp16 (dtype: ifx_out_dtype).  Replaces
+ * FusedQuantGemm::SiluMulQuantizeQ8_1 (fused_quant_gemm.h:121-129; kernel
+ * fused_dequant_gemv.cuh:657-734), which reads fp16. */
+int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void *q8_1, int M,
+                               int K, void *stream);
+
 /* Quantized GEMV/GEMM y[m][n] (op)= sum_k W[n][k] * a[m][k] for any M >= 1.
  * Replaces FusedQuantGemm::GemvQ8_1 / GemvQ8_1Accum / GemvQ8_1AccumF32 /
  * GemvQ8_1WithBias (fused_quant_gemm.h:171-173, 190-193, 202-205; .cu

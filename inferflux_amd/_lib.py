@@ -15,6 +15,8 @@ _vp, _i32, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
 SIGNATURES = {
     "ifx_q8_1_quantize_f32": ([_vp, _vp, _i32, _i32, _vp], _i32),
     "ifx_q8_1_quantize_f16": ([_vp, _vp, _i32, _i32, _vp], _i32),
+    "ifx_rmsnorm_quantize_q8_1": ([_vp, _i32, _vp, _vp, _i32, _i32, ctypes.c_float, _vp], _i32),
+    "ifx_silu_mul_quantize_q8_1": ([_vp, _vp, _i32, _vp, _i32, _i32, _vp], _i32),
     "ifx_qgemv": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemv_grouped": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),

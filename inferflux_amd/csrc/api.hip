@@ -15,6 +15,10 @@
 namespace ifx {
 hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
                                 hipStream_t stream);
+hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t *w, void *out,
+                                        int M, int K, float eps, hipStream_t stream);
+hipError_t launch_silu_mul_quantize_q8_1(const void *g, const void *u, bool f16, void *out,
+                                         int64_t M, int64_t K, hipStream_t stream);
 hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int64_t n_elems,
                              hipStream_t stream);
 hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const void *bias,
@@ -150,6 +154,26 @@ int ifx_q8_1_quantize_f16(const uint16_t *x, void *q8_1, int M, int K, void *str
   if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_quantize_q8_1(x, true, q8_1, M, K,
                                              static_cast<hipStream_t>(stream)));
+}
+
+int ifx_rmsnorm_quantize_q8_1(const void *residual, int residual_dtype,
+                              const uint16_t *norm_weight, void *q8_1, int M, int K, float eps,
+                              void *stream) {
+  if (!residual || !norm_weight || !q8_1) return IFX_NULL_POINTER;
+  if (residual_dtype != IFX_OUT_F32 && residual_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (M < 0 || K <= 0 || K % 32 || !(eps >= 0.0f)) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_rmsnorm_quantize_q8_1(residual, residual_dtype == IFX_OUT_F16,
+                                                     norm_weight, q8_1, M, K, eps,
+                                                     static_cast<hipStream_t>(stream)));
+}
+
+int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void *q8_1, int M,
+                               int K, void *stream) {
+  if (!gate || !up || !q8_1) return IFX_NULL_POINTER;
+  if (dtype != IFX_OUT_F32 && dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_silu_mul_quantize_q8_1(gate, up, dtype == IFX_OUT_F16, q8_1, M, K,
+                                                      static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,

@@ -75,6 +75,111 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1_f16(const uint16_t *__res
                   out + blk * kQ8_1Bytes, l);
 }
 
+// ---------------------------------------------------------------------------
+// Fused producers of Q8_1 activations (the steps before the GEMVs of a
+// decode layer), with the quantizer above as their last step.
+// ---------------------------------------------------------------------------
+
+template <bool F16>
+__device__ __forceinline__ f32x4 load4(const void *p, int64_t i) {
+  if constexpr (F16) {
+    const u32x2 v = ldg<u32x2>(static_cast<const uint16_t *>(p) + i);
+    return f32x4{h2f(v.x & 0xFFFFu), h2f(v.x >> 16), h2f(v.y & 0xFFFFu), h2f(v.y >> 16)};
+  } else {
+    return ldg<f32x4>(static_cast<const float *>(p) + i);
+  }
+}
+
+// RMSNorm then Q8_1 (fused_dequant_gemv.cuh:736-904): per row,
+// rms = 1 / sqrt(sum(x^2) / K + eps), y = (x * rms) * w, quantized per 32.
+// One workgroup of 256 threads per row: the sum of squares is reduced with
+// DPP within each wave and through LDS across the four waves; then 8 lanes
+// per Q8_1 block apply the norm and quantize (L2-resident second read of
+// the row).  The reference evaluates rsqrtf (an approximation); here the
+// square root and division are correctly rounded.
+template <bool F16>
+__global__ __launch_bounds__(256) void k_rmsnorm_quantize_q8_1(const void *__restrict__ x,
+                                                               const uint16_t *__restrict__ w,
+                                                               uint8_t *__restrict__ out, int K,
+                                                               float eps) {
+  __shared__ float part[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t base = row * K;
+  float ss = 0.0f;
+  for (int i = 4 * tid; i < K; i += 4 * 256) {
+    const f32x4 v = load4<F16>(x, base + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum_to63(ss);
+  if ((tid & 63) == 63) part[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
+  const int nblk = K >> 5;
+  uint8_t *orow = out + row * nblk * kQ8_1Bytes;
+  // whole 8-lane groups per block: every shuffle partner is live
+  for (int b = tid >> 3; b < nblk; b += 32) {
+    const int l = tid & 7;
+    const int i = b * 32 + l * 4;
+    const f32x4 v = load4<F16>(x, base + i);
+    const u32x2 wv = ldg<u32x2>(w + i);
+    const float y0 = materialize_f32(v.x * rms) * h2f(wv.x & 0xFFFFu);
+    const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
+    const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
+    const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
+    quantize4_store(y0, y1, y2, y3, orow + b * kQ8_1Bytes, l);
+  }
+}
+
+// SiLU(gate) * up then Q8_1 (fused_dequant_gemv.cuh:657-734):
+// y = (g / (1 + exp(-g))) * u, 8 lanes per Q8_1 block.
+template <bool F16>
+__global__ __launch_bounds__(256) void k_silu_mul_quantize_q8_1(const void *__restrict__ g,
+                                                                const void *__restrict__ u,
+                                                                uint8_t *__restrict__ out,
+                                                                int64_t nblocks) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t blk = t >> 3;
+  const int l = threadIdx.x & 7;
+  if (blk >= nblocks) return;
+  const f32x4 gv = load4<F16>(g, blk * 32 + l * 4);
+  const f32x4 uv = load4<F16>(u, blk * 32 + l * 4);
+  float y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float gi = gv[i];
+    y[i] = materialize_f32(gi / (1.0f + expf(-gi))) * uv[i];
+  }
+  quantize4_store(y[0], y[1], y[2], y[3], out + blk * kQ8_1Bytes, l);
+}
+
+hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t *w, void *out,
+                                        int M, int K, float eps, hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  if (f16)
+    hipLaunchKernelGGL(k_rmsnorm_quantize_q8_1<true>, dim3(M), dim3(256), 0, stream, x, w,
+                       static_cast<uint8_t *>(out), K, eps);
+  else
+    hipLaunchKernelGGL(k_rmsnorm_quantize_q8_1<false>, dim3(M), dim3(256), 0, stream, x, w,
+                       static_cast<uint8_t *>(out), K, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quantize_q8_1(const void *g, const void *u, bool f16, void *out,
+                                         int64_t M, int64_t K, hipStream_t stream) {
+  const int64_t nblocks = M * (K / 32);
+  if (nblocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((nblocks * 8 + 255) / 256));
+  if (f16)
+    hipLaunchKernelGGL(k_silu_mul_quantize_q8_1<true>, grid, dim3(256), 0, stream, g, u,
+                       static_cast<uint8_t *>(out), nblocks);
+  else
+    hipLaunchKernelGGL(k_silu_mul_quantize_q8_1<false>, grid, dim3(256), 0, stream, g, u,
+                       static_cast<uint8_t *>(out), nblocks);
+  return hipGetLastError();
+}
+
 hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
                                 hipStream_t stream) {
   const int64_t nblocks = M * (K / 32);

@@ -95,6 +95,31 @@ void FusedQuantGemm::QuantizeRowQ8_1(const float *input, void *output_q8_1, int 
   ifx_q8_1_quantize_f32(input, output_q8_1, M, K, stream);
 }
 
+void FusedQuantGemm::SiluMulQuantizeQ8_1(const uint16_t *gate, const uint16_t *up,
+                                         void *output_q8_1, int M, int K, hipStream_t stream) {
+  ifx_silu_mul_quantize_q8_1(gate, up, IFX_OUT_F16, output_q8_1, M, K, stream);
+}
+
+void FusedQuantGemm::SiluMulQuantizeQ8_1(const float *gate, const float *up, void *output_q8_1,
+                                         int M, int K, hipStream_t stream) {
+  ifx_silu_mul_quantize_q8_1(gate, up, IFX_OUT_F32, output_q8_1, M, K, stream);
+}
+
+void FusedQuantGemm::FusedRmsNormQuantizeQ8_1(const uint16_t *residual,
+                                              const uint16_t *norm_weight, void *output_q8_1,
+                                              int M, int K, float rms_norm_eps,
+                                              hipStream_t stream) {
+  ifx_rmsnorm_quantize_q8_1(residual, IFX_OUT_F16, norm_weight, output_q8_1, M, K, rms_norm_eps,
+                            stream);
+}
+
+void FusedQuantGemm::FusedRmsNormQuantizeQ8_1(const float *residual, const uint16_t *norm_weight,
+                                              void *output_q8_1, int M, int K,
+                                              float rms_norm_eps, hipStream_t stream) {
+  ifx_rmsnorm_quantize_q8_1(residual, IFX_OUT_F32, norm_weight, output_q8_1, M, K, rms_norm_eps,
+                            stream);
+}
+
 bool FusedQuantGemm::GemvQ8_1(const QuantizedWeightInfo &weight, const void *act_q8_1,
                               uint16_t *output, int M, int N, int K, hipStream_t stream,
                               const NativeExecutionPolicy *policy) {

@@ -6,6 +6,7 @@ Errors follow the reference's contract (fused_quant_gemm.cu:2085-2117):
 a positive status means "not handled" and is raised as NotHandled so the
 caller can pick a fallback; a negative status is a HIP launch error.
 """
+
 import torch
 
 from . import _lib
@@ -70,6 +71,38 @@ def quantize_q8_1(x, out=None, stream=None):
     else:
         raise TypeError("x must be float32 or float16")
     _check(rc, "ifx_q8_1_quantize")
+    return out
+
+
+def rmsnorm_quantize_q8_1(x, norm_weight, eps=1e-6, out=None, stream=None):
+    """RMSNorm of fp32/fp16 rows x [M, K] by fp16 norm_weight [K], then Q8_1."""
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, K // 32 * 36), dtype=torch.uint8, device=x.device)
+    if norm_weight.dtype != torch.float16 or norm_weight.numel() != K:
+        raise TypeError("norm_weight must be float16 [K]")
+    if x.dtype not in (torch.float32, torch.float16):
+        raise TypeError("x must be float32 or float16")
+    dt = OUT_F16 if x.dtype == torch.float16 else OUT_F32
+    rc = _lib.load().ifx_rmsnorm_quantize_q8_1(_dev(x, "x"), dt, _dev(norm_weight, "norm_weight"),
+                                               _dev(out, "out"), M, K, float(eps), _stream(stream))
+    _check(rc, "ifx_rmsnorm_quantize_q8_1")
+    return out
+
+
+def silu_mul_quantize_q8_1(gate, up, out=None, stream=None):
+    """SiLU(gate) * up for fp32/fp16 [M, K], then Q8_1."""
+    M, K = gate.shape
+    if up.shape != gate.shape or up.dtype != gate.dtype:
+        raise ValueError("gate and up must match")
+    if gate.dtype not in (torch.float32, torch.float16):
+        raise TypeError("gate/up must be float32 or float16")
+    if out is None:
+        out = torch.empty((M, K // 32 * 36), dtype=torch.uint8, device=gate.device)
+    dt = OUT_F16 if gate.dtype == torch.float16 else OUT_F32
+    rc = _lib.load().ifx_silu_mul_quantize_q8_1(_dev(gate, "gate"), _dev(up, "up"), dt,
+                                                _dev(out, "out"), M, K, _stream(stream))
+    _check(rc, "ifx_silu_mul_quantize_q8_1")
     return out
 
 

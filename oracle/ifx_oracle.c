@@ -250,6 +250,70 @@ int orc_quantize_q8_1_f16(const uint16_t *x, void *out, int64_t M, int64_t K) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Fused producers of Q8_1 activations.                                      */
+/* RMSNorm + Q8_1: native/kernels/fused_dequant_gemv.cuh:736-904 (and the    */
+/*   helpers LoadHalfToSmemSumSq / ApplyNormInPlace, :24-63): per row,       */
+/*   rms = rsqrt(sum(x^2)/K + eps), y = (x * rms) * w, then the quantizer.   */
+/*   Here rms is evaluated in fp64 and rounded once to fp32 (the device     */
+/*   result differs by rounding only), y in fp32 as two rounded products.   */
+/* SiLU*mul + Q8_1: fused_dequant_gemv.cuh:657-734: y = (g / (1 + exp(-g)))  */
+/*   * u; the silu factor in fp64 rounded to fp32, the product in fp32.     */
+/* The *_values functions return y (the pre-quantization fp32 values).      */
+/* ------------------------------------------------------------------------ */
+static float rms_factor(const float *x, int64_t K, float eps) {
+  double ss = 0.0;
+  for (int64_t i = 0; i < K; ++i) ss += (double)x[i] * (double)x[i];
+  return (float)(1.0 / sqrt(ss / (double)K + (double)eps));
+}
+
+int orc_rmsnorm_values(const float *x, const uint16_t *w, float *y, int64_t M, int64_t K,
+                       float eps) {
+  if (K % 32) return 1;
+  for (int64_t m = 0; m < M; ++m) {
+    const float *xr = x + m * K;
+    const float rms = rms_factor(xr, K, eps);
+    for (int64_t i = 0; i < K; ++i) {
+      const float t = xr[i] * rms;
+      y[m * K + i] = t * orc_f16_to_f32(w[i]);
+    }
+  }
+  return 0;
+}
+
+int orc_rmsnorm_quantize_q8_1(const float *x, const uint16_t *w, void *out, int64_t M, int64_t K,
+                              float eps) {
+  if (K % 32) return 1;
+  float *y = (float *)malloc(sizeof(float) * (size_t)K);
+  if (!y) return 2;
+  uint8_t *o = (uint8_t *)out;
+  for (int64_t m = 0; m < M; ++m) {
+    orc_rmsnorm_values(x + m * K, w, y, 1, K, eps);
+    for (int64_t b = 0; b < K / 32; ++b) quantize_q8_1_block(y + b * 32, o + (m * (K / 32) + b) * 36);
+  }
+  free(y);
+  return 0;
+}
+
+int orc_silu_mul_values(const float *g, const float *u, float *y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float s = (float)((double)g[i] / (1.0 + exp(-(double)g[i])));
+    y[i] = s * u[i];
+  }
+  return 0;
+}
+
+int orc_silu_mul_quantize_q8_1(const float *g, const float *u, void *out, int64_t M, int64_t K) {
+  if (K % 32) return 1;
+  float y[32];
+  uint8_t *o = (uint8_t *)out;
+  for (int64_t b = 0; b < M * (K / 32); ++b) {
+    orc_silu_mul_values(g + b * 32, u + b * 32, y, 32);
+    quantize_q8_1_block(y, o + b * 36);
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Exact GEMV/GEMM in fp64 (the mathematical target).                        */
 /*   y[m][n] = sum_k w[n][k] * a[m][k], w the exact dequantized weight        */
 /*   (each w is exact in fp64) and a = f16(d_blk) * q (exact in fp64).        */

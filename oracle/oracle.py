@@ -44,6 +44,10 @@ def lib():
         L.orc_dequantize.argtypes = [i32, vp, vp, i64, i64]
         L.orc_quantize_q8_1_f32.argtypes = [vp, vp, i64, i64]
         L.orc_quantize_q8_1_f16.argtypes = [vp, vp, i64, i64]
+        L.orc_rmsnorm_values.argtypes = [vp, vp, vp, i64, i64, ctypes.c_float]
+        L.orc_rmsnorm_quantize_q8_1.argtypes = [vp, vp, vp, i64, i64, ctypes.c_float]
+        L.orc_silu_mul_values.argtypes = [vp, vp, vp, i64]
+        L.orc_silu_mul_quantize_q8_1.argtypes = [vp, vp, vp, i64, i64]
         L.orc_gemv_exact.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
         L.orc_gemv_q8_1.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
         L.orc_ggml_cpu_gemv.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
@@ -109,6 +113,47 @@ def quantize_q8_1(x):
         x = np.ascontiguousarray(x, dtype=np.float32)
         rc = lib().orc_quantize_q8_1_f32(_p(x), _p(out), M, K)
     if rc:
+        raise ValueError("K must be a multiple of 32")
+    return out
+
+
+def _f32(x):
+    """fp16 inputs are widened exactly, as the device kernels do."""
+    return np.ascontiguousarray(np.asarray(x).astype(np.float32))
+
+
+def rmsnorm_values(x, w_f16, eps):
+    """fp32 pre-quantization values of RMSNorm: (x * rms) * w."""
+    x = _f32(x)
+    M, K = x.shape
+    w = np.ascontiguousarray(w_f16, dtype=np.float16).view(np.uint16)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm_values(_p(x), _p(w), _p(y), M, K, eps)
+    return y
+
+
+def rmsnorm_quantize_q8_1(x, w_f16, eps):
+    x = _f32(x)
+    M, K = x.shape
+    w = np.ascontiguousarray(w_f16, dtype=np.float16).view(np.uint16)
+    out = np.empty((M, K // 32 * 36), np.uint8)
+    if lib().orc_rmsnorm_quantize_q8_1(_p(x), _p(w), _p(out), M, K, eps):
+        raise ValueError("K must be a multiple of 32")
+    return out
+
+
+def silu_mul_values(g, u):
+    g, u = _f32(g), _f32(u)
+    y = np.empty_like(g)
+    lib().orc_silu_mul_values(_p(g), _p(u), _p(y), g.size)
+    return y
+
+
+def silu_mul_quantize_q8_1(g, u):
+    g, u = _f32(g), _f32(u)
+    M, K = g.shape
+    out = np.empty((M, K // 32 * 36), np.uint8)
+    if lib().orc_silu_mul_quantize_q8_1(_p(g), _p(u), _p(out), M, K):
         raise ValueError("K must be a multiple of 32")
     return out
 

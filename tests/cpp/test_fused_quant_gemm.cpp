@@ -27,6 +27,9 @@ int orc_block_elems(int qtype);
 uint16_t orc_f32_to_f16(float f);
 float orc_f16_to_f32(uint16_t h);
 int orc_quantize_q8_1_f32(const float *x, void *out, int64_t M, int64_t K);
+int orc_rmsnorm_quantize_q8_1(const float *x, const uint16_t *w, void *out, int64_t M, int64_t K,
+                              float eps);
+int orc_silu_mul_quantize_q8_1(const float *g, const float *u, void *out, int64_t M, int64_t K);
 int orc_gemv_exact(int qtype, const void *W, const void *A, double *y, int M, int N, int K,
                    int threads);
 }
@@ -289,6 +292,40 @@ void TestGpuCase(int qtype, int M, int N, int K) {
   HIP_OK(hipStreamDestroy(s));
 }
 
+// Exact-arithmetic cases of the fused producers (the randomized ones run
+// from Python): x = +-1 with eps = 0 gives rms = 1; gate >= 20 gives
+// silu(gate) = gate in fp32.
+void TestProducers() {
+  std::printf("[gpu producers]\n");
+  std::fflush(stdout);
+  const int M = 2, K = 1024;
+  Rng r(77);
+  std::vector<float> x(M * K), g(M * K), u(M * K);
+  std::vector<uint16_t> w(K);
+  for (auto &v : x) v = (r.next() & 1) ? 1.0f : -1.0f;
+  for (auto &v : w) v = orc_f32_to_f16(r.normal());
+  for (auto &v : g) v = 20.0f + static_cast<float>(r.next() % 20);
+  for (auto &v : u) v = static_cast<float>(static_cast<int>(r.next() % 7) - 3);
+  Dev dx(x.size() * 4), dw(w.size() * 2), dg(g.size() * 4), du(u.size() * 4),
+      da(static_cast<size_t>(M) * (K / 32) * 36);
+  HIP_OK(hipMemcpy(dx.p, x.data(), x.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dw.p, w.data(), w.size() * 2, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dg.p, g.data(), g.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(du.p, u.data(), u.size() * 4, hipMemcpyHostToDevice));
+  std::vector<uint8_t> a(static_cast<size_t>(M) * (K / 32) * 36), e(a.size());
+  FusedQuantGemm::FusedRmsNormQuantizeQ8_1(dx.as<float>(), dw.as<uint16_t>(), da.p, M, K, 0.0f,
+                                           nullptr);
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(a.data(), da.p, a.size(), hipMemcpyDeviceToHost));
+  orc_rmsnorm_quantize_q8_1(x.data(), w.data(), e.data(), M, K, 0.0f);
+  EXPECT(a == e);
+  FusedQuantGemm::SiluMulQuantizeQ8_1(dg.as<float>(), du.as<float>(), da.p, M, K, nullptr);
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(a.data(), da.p, a.size(), hipMemcpyDeviceToHost));
+  orc_silu_mul_quantize_q8_1(g.data(), u.data(), e.data(), M, K);
+  EXPECT(a == e);
+}
+
 template <size_t C>
 void TestGrouped(int qtype, int M, int K, const std::array<int, C> &Ns) {
   std::printf("[gpu grouped x%zu] qtype=%d M=%d K=%d\n", C, qtype, M, K);
@@ -334,6 +371,7 @@ int main(int argc, char **argv) {
     TestGpuCase(Q4_K, 5, 200, 1024);
     TestGpuCase(Q6_K, 24, 96, 2048);
     TestGpuCase(Q8_0, 40, 160, 512);
+    TestProducers();
     TestGrouped<2>(Q4_K, 1, 2048, {300, 173});
     TestGrouped<3>(Q4_K, 2, 1024, {128, 64, 65});
     TestGrouped<3>(Q6_K, 1, 512, {33, 1, 250});

@@ -275,3 +275,87 @@ def test_host_cpp_gpu():
     r = subprocess.run([binary(), "gpu"], capture_output=True, text=True, timeout=100)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+# ------------------------------------------------ fused Q8_1 producers
+def _q8_1_fields(a):
+    b = a.reshape(a.shape[0], -1, 36)
+    d = b[:, :, 0:2].copy().view(np.float16)[:, :, 0]
+    s = b[:, :, 2:4].copy().view(np.float16)[:, :, 0]
+    q = b[:, :, 4:].view(np.int8).astype(np.int32)
+    return d, s, q
+
+
+def check_q8_1_close(a_gpu, a_ref, y_ref):
+    """The device's pre-quantization values differ from the fp64-based
+    oracle's by rounding (sum order of the norm, exp): codes may differ by
+    one, rarely, and scales by one fp16 ulp; each block must still be a
+    valid quantization of the reference values and its s field must be
+    f16(d * sum(q)) of its own codes."""
+    if np.array_equal(a_gpu, a_ref):
+        return
+    dg, sg, qg = _q8_1_fields(a_gpu)
+    dr, sr, qr = _q8_1_fields(a_ref)
+    diff = np.abs(qg - qr)
+    assert diff.max() <= 1, f"code differs by {diff.max()}"
+    assert (diff > 0).mean() <= 2e-3, f"{(diff > 0).mean():.2e} of codes differ"
+    du = np.abs(dg.view(np.int16).astype(np.int32) - dr.view(np.int16).astype(np.int32))
+    assert du.max() <= 1, "scale differs by more than one fp16 ulp"
+    sg_expect = (dg.astype(np.float32) * qg.sum(axis=2).astype(np.float32)).astype(np.float16)
+    assert np.array_equal(sg.view(np.uint16), sg_expect.view(np.uint16))
+    yb = y_ref.reshape(qg.shape).astype(np.float64)
+    d64 = dg.astype(np.float64)[:, :, None]
+    assert np.all(np.abs(d64 * qg - yb) <= 0.5 * d64 * (1 + 1e-2) + 1e-7 * np.abs(yb))
+
+
+@pytest.mark.parametrize("x_dtype", ["f32", "f16"])
+def test_rmsnorm_quantize_exact_kat(orc, dev, x_dtype):
+    import torch
+    from inferflux_amd import ops
+    note(f"rmsnorm kat {x_dtype}")
+    rng = np.random.default_rng(31)
+    x = np.where(rng.random((3, 2048)) < 0.5, -1.0, 1.0).astype(np.float32)
+    w = rng.standard_normal(2048).astype(np.float16)
+    xt = up(x if x_dtype == "f32" else x.astype(np.float16), dev)
+    a = down(ops.rmsnorm_quantize_q8_1(xt, up(w, dev), eps=0.0))
+    assert np.array_equal(a, orc.rmsnorm_quantize_q8_1(x, w, 0.0))
+
+
+@pytest.mark.parametrize("M,K,x_dtype", [(1, 2048, "f32"), (5, 5120, "f32"), (2, 11008, "f16"),
+                                         (1, 32, "f32"), (3, 13824, "f16")])
+def test_rmsnorm_quantize_parity(orc, dev, M, K, x_dtype):
+    from inferflux_amd import ops
+    note(f"rmsnorm M={M} K={K} {x_dtype}")
+    rng = np.random.default_rng(M * K)
+    x = (rng.standard_normal((M, K)) * 4).astype(np.float32)
+    if x_dtype == "f16":
+        x = x.astype(np.float16)
+    w = rng.uniform(0.2, 2.0, K).astype(np.float16)
+    a = down(ops.rmsnorm_quantize_q8_1(up(x, dev), up(w, dev), eps=1e-6))
+    check_q8_1_close(a, orc.rmsnorm_quantize_q8_1(x, w, 1e-6), orc.rmsnorm_values(x, w, 1e-6))
+
+
+@pytest.mark.parametrize("M,K,dtype", [(1, 11008, "f32"), (4, 13824, "f32"), (2, 2048, "f16"),
+                                       (3, 32, "f32")])
+def test_silu_mul_quantize_parity(orc, dev, M, K, dtype):
+    from inferflux_amd import ops
+    note(f"silu_mul M={M} K={K} {dtype}")
+    rng = np.random.default_rng(M + K)
+    g = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    u = rng.standard_normal((M, K)).astype(np.float32)
+    if dtype == "f16":
+        g, u = g.astype(np.float16), u.astype(np.float16)
+    a = down(ops.silu_mul_quantize_q8_1(up(g, dev), up(u, dev)))
+    check_q8_1_close(a, orc.silu_mul_quantize_q8_1(g, u), orc.silu_mul_values(g, u))
+
+
+def test_silu_mul_quantize_exact_kat(orc, dev):
+    """gate >= 20: exp(-gate) vanishes in fp32 next to 1, so y = gate * up
+    exactly; with integer gate/up the codes are exact on both sides."""
+    from inferflux_amd import ops
+    rng = np.random.default_rng(33)
+    g = rng.integers(20, 40, (2, 256)).astype(np.float32)
+    u = rng.integers(-3, 4, (2, 256)).astype(np.float32)
+    a = down(ops.silu_mul_quantize_q8_1(up(g, dev), up(u, dev)))
+    assert np.array_equal(a, orc.silu_mul_quantize_q8_1(g, u))
+    assert np.array_equal(a, orc.quantize_q8_1(g * u))

@@ -290,3 +290,48 @@ def test_q8_1_double_rounding_fixture(orc):
     """s is rounded to fp32 first, then to fp16 (fused_dequant_gemv.cuh:650)."""
     z = np.load(os.path.join(GOLDEN, "gemv_small.npz"))
     assert np.array_equal(orc.quantize_q8_1(z["dr_x"]), z["dr_q8_1"])
+
+
+# ------------------------------------------------ fused Q8_1 producers
+def test_rmsnorm_values_vs_fp64(orc):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 2048)) * 3).astype(np.float32)
+    w = (rng.standard_normal(2048) * 0.5).astype(np.float16)
+    y = orc.rmsnorm_values(x, w, 1e-5)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + 1e-5) * w.astype(np.float64)
+    assert np.allclose(y, ref, rtol=4e-7, atol=1e-30)
+    # fp16 residual input is widened exactly
+    x16 = x.astype(np.float16)
+    assert np.array_equal(orc.rmsnorm_values(x16, w, 1e-5),
+                          orc.rmsnorm_values(x16.astype(np.float32), w, 1e-5))
+
+
+def test_rmsnorm_quantize_is_quantizer_of_values(orc):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((2, 1024)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 1024).astype(np.float16)
+    assert np.array_equal(orc.rmsnorm_quantize_q8_1(x, w, 1e-6),
+                          orc.quantize_q8_1(orc.rmsnorm_values(x, w, 1e-6)))
+
+
+def test_rmsnorm_exact_kat(orc):
+    """x = +-1 and eps = 0: sum(x^2) = K, rms = 1 exactly, y = x * w."""
+    rng = np.random.default_rng(7)
+    x = np.where(rng.random((2, 512)) < 0.5, -1.0, 1.0).astype(np.float32)
+    w = rng.standard_normal(512).astype(np.float16)
+    y = orc.rmsnorm_values(x, w, 0.0)
+    assert np.array_equal(y, x * w.astype(np.float32))
+
+
+def test_silu_mul_values_vs_fp64(orc):
+    rng = np.random.default_rng(8)
+    g = (rng.standard_normal(4096) * 3).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    y = orc.silu_mul_values(g, u)
+    gd = g.astype(np.float64)
+    ref = gd / (1 + np.exp(-gd)) * u
+    assert np.allclose(y, ref, rtol=3e-7, atol=1e-30)
+    # silu(0) = 0; silu(g) = g in fp32 once exp(-g) < 2^-24
+    z = orc.silu_mul_values(np.array([0.0, 20.0, 30.0], np.float32), np.array([5.0, 3.0, -2.0], np.float32))
+    assert np.array_equal(z, np.array([0.0, 60.0, -60.0], np.float32))
