@@ -121,6 +121,19 @@ class FusedQuantGemm {
                              const void *act_q8_1, int M, int K, hipStream_t stream,
                              const NativeExecutionPolicy *policy = nullptr);
 
+  // fused_quant_gemm.h:281-307: silu(gate . a) * (up . a) in one launch, fp16
+  // out; the WithEpilogue variant also writes the Q8_1 blocks of the result
+  // (act_q8_1_out, may be null) for the down projection.  M <= 2 and N %
+  // 32 == 0 (else false: grouped GEMV + SiluMulQuantizeQ8_1).
+  static bool FusedGateUpSiluGemvQ8_1(const QuantizedWeightInfo &gate_raw,
+                                      const QuantizedWeightInfo &up_raw, const void *act_q8_1,
+                                      uint16_t *output, int M, int N, int K, hipStream_t stream);
+  static bool FusedGateUpSiluGemvQ8_1WithEpilogue(const QuantizedWeightInfo &gate_raw,
+                                                  const QuantizedWeightInfo &up_raw,
+                                                  const void *act_q8_1, uint16_t *output,
+                                                  void *act_q8_1_out, int M, int N, int K,
+                                                  hipStream_t stream);
+
   // fused_quant_gemm.h:333.
   static bool SupportsQ8_1Activations(int quant_type);
   // fused_quant_gemm.h:343-348 and .cu:830-880, re-derived for gfx950.

@@ -102,6 +102,21 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
                       const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                       void *stream);
 
+/* Fused gate/up GEMV with SiLU: h[m][o] = silu(W_gate[o] . a[m]) *
+ * (W_up[o] . a[m]), written to H [M][N] (fp32 or fp16, h_dtype; may be
+ * NULL) and/or quantized to Q8_1 blocks of 32 consecutive outputs in
+ * q8_1_out [M][N/32] (may be NULL; not both), ready for the down
+ * projection without a separate quantize launch.  Handles 1 <= M <= 2 and
+ * N % 32 == 0; other shapes return IFX_BAD_GEOMETRY (not handled: use
+ * ifx_qgemv_grouped + ifx_silu_mul_quantize_q8_1).
+ * Replaces FusedQuantGemm::FusedGateUpSiluGemvQ8_1 and
+ * FusedGateUpSiluGemvQ8_1WithEpilogue (fused_quant_gemm.h:281-307; kernels
+ * mmvq.cuh:1686-2030), whose Q8_1 epilogue writes a per-element scale; this
+ * one writes whole Q8_1 blocks. */
+int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
+                           const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
+                           int N, int K, void *stream);
+
 /* The prefill GEMM alone (int8 MFMA, fp32 accumulate), for any M >= 1.
  * Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
  * (quantized_weight_map.cpp:176-233, cublas_gemm.h:47, called at

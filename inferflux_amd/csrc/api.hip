@@ -26,6 +26,8 @@ hipError_t launch_gemv(int qtype, const void *W, const void *A, void *Y, const v
 hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void *const *Y,
                                const int *N, const void *A, bool f16, int M, int K, int mode,
                                hipStream_t stream);
+hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const void *A, void *H,
+                              bool f16h, void *Q, int M, int N, int K, hipStream_t stream);
 hipError_t launch_mmvq(int qtype, int count, const void *const *W, void *const *Y,
                        const int *N, const void *bias, const void *A, bool f16, int M, int K,
                        int mode, hipStream_t stream);
@@ -223,6 +225,26 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
     if (rc != IFX_OK) return rc;
   }
   return IFX_OK;
+}
+
+int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
+                           const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
+                           int N, int K, void *stream) {
+  if (!W_gate || !W_up || !A_q8_1 || (!H && !q8_1_out)) return IFX_NULL_POINTER;
+  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  // the fused kernel serves the decode batch M <= 2 and whole Q8_1 blocks
+  // of outputs; other shapes take the grouped GEMV + SiLU producer
+  if (M < 1 || M > 2 || N % 32 != 0) return IFX_BAD_GEOMETRY;
+  // geometry and 32-bit range checks of the GEMV (the output pointer is
+  // only checked for presence)
+  void *probe_out = H ? H : q8_1_out;
+  const int rc = check_gemm_args(quant_type, W_gate, A_q8_1, probe_out, IFX_OUT_F32, IFX_STORE,
+                                 nullptr, M, N, K);
+  if (rc != IFX_OK) return rc;
+  return status_of(ifx::launch_gemv_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
+                                           h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,

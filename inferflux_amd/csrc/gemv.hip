@@ -26,7 +26,7 @@
 //    the G waves of the group through LDS.
 //  * Q4_K: the 16-byte super-block header is loaded by one of the eight
 //    lanes that share it and broadcast to the others with DPP.
-#include "ifx_common.h"
+#include "ifx_q8_1.h"
 
 #include <stdlib.h>
 
@@ -40,7 +40,7 @@ enum OutMode { kOutStore = 0, kOutAccum = 1, kOutBias = 2 };
 // (high nibbles), p = j >> 1.
 // ---------------------------------------------------------------------------
 template <int MC, int R>
-__device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (&rows)[R],
+__device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
                                           uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
   const int b = s >> 3, j = s & 7, p = j >> 1, h = j & 1;
   // weights first: all R rows in flight before anything waits.  rows[r] is
@@ -52,8 +52,8 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
     // the 16-byte header is loaded by one lane of the eight that share the
     // super-block (lane & 7 == 0, i.e. j == 0) and broadcast to the others
     hdr[r] = u32x4{0, 0, 0, 0};
-    if (j == 0) hdr[r] = wload<u32x4>(Wr, wo, rows[r]);
-    q[r] = wload<u32x4>(Wr, wo + 16 + 16 * j, rows[r]);
+    if (j == 0) hdr[r] = wload<u32x4>(Wr[r], wo, rows[r]);
+    q[r] = wload<u32x4>(Wr[r], wo + 16 + 16 * j, rows[r]);
   }
   // activations: Q8_1 blocks (b*8 + 2p) and (b*8 + 2p + 1), bytes 16h..16h+15
   i32x4 xa[MC], xb[MC];
@@ -126,7 +126,7 @@ __device__ __forceinline__ void q4k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
 // (sub-blocks cc and cc + 2), values 16h..16h+15 (h = j & 1).
 // ---------------------------------------------------------------------------
 template <int MC, int R>
-__device__ __forceinline__ void q6k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (&rows)[R],
+__device__ __forceinline__ void q6k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
                                           uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
   const int b = s >> 3, j = s & 7, g = j >> 2, cc = (j >> 1) & 1, h = j & 1;
   u32x4 ql[R], qh[R];
@@ -135,10 +135,10 @@ __device__ __forceinline__ void q6k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
   const uint32_t wo = b * kQ6KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    ql[r] = wload<u32x4>(Wr, wo + g * 64 + cc * 32 + 16 * h, rows[r]);
-    qh[r] = wload<u32x4>(Wr, wo + 128 + g * 32 + 16 * h, rows[r]);
-    scw[r] = wload<u32x2>(Wr, wo + 192 + g * 8, rows[r]);
-    dbits[r] = wload<uint16_t>(Wr, wo + 208, rows[r]);
+    ql[r] = wload<u32x4>(Wr[r], wo + g * 64 + cc * 32 + 16 * h, rows[r]);
+    qh[r] = wload<u32x4>(Wr[r], wo + 128 + g * 32 + 16 * h, rows[r]);
+    scw[r] = wload<u32x2>(Wr[r], wo + 192 + g * 8, rows[r]);
+    dbits[r] = wload<uint16_t>(Wr[r], wo + 208, rows[r]);
   }
   i32x4 xa[MC], xb[MC];
   float da[MC], db[MC];
@@ -202,16 +202,16 @@ __device__ __forceinline__ void q6k_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (
 // Q8_0: slice s is block s of the row (34 bytes: fp16 d, 32 int8 codes).
 // ---------------------------------------------------------------------------
 template <int MC, int R>
-__device__ __forceinline__ void q8_0_slice(rsrc_t Wr, rsrc_t Ar, const uint32_t (&rows)[R],
+__device__ __forceinline__ void q8_0_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
                                            uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
   i32x4 w0[R], w1[R];
   uint16_t dbits[R];
   const uint32_t wo = s * kQ8_0Bytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    dbits[r] = wload<uint16_t>(Wr, wo, rows[r]);
-    w0[r] = wload<i32x4>(Wr, wo + 2, rows[r]);
-    w1[r] = wload<i32x4>(Wr, wo + 18, rows[r]);
+    dbits[r] = wload<uint16_t>(Wr[r], wo, rows[r]);
+    w0[r] = wload<i32x4>(Wr[r], wo + 2, rows[r]);
+    w1[r] = wload<i32x4>(Wr[r], wo + 18, rows[r]);
   }
   i32x4 x0[MC], x1[MC];
   float da[MC];
@@ -295,8 +295,12 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const rsrc_t Ar = make_rsrc(args.A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
 
   uint32_t rows[R];  // byte offset of each row (rows past N repeat row N-1)
+  rsrc_t Wrs[R];     // the tensor each row is read from
 #pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = static_cast<uint32_t>(min(row0 + r, N - 1)) * w_row;
+  for (int r = 0; r < R; ++r) {
+    rows[r] = static_cast<uint32_t>(min(row0 + r, N - 1)) * w_row;
+    Wrs[r] = Wr;
+  }
 
   float acc[R][MC];
 #pragma unroll
@@ -307,11 +311,11 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const int nslice = K >> 5;
   for (int s = gw * 64 + lane; s < nslice; s += 64 * G) {
     if constexpr (QT == kTypeQ4_K)
-      q4k_slice<MC, R>(Wr, Ar, rows, a_row, mvalid, s, acc);
+      q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
-      q6k_slice<MC, R>(Wr, Ar, rows, a_row, mvalid, s, acc);
+      q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else
-      q8_0_slice<MC, R>(Wr, Ar, rows, a_row, mvalid, s, acc);
+      q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }
 
   // Sum each partial over the wave (DPP adds, no LDS); lane 63 ends with
@@ -426,6 +430,121 @@ static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStre
   case kTypeQ4_K: launch_type<kTypeQ4_K>(args, f16, stream); break;
   case kTypeQ6_K: launch_type<kTypeQ6_K>(args, f16, stream); break;
   case kTypeQ8_0: launch_type<kTypeQ8_0>(args, f16, stream); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Fused gate/up GEMV with SiLU(gate) * up and a Q8_1 epilogue (replaces the
+// reference's FusedGateUpSiluGemvQ8_1[WithEpilogue], mmvq.cuh:1686-2030):
+// h[m][o] = silu(gate[o] . a[m]) * (up[o] . a[m]), written as fp32/fp16
+// and/or as Q8_1 blocks of 32 consecutive outputs, ready for the down
+// projection.  A workgroup of 16 waves owns 32 consecutive outputs (one Q8_1
+// block per batch column): wave w computes outputs 2w and 2w+1 from the
+// rows gate[o], gate[o+1], up[o], up[o+1] (one lane per 32-value slice),
+// puts its h values in LDS, and after one barrier 8 lanes per batch column
+// quantize the block with the standard quantizer.  (The reference's
+// epilogue writes a per-element scale; this one is the full Q8_1 block.)
+// ---------------------------------------------------------------------------
+template <int QT, int MC, bool F16H>
+__global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict__ Wg,
+                                                      const uint8_t *__restrict__ Wu,
+                                                      const uint8_t *__restrict__ A,
+                                                      void *__restrict__ H,
+                                                      uint8_t *__restrict__ Q, int M, int N,
+                                                      int K) {
+  constexpr int R = 4, V = R * MC;
+  __shared__ float hb[MC][32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int o0 = blockIdx.x * 32 + 2 * wave;  // this wave's two outputs
+  const int col0 = blockIdx.y * MC;
+  const int mvalid = min(MC, M - col0);
+  const int nslice = K >> 5;
+  const uint32_t a_row = static_cast<uint32_t>(nslice) * kQ8_1Bytes;
+  const uint32_t w_row = (QT == kTypeQ4_K)   ? static_cast<uint32_t>(K >> 8) * kQ4KBytes
+                         : (QT == kTypeQ6_K) ? static_cast<uint32_t>(K >> 8) * kQ6KBytes
+                                             : static_cast<uint32_t>(nslice) * kQ8_0Bytes;
+  const rsrc_t Wgr = make_rsrc(Wg, w_row * static_cast<uint32_t>(N));
+  const rsrc_t Wur = make_rsrc(Wu, w_row * static_cast<uint32_t>(N));
+  const rsrc_t Ar = make_rsrc(A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
+  const uint32_t r0 = static_cast<uint32_t>(o0) * w_row;
+  const uint32_t rows[R] = {r0, r0 + w_row, r0, r0 + w_row};
+  const rsrc_t Wrs[R] = {Wgr, Wgr, Wur, Wur};
+
+  float acc[R][MC];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MC; ++c) acc[r][c] = 0.0f;
+  for (int s = lane; s < nslice; s += 64) {
+    if constexpr (QT == kTypeQ4_K)
+      q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ6_K)
+      q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else
+      q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+  }
+  float v[V];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MC; ++c) v[r * MC + c] = wave_sum_to63(acc[r][c]);
+  if (lane == 63) {
+#pragma unroll
+    for (int c = 0; c < MC; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float gsum = v[t * MC + c], usum = v[(2 + t) * MC + c];
+        const float h = materialize_f32(gsum / (1.0f + expf(-gsum))) * usum;
+        hb[c][2 * wave + t] = h;
+        if (H && c < mvalid) {
+          const int64_t o = static_cast<int64_t>(col0 + c) * N + o0 + t;
+          if constexpr (F16H) static_cast<uint16_t *>(H)[o] = static_cast<uint16_t>(f2h_bits(h));
+          else static_cast<float *>(H)[o] = h;
+        }
+      }
+  }
+  if (Q) {
+    __syncthreads();
+    // whole groups of 8 lanes per batch column (quantizer shuffles stay inside)
+    const int c = threadIdx.x >> 3, l = threadIdx.x & 7;
+    if (c < mvalid) {
+      const f32x4 h4 = *reinterpret_cast<const f32x4 *>(&hb[c][4 * l]);
+      quantize4_store(h4.x, h4.y, h4.z, h4.w,
+                      Q + (static_cast<int64_t>(col0 + c) * (N >> 5) + blockIdx.x) * kQ8_1Bytes, l);
+    }
+  }
+}
+
+template <int QT, int MC>
+static void launch_swiglu_mc(const uint8_t *Wg, const uint8_t *Wu, const uint8_t *A, void *H,
+                             bool f16h, uint8_t *Q, int M, int N, int K, hipStream_t s) {
+  const dim3 grid(N / 32, (M + MC - 1) / MC);
+  if (f16h)
+    hipLaunchKernelGGL((k_gemv_swiglu<QT, MC, true>), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
+  else
+    hipLaunchKernelGGL((k_gemv_swiglu<QT, MC, false>), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
+}
+
+template <int QT>
+static void launch_swiglu_t(const uint8_t *Wg, const uint8_t *Wu, const uint8_t *A, void *H,
+                            bool f16h, uint8_t *Q, int M, int N, int K, hipStream_t s) {
+  if (M == 1) launch_swiglu_mc<QT, 1>(Wg, Wu, A, H, f16h, Q, M, N, K, s);
+  else launch_swiglu_mc<QT, 2>(Wg, Wu, A, H, f16h, Q, M, N, K, s);
+}
+
+// 1 <= M <= 2, N % 32 == 0, K as for launch_gemv (checked by the caller).
+hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const void *A, void *H,
+                              bool f16h, void *Q, int M, int N, int K, hipStream_t stream) {
+  const uint8_t *g = static_cast<const uint8_t *>(Wg), *u = static_cast<const uint8_t *>(Wu);
+  const uint8_t *a = static_cast<const uint8_t *>(A);
+  uint8_t *q = static_cast<uint8_t *>(Q);
+  switch (qtype) {
+  case kTypeQ4_K: launch_swiglu_t<kTypeQ4_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
+  case kTypeQ6_K: launch_swiglu_t<kTypeQ6_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
+  case kTypeQ8_0: launch_swiglu_t<kTypeQ8_0>(g, u, a, H, f16h, q, M, N, K, stream); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

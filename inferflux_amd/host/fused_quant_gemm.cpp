@@ -168,6 +168,26 @@ bool FusedQuantGemm::GemvQ8_1Triple(const std::array<PackedProjectionSpec, 3> &p
   return LaunchGroup(projections, act_q8_1, M, K, stream, policy);
 }
 
+bool FusedQuantGemm::FusedGateUpSiluGemvQ8_1(const QuantizedWeightInfo &gate_raw,
+                                             const QuantizedWeightInfo &up_raw,
+                                             const void *act_q8_1, uint16_t *output, int M,
+                                             int N, int K, hipStream_t stream) {
+  return FusedGateUpSiluGemvQ8_1WithEpilogue(gate_raw, up_raw, act_q8_1, output, nullptr, M, N, K,
+                                             stream);
+}
+
+bool FusedQuantGemm::FusedGateUpSiluGemvQ8_1WithEpilogue(const QuantizedWeightInfo &gate_raw,
+                                                         const QuantizedWeightInfo &up_raw,
+                                                         const void *act_q8_1, uint16_t *output,
+                                                         void *act_q8_1_out, int M, int N, int K,
+                                                         hipStream_t stream) {
+  if (!Usable(gate_raw, act_q8_1, output) || !Usable(up_raw, act_q8_1, output)) return false;
+  if (gate_raw.quant_type != up_raw.quant_type) return false;
+  if (!ViewCovers(gate_raw, N, K) || !ViewCovers(up_raw, N, K)) return false;
+  return ifx_qgemv_gate_up_silu(gate_raw.quant_type, gate_raw.data, up_raw.data, act_q8_1, output,
+                                IFX_OUT_F16, act_q8_1_out, M, N, K, stream) == IFX_OK;
+}
+
 bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
   return quant_type == static_cast<int>(TensorType::Q4_K) ||
          quant_type == static_cast<int>(TensorType::Q6_K) ||

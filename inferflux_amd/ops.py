@@ -155,6 +155,31 @@ def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mo
     return outs
 
 
+def qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, h_out=None, q8_1_out=None, want_h=True,
+                       want_q8_1=True, h_dtype=torch.float32, stream=None):
+    """h = silu(Wg . a) * (Wu . a) for M <= 2 in one launch; returns
+    (h [M, N] or None, Q8_1 [M, N/32*36] or None)."""
+    if want_h and h_out is None:
+        h_out = torch.empty((M, N), dtype=h_dtype, device=A.device)
+    if want_q8_1 and q8_1_out is None:
+        q8_1_out = torch.empty((M, N // 32 * 36), dtype=torch.uint8, device=A.device)
+    for W in (Wg, Wu):
+        if W.numel() < weight_bytes(qtype, N, K):
+            raise ValueError("W is smaller than N x K blocks")
+    if h_out is not None and (h_out.numel() < M * N or
+                              h_out.dtype not in (torch.float32, torch.float16)):
+        raise ValueError("bad h output")
+    if q8_1_out is not None and q8_1_out.numel() < M * (N // 32) * 36:
+        raise ValueError("bad Q8_1 output")
+    hd = OUT_F16 if h_out is not None and h_out.dtype == torch.float16 else OUT_F32
+    rc = _lib.load().ifx_qgemv_gate_up_silu(
+        qtype, _dev(Wg, "Wg"), _dev(Wu, "Wu"), _dev(A, "A"),
+        _dev(h_out, "h") if h_out is not None else None, hd,
+        _dev(q8_1_out, "q8_1_out") if q8_1_out is not None else None, M, N, K, _stream(stream))
+    _check(rc, "ifx_qgemv_gate_up_silu")
+    return h_out, q8_1_out
+
+
 def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None):
     out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)
     od = OUT_F16 if out_dtype == torch.float16 else OUT_F32
