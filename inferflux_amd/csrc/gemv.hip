@@ -10,9 +10,16 @@
 // s = d*sum(q) field (mmvq.cuh:121-125).
 //
 // Work mapping (wave64, memory bound):
-//  * A "slice" is 32 weights of one row: 16 bytes of Q4_K qs (two half
-//    sub-blocks), 16 bytes of Q6_K ql plus the matching 16 bytes of qh, or
-//    one whole Q8_0 block.  A row has K/32 slices.
+//  * A "slice" is the run of weights one lane owns.  At M <= 2 (Q6_K: M = 1)
+//    Q4_K and Q6_K use wide 64-value slices (32 bytes of Q4_K qs = one
+//    sub-block pair; 32 bytes of Q6_K ql + the 16 bytes of qh they share):
+//    the kernel is VALU co-limited there, and the per-slice costs (header
+//    broadcast, scale/min decode, activation scales) are paid once per 64
+//    weights.  Otherwise a slice is 32 weights: 16 bytes of Q4_K qs (two
+//    half sub-blocks), 16 bytes of Q6_K ql plus the matching 16 bytes of
+//    qh, or one whole Q8_0 block.
+//  * Half-wave mode (wide slices, K <= 2048, i.e. at most 32 slices a row):
+//    lanes 0-31 and 32-63 own different rows, so no lane idles.
 //  * A row group of R consecutive rows is owned by G waves (G = 1..4 by K,
 //    so that 64*G lanes roughly cover K/32 slices); lane t of the group
 //    takes slices t, t + 64G, ...  For each slice a lane loads the
@@ -60,18 +67,12 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
   float da[MC], db[MC], sa[MC], sbv[MC];
 #pragma unroll
   for (int c = 0; c < MC; ++c) {
-    if (c < mvalid) {
+    if (c == 0 || c < mvalid) {  // mvalid >= 1
       const uint32_t ao = (b * 8 + 2 * p) * kQ8_1Bytes;
-#ifdef IFX_EXP_NOA
-      const uint32_t dsa = 0x3C003C00u ^ ao, dsb = 0x3C003C00u ^ (ao << 3);
-      xa[c] = i32x4{static_cast<int>(ao), s, 3, 5};
-      xb[c] = i32x4{s, static_cast<int>(ao), 7, 1};
-#else
       const uint32_t dsa = bload<uint32_t>(Ar, ao, c * a_row);
       const uint32_t dsb = bload<uint32_t>(Ar, ao + kQ8_1Bytes, c * a_row);
       xa[c] = bload<i32x4>(Ar, ao + 4 + 16 * h, c * a_row);
       xb[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 4 + 16 * h, c * a_row);
-#endif
       da[c] = h2f(dsa & 0xFFFFu);
       db[c] = h2f(dsb & 0xFFFFu);
       // the min term is per 32-value sub-block: only the h == 0 lane adds it
@@ -83,6 +84,8 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
     }
   }
   const int shift = 8 * ((2 * p) & 3);
+  const uint32_t lo_mask = p < 2 ? 0x3F3F3F3Fu : 0x0F0F0F0Fu;
+  const uint32_t top_mask = p < 2 ? 0u : 0x30303030u;
 #pragma unroll
   for (int r = 0; r < R; ++r)
     hdr[r] = u32x4{bcast8(hdr[r].x), bcast8(hdr[r].y), bcast8(hdr[r].z), bcast8(hdr[r].w)};
@@ -92,15 +95,17 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
     const float dmin = h2f(hdr[r].x >> 16);
     // 6-bit scale/min unpack (quant_common.cuh:83-94) for 4 sub-blocks per
     // dword: sub-blocks 0-3 from bytes 0-7, 4-7 from bytes 8-11 + top bits.
+    // Branch-free: the low bits come from S0/S1 (p < 2, six bits) or from
+    // the nibbles of S2 (p >= 2, plus the top two bits of S0/S1); the
+    // masks are per-lane constants.
     const uint32_t S0 = hdr[r].y, S1 = hdr[r].z, S2 = hdr[r].w;
-    const uint32_t scw = (p < 2) ? (S0 & 0x3F3F3F3Fu)
-                                 : ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u));
-    const uint32_t mw = (p < 2) ? (S1 & 0x3F3F3F3Fu)
-                                : (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u));
-    const float dsc0 = d * static_cast<float>((scw >> shift) & 0xFFu);
-    const float dsc1 = d * static_cast<float>((scw >> (shift + 8)) & 0xFFu);
-    const float dm0 = dmin * static_cast<float>((mw >> shift) & 0xFFu);
-    const float dm1 = dmin * static_cast<float>((mw >> (shift + 8)) & 0xFFu);
+    const uint32_t scw = ((p < 2 ? S0 : S2) & lo_mask) | ((S0 >> 2) & top_mask);
+    const uint32_t mw = ((p < 2 ? S1 : (S2 >> 4)) & lo_mask) | ((S1 >> 2) & top_mask);
+    const uint32_t sct = scw >> shift, mt = mw >> shift;
+    const float dsc0 = d * static_cast<float>(sct & 0xFFu);
+    const float dsc1 = d * static_cast<float>((sct >> 8) & 0xFFu);
+    const float dm0 = dmin * static_cast<float>(mt & 0xFFu);
+    const float dm1 = dmin * static_cast<float>((mt >> 8) & 0xFFu);
     const int lo0 = q[r].x & 0x0F0F0F0F, hi0 = (q[r].x >> 4) & 0x0F0F0F0F;
     const int lo1 = q[r].y & 0x0F0F0F0F, hi1 = (q[r].y >> 4) & 0x0F0F0F0F;
     const int lo2 = q[r].z & 0x0F0F0F0F, hi2 = (q[r].z >> 4) & 0x0F0F0F0F;
@@ -115,6 +120,89 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
       dh = dot4(hi1, xb[c].y, dh);
       dh = dot4(hi2, xb[c].z, dh);
       dh = dot4(hi3, xb[c].w, dh);
+      acc[r][c] += dsc0 * da[c] * static_cast<float>(dl) + dsc1 * db[c] * static_cast<float>(dh) -
+                   (dm0 * sa[c] + dm1 * sbv[c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K, wide slices (MC <= 2): slice w (0..3) of super-block b covers qs
+// bytes 32w..32w+31, i.e. all 32 values of sub-blocks 2w (low nibbles) and
+// 2w+1 (high nibbles).  One lane per 64 weights: the header broadcast, the
+// 6-bit scale/min decode and the min term are paid once per 32 bytes
+// instead of once per 16 (the GEMV is VALU co-limited at M <= 2).  The row
+// of load r is at voff[r] + soff[r] (one of the two is zero: per-lane rows
+// in half-wave mode, wave-uniform rows otherwise).
+// ---------------------------------------------------------------------------
+template <int MC, int R>
+__device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
+                                         const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
+                                         int s, float (&acc)[R][MC]) {
+  const int b = s >> 2, w = s & 3;
+  u32x4 hdr[R], q0[R], q1[R];
+  const uint32_t wo = b * kQ4KBytes;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // header: loaded by the w == 0 lane of each quad, broadcast below
+    hdr[r] = u32x4{0, 0, 0, 0};
+    if (w == 0) hdr[r] = wload<u32x4>(Wr, voff[r] + wo, soff[r]);
+    q0[r] = wload<u32x4>(Wr, voff[r] + wo + 16 + 32 * w, soff[r]);
+    q1[r] = wload<u32x4>(Wr, voff[r] + wo + 32 + 32 * w, soff[r]);
+  }
+  // activations: Q8_1 blocks 8b + 2w and 8b + 2w + 1, all 32 codes of each
+  i32x4 xa0[MC], xa1[MC], xb0[MC], xb1[MC];
+  float da[MC], db[MC], sa[MC], sbv[MC];
+#pragma unroll
+  for (int c = 0; c < MC; ++c) {
+    if (c == 0 || c < mvalid) {  // mvalid >= 1
+      const uint32_t ao = (b * 8 + 2 * w) * kQ8_1Bytes;
+      const uint32_t dsa = bload<uint32_t>(Ar, ao, c * a_row);
+      const uint32_t dsb = bload<uint32_t>(Ar, ao + kQ8_1Bytes, c * a_row);
+      xa0[c] = bload<i32x4>(Ar, ao + 4, c * a_row);
+      xa1[c] = bload<i32x4>(Ar, ao + 20, c * a_row);
+      xb0[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 4, c * a_row);
+      xb1[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 20, c * a_row);
+      da[c] = h2f(dsa & 0xFFFFu);
+      db[c] = h2f(dsb & 0xFFFFu);
+      sa[c] = h2f(dsa >> 16);
+      sbv[c] = h2f(dsb >> 16);
+    } else {
+      xa0[c] = xa1[c] = xb0[c] = xb1[c] = i32x4{0, 0, 0, 0};
+      da[c] = db[c] = sa[c] = sbv[c] = 0.0f;
+    }
+  }
+  const int shift = 8 * ((2 * w) & 3);
+  const uint32_t lo_mask = w < 2 ? 0x3F3F3F3Fu : 0x0F0F0F0Fu;
+  const uint32_t top_mask = w < 2 ? 0u : 0x30303030u;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    hdr[r] = u32x4{dpp<0x00>(0u, hdr[r].x), dpp<0x00>(0u, hdr[r].y), dpp<0x00>(0u, hdr[r].z),
+                   dpp<0x00>(0u, hdr[r].w)};  // quad_perm [0,0,0,0]
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float d = h2f(hdr[r].x & 0xFFFFu);
+    const float dmin = h2f(hdr[r].x >> 16);
+    // 6-bit scale/min unpack (quant_common.cuh:83-94), branch-free
+    const uint32_t S0 = hdr[r].y, S1 = hdr[r].z, S2 = hdr[r].w;
+    const uint32_t scw = ((w < 2 ? S0 : S2) & lo_mask) | ((S0 >> 2) & top_mask);
+    const uint32_t mw = ((w < 2 ? S1 : (S2 >> 4)) & lo_mask) | ((S1 >> 2) & top_mask);
+    const uint32_t sct = scw >> shift, mt = mw >> shift;
+    const float dsc0 = d * static_cast<float>(sct & 0xFFu);
+    const float dsc1 = d * static_cast<float>((sct >> 8) & 0xFFu);
+    const float dm0 = dmin * static_cast<float>(mt & 0xFFu);
+    const float dm1 = dmin * static_cast<float>((mt >> 8) & 0xFFu);
+    const uint32_t qv[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+#pragma unroll
+    for (int c = 0; c < MC; ++c) {
+      const int xa[8] = {xa0[c].x, xa0[c].y, xa0[c].z, xa0[c].w, xa1[c].x, xa1[c].y, xa1[c].z, xa1[c].w};
+      const int xb[8] = {xb0[c].x, xb0[c].y, xb0[c].z, xb0[c].w, xb1[c].x, xb1[c].y, xb1[c].z, xb1[c].w};
+      int dl = 0, dh = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dl = dot4(static_cast<int>(qv[i] & 0x0F0F0F0Fu), xa[i], dl);
+        dh = dot4(static_cast<int>((qv[i] >> 4) & 0x0F0F0F0Fu), xb[i], dh);
+      }
       acc[r][c] += dsc0 * da[c] * static_cast<float>(dl) + dsc1 * db[c] * static_cast<float>(dh) -
                    (dm0 * sa[c] + dm1 * sbv[c]);
     }
@@ -145,7 +233,7 @@ __device__ __forceinline__ void q6k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
   int suma[MC], sumb[MC];
 #pragma unroll
   for (int c = 0; c < MC; ++c) {
-    if (c < mvalid) {
+    if (c == 0 || c < mvalid) {  // mvalid >= 1
       const uint32_t ao = (b * 8 + g * 4 + cc) * kQ8_1Bytes, bo = ao + 2 * kQ8_1Bytes;
       xa[c] = bload<i32x4>(Ar, ao + 4 + 16 * h, c * a_row);
       xb[c] = bload<i32x4>(Ar, bo + 4 + 16 * h, c * a_row);
@@ -199,6 +287,92 @@ __device__ __forceinline__ void q6k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K, wide slices (MC <= 2): slice w (0..3) of super-block b is half
+// g = w >> 1 (values 128g..128g+127) and sub-range h = w & 1: qh bytes
+// 32g + 16h.. (16 bytes, each holding the top bits of 4 values) and the ql
+// bytes 64g + 16h.. and 64g + 32 + 16h.. they pair with, i.e. values
+// 128g + 32k + 16h + i for k = 0..3, i = 0..15 (scale 8g + 2k + h, Q8_1
+// block 8b + 4g + k).  One lane per 64 weights; qh is read once.
+// ---------------------------------------------------------------------------
+template <int MC, int R>
+__device__ __forceinline__ void q6k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
+                                         const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
+                                         int s, float (&acc)[R][MC]) {
+  const int b = s >> 2, g = (s >> 1) & 1, h = s & 1;
+  u32x4 ql0[R], ql1[R], qh[R];
+  u32x2 scw[R];
+  uint16_t dbits[R];
+  const uint32_t wo = b * kQ6KBytes;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    ql0[r] = wload<u32x4>(Wr, voff[r] + wo + g * 64 + 16 * h, soff[r]);
+    ql1[r] = wload<u32x4>(Wr, voff[r] + wo + g * 64 + 32 + 16 * h, soff[r]);
+    qh[r] = wload<u32x4>(Wr, voff[r] + wo + 128 + g * 32 + 16 * h, soff[r]);
+    scw[r] = wload<u32x2>(Wr, voff[r] + wo + 192 + g * 8, soff[r]);
+    dbits[r] = wload<uint16_t>(Wr, voff[r] + wo + 208, soff[r]);
+  }
+  i32x4 x[4][MC];
+  float da[4][MC];
+  int sum32[4][MC];  // 32 * sum of the 16 activation codes (the -32 offset)
+#pragma unroll
+  for (int c = 0; c < MC; ++c) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (c == 0 || c < mvalid) {  // mvalid >= 1
+        const uint32_t ao = (b * 8 + g * 4 + k) * kQ8_1Bytes;
+        x[k][c] = bload<i32x4>(Ar, ao + 4 + 16 * h, c * a_row);
+        da[k][c] = h2f(bload<uint16_t>(Ar, ao, c * a_row));
+        int sm = dot4(0x01010101, x[k][c].x, 0);
+        sm = dot4(0x01010101, x[k][c].y, sm);
+        sm = dot4(0x01010101, x[k][c].z, sm);
+        sm = dot4(0x01010101, x[k][c].w, sm);
+        sum32[k][c] = 32 * sm;
+      } else {
+        x[k][c] = i32x4{0, 0, 0, 0};
+        da[k][c] = 0.0f;
+        sum32[k][c] = 0;
+      }
+    }
+  }
+  const int scs = 8 * h;  // scale byte h (k = 0, 2) or h + 2 (k = 1, 3) of its dword
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float d = h2f(dbits[r]);
+    // scales[8g + 2k + h]: dword 0 holds k = 0 (byte h) and k = 1 (byte h + 2),
+    // dword 1 holds k = 2 and k = 3
+    float dsk[4];
+    dsk[0] = d * static_cast<float>(static_cast<int8_t>((scw[r].x >> scs) & 0xFFu));
+    dsk[1] = d * static_cast<float>(static_cast<int8_t>((scw[r].x >> (scs + 16)) & 0xFFu));
+    dsk[2] = d * static_cast<float>(static_cast<int8_t>((scw[r].y >> scs) & 0xFFu));
+    dsk[3] = d * static_cast<float>(static_cast<int8_t>((scw[r].y >> (scs + 16)) & 0xFFu));
+    const uint32_t l0[4] = {ql0[r].x, ql0[r].y, ql0[r].z, ql0[r].w};
+    const uint32_t l1[4] = {ql1[r].x, ql1[r].y, ql1[r].z, ql1[r].w};
+    const uint32_t hv[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
+    int v[4][4];  // 6-bit codes of value group k, dword i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[0][i] = static_cast<int>((l0[i] & 0x0F0F0F0Fu) | ((hv[i] << 4) & 0x30303030u));
+      v[1][i] = static_cast<int>((l1[i] & 0x0F0F0F0Fu) | ((hv[i] << 2) & 0x30303030u));
+      v[2][i] = static_cast<int>(((l0[i] >> 4) & 0x0F0F0F0Fu) | (hv[i] & 0x30303030u));
+      v[3][i] = static_cast<int>(((l1[i] >> 4) & 0x0F0F0F0Fu) | ((hv[i] >> 2) & 0x30303030u));
+    }
+#pragma unroll
+    for (int c = 0; c < MC; ++c) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        int dt = dot4(v[k][0], x[k][c].x, -sum32[k][c]);
+        dt = dot4(v[k][1], x[k][c].y, dt);
+        dt = dot4(v[k][2], x[k][c].z, dt);
+        dt = dot4(v[k][3], x[k][c].w, dt);
+        sum += dsk[k] * da[k][c] * static_cast<float>(dt);
+      }
+      acc[r][c] += sum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q8_0: slice s is block s of the row (34 bytes: fp16 d, 32 int8 codes).
 // ---------------------------------------------------------------------------
 template <int MC, int R>
@@ -217,7 +391,7 @@ __device__ __forceinline__ void q8_0_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, con
   float da[MC];
 #pragma unroll
   for (int c = 0; c < MC; ++c) {
-    if (c < mvalid) {
+    if (c == 0 || c < mvalid) {  // mvalid >= 1
       const uint32_t ao = s * kQ8_1Bytes;
       x0[c] = bload<i32x4>(Ar, ao + 4, c * a_row);
       x1[c] = bload<i32x4>(Ar, ao + 20, c * a_row);
@@ -269,9 +443,19 @@ struct GemvArgs {
   int M, K, mode;
 };
 
-template <int QT, int MC, int R, int G, int P, bool F16OUT>
+// Q4_K with MC <= 2 and Q6_K with MC = 1 use the wide (64-value) slices
+// (Q6_K at MC = 2 is faster with 32-value slices: fewer registers).  H = 2 (half-wave
+// mode, wide slices, K <= 2048 so that one row needs at most 32 lanes):
+// lanes 0-31 and 32-63 own different sets of R rows.
+template <int QT, int MC>
+constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) || (QT == kTypeQ6_K && MC == 1);
+
+template <int QT, int MC, int R, int G, int P, bool F16OUT, int H>
 __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
+  static_assert(H == 1 || (G == 1 && kWide<QT, MC>), "half-wave mode: wide slices, one wave per row group");
   constexpr int V = R * MC;  // partial sums per lane; a power of two <= 64
+  constexpr int LPR = 64 / H;                       // lanes per row set
+  constexpr int SV = kWide<QT, MC> ? 64 : 32;       // values per slice
   __shared__ float red[(G > 1) ? P * G * V : 1];
   const int bx = blockIdx.x;
   const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
@@ -283,7 +467,9 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int gw = wave % G;   // wave within its row group
   const int grp = wave / G;  // row group within the workgroup
-  const int row0 = ((bx - sg.blk_begin) * P + grp) * R;
+  const int half = (H == 2) ? (lane >> 5) : 0;
+  const int lt = lane & (LPR - 1);  // lane within its row set
+  const int row0 = (((bx - sg.blk_begin) * P + grp) * H + half) * R;
   const int col0 = blockIdx.y * MC;
   const int mvalid = min(MC, M - col0);
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
@@ -301,6 +487,14 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
     rows[r] = static_cast<uint32_t>(min(row0 + r, N - 1)) * w_row;
     Wrs[r] = Wr;
   }
+  // wide slices: row offsets go in voffset when they differ per lane (H = 2),
+  // in soffset when they are wave-uniform
+  uint32_t voff[R], soff[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    voff[r] = (H == 2) ? rows[r] : 0u;
+    soff[r] = (H == 2) ? 0u : rows[r];
+  }
 
   float acc[R][MC];
 #pragma unroll
@@ -308,9 +502,13 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
 #pragma unroll
     for (int c = 0; c < MC; ++c) acc[r][c] = 0.0f;
 
-  const int nslice = K >> 5;
-  for (int s = gw * 64 + lane; s < nslice; s += 64 * G) {
-    if constexpr (QT == kTypeQ4_K)
+  const int nslice = K / SV;
+  for (int s = gw * LPR + lt; s < nslice; s += LPR * G) {
+    if constexpr (kWide<QT, MC> && QT == kTypeQ4_K)
+      q4k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
+    else if constexpr (kWide<QT, MC>)
+      q6k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ4_K)
       q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
       q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
@@ -324,7 +522,8 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int c = 0; c < MC; ++c) v[r * MC + c] = wave_sum_to63(acc[r][c]);
+    for (int c = 0; c < MC; ++c)
+      v[r * MC + c] = (H == 2) ? halfwave_sum_to31(acc[r][c]) : wave_sum_to63(acc[r][c]);
   if constexpr (G > 1) {
     if (lane == 63) {
 #pragma unroll
@@ -340,7 +539,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       v[i] = t;
     }
   } else {
-    if (lane != 63) return;
+    if ((lane & (LPR - 1)) != LPR - 1) return;
   }
 #pragma unroll
   for (int idx = 0; idx < V; ++idx) {
@@ -363,53 +562,75 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   }
 }
 
-template <int QT, int MC, int R, int G>
+template <int QT, int MC, int R, int G, int H = 1>
 static void launch_t(GemvArgs args, bool f16, hipStream_t s) {
   constexpr int P = (G >= 3) ? 1 : 4 / G;
   int blocks = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = blocks;
-    const int groups = (args.seg[i].N + R - 1) / R;
+    const int groups = (args.seg[i].N + H * R - 1) / (H * R);
     blocks += (groups + P - 1) / P;
   }
   const dim3 grid(blocks, (args.M + MC - 1) / MC);
   const dim3 block(64 * G * P);
   if (f16)
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, true>), grid, block, 0, s, args);
+    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, true, H>), grid, block, 0, s, args);
   else
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false>), grid, block, 0, s, args);
+    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false, H>), grid, block, 0, s, args);
 }
 
 template <int QT, int MC, int R>
 static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
-  // waves per row group: enough lanes to cover the K/32 slices, at most 4
-  const int nslice = args.K >> 5;
+  // waves per row group: enough lanes to cover the slices, at most 4; a
+  // row of at most 32 wide slices takes half a wave
+  const int nslice = args.K / (kWide<QT, MC> ? 64 : 32);
   const int g = (nslice + 63) / 64;
+  if constexpr (kWide<QT, MC>) {
+    if (nslice <= 32) {
+      launch_t<QT, MC, R, 1, 2>(args, f16, s);
+      return;
+    }
+  }
   if (g <= 1) launch_t<QT, MC, R, 1>(args, f16, s);
   else if (g == 2) launch_t<QT, MC, R, 2>(args, f16, s);
   else if (g == 3) launch_t<QT, MC, R, 3>(args, f16, s);
   else launch_t<QT, MC, R, 4>(args, f16, s);
 }
 
-// Rows per wave: enough waves to keep ~4 per SIMD in flight on small N, more
-// rows per wave (more bytes in flight per lane) on large N.  Measured on
-// MI355X: N = 2048 -> 1, N = 11008/13824 -> 2, N = 151936 -> 4.
+// Rows per wave (R; a half-wave launch covers 2R): enough waves to keep
+// ~4 per SIMD in flight on small N, more rows per wave (more bytes in
+// flight per lane) on large N.  Measured on MI355X (M = 1 / 2):
+//  * 32-value slices: N = 2048 -> 1 (2 when K >= 8192), N = 11008/13824
+//    -> 2, N = 151936 -> 4;
+//  * wide Q4_K slices: N < 8192 -> 1, else 2 * M rows per wave (4 * M
+//    from N = 65536 on); wide Q6_K slices: R = 2.
 // IFX_GEMV_ROWS in {1, 2, 4, 8} overrides it (tuning; read once).
-static int rows_per_wave(int N) {
+static int rows_env() {
   static const int env = [] {
     const char *e = getenv("IFX_GEMV_ROWS");
     const int v = e ? atoi(e) : 0;
     return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
   }();
-  if (env) return env;
-  return N < 8192 ? 1 : N < 65536 ? 2 : 4;
+  return env;
+}
+
+template <int QT, int MC>
+static int rows_per_wave(int N, int K) {
+  if (rows_env()) return rows_env();
+  if constexpr (kWide<QT, MC> && QT == kTypeQ6_K) return 2;
+  if constexpr (kWide<QT, MC>) {
+    if (N < 8192) return 1;
+    const int h = (K / 64 <= 32) ? 2 : 1;
+    return (N >= 65536 ? 4 : 2) * MC / h;
+  }
+  return N < 8192 ? (K >= 8192 ? 2 : 1) : N < 65536 ? 2 : 4;
 }
 
 template <int QT, int MC>
 static void launch_r(const GemvArgs &args, bool f16, hipStream_t s) {
   int n_total = 0;
   for (int i = 0; i < args.nseg; ++i) n_total += args.seg[i].N;
-  switch (rows_per_wave(n_total)) {
+  switch (rows_per_wave<QT, MC>(n_total, args.K)) {
   case 1: launch_g<QT, MC, 1>(args, f16, s); break;
   case 2: launch_g<QT, MC, 2>(args, f16, s); break;
   case 8: launch_g<QT, MC, 8>(args, f16, s); break;
@@ -510,7 +731,7 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
     __syncthreads();
     // whole groups of 8 lanes per batch column (quantizer shuffles stay inside)
     const int c = threadIdx.x >> 3, l = threadIdx.x & 7;
-    if (c < mvalid) {
+    if (c == 0 || c < mvalid) {  // mvalid >= 1
       const f32x4 h4 = *reinterpret_cast<const f32x4 *>(&hb[c][4 * l]);
       quantize4_store(h4.x, h4.y, h4.z, h4.w,
                       Q + (static_cast<int64_t>(col0 + c) * (N >> 5) + blockIdx.x) * kQ8_1Bytes, l);

@@ -131,6 +131,17 @@ __device__ __forceinline__ float wave_sum_to63(float v) {
   return v;
 }
 
+// Sums over lanes 0-31 and over lanes 32-63 (two independent halves): the
+// first five steps of wave_sum_to63; lane 31 and lane 63 hold the totals.
+__device__ __forceinline__ float halfwave_sum_to31(float v) {
+  v += dppf<0xB1>(v);
+  v += dppf<0x4E>(v);
+  v += dppf<0x141>(v);
+  v += dppf<0x140>(v);
+  v += dppf<0x142, 0xA>(v);
+  return v;
+}
+
 // Lane 8k's value in lanes 8k .. 8k+7 (row_newbcast of lanes 0 and 8 of
 // each 16-lane row into banks 0-1 and 2-3).
 __device__ __forceinline__ uint32_t bcast8(uint32_t v) {
