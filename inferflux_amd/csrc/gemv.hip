@@ -31,8 +31,9 @@
 //  * Partial sums acc[R*MC] are combined across the 64 lanes of a wave with
 //    DPP adds (no LDS traffic; lane 63 ends with the totals), then across
 //    the G waves of the group through LDS.
-//  * Q4_K: the 16-byte super-block header is loaded by one of the eight
-//    lanes that share it and broadcast to the others with DPP.
+//  * Q4_K header (16 bytes per super-block): with 32-value slices it is
+//    loaded by one of the eight lanes that share it and broadcast with DPP;
+//    with wide slices each of the four lanes loads it (measured faster).
 #include "ifx_q8_1.h"
 
 #include <stdlib.h>
@@ -144,9 +145,9 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
   const uint32_t wo = b * kQ4KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    // header: loaded by the w == 0 lane of each quad, broadcast below
-    hdr[r] = u32x4{0, 0, 0, 0};
-    if (w == 0) hdr[r] = wload<u32x4>(Wr, voff[r] + wo, soff[r]);
+    // header: every lane loads its super-block's 16-byte header itself (no
+    // branch, no broadcast; the four lanes' requests hit the same line)
+    hdr[r] = wload<u32x4>(Wr, voff[r] + wo, soff[r]);
     q0[r] = wload<u32x4>(Wr, voff[r] + wo + 16 + 32 * w, soff[r]);
     q1[r] = wload<u32x4>(Wr, voff[r] + wo + 32 + 32 * w, soff[r]);
   }
@@ -175,10 +176,6 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
   const int shift = 8 * ((2 * w) & 3);
   const uint32_t lo_mask = w < 2 ? 0x3F3F3F3Fu : 0x0F0F0F0Fu;
   const uint32_t top_mask = w < 2 ? 0u : 0x30303030u;
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    hdr[r] = u32x4{dpp<0x00>(0u, hdr[r].x), dpp<0x00>(0u, hdr[r].y), dpp<0x00>(0u, hdr[r].z),
-                   dpp<0x00>(0u, hdr[r].w)};  // quad_perm [0,0,0,0]
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float d = h2f(hdr[r].x & 0xFFFFu);
@@ -599,11 +596,13 @@ static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
 
 // Rows per wave (R; a half-wave launch covers 2R): enough waves to keep
 // ~4 per SIMD in flight on small N, more rows per wave (more bytes in
-// flight per lane) on large N.  Measured on MI355X (M = 1 / 2):
+// flight per lane) on large N.  Measured on MI355X with cold weights (each
+// launch reads a copy not in the 256 MB Infinity Cache), M = 1 / 2:
 //  * 32-value slices: N = 2048 -> 1 (2 when K >= 8192), N = 11008/13824
 //    -> 2, N = 151936 -> 4;
-//  * wide Q4_K slices: N < 8192 -> 1, else 2 * M rows per wave (4 * M
-//    from N = 65536 on); wide Q6_K slices: R = 2.
+//  * wide Q4_K slices: half-wave R = 1 for N < 8192, else 2 (4 rows a
+//    wave); full-wave R = M for N < 8192, else 2M;
+//  * wide Q6_K slices: R = 2.
 // IFX_GEMV_ROWS in {1, 2, 4, 8} overrides it (tuning; read once).
 static int rows_env() {
   static const int env = [] {
@@ -619,9 +618,9 @@ static int rows_per_wave(int N, int K) {
   if (rows_env()) return rows_env();
   if constexpr (kWide<QT, MC> && QT == kTypeQ6_K) return 2;
   if constexpr (kWide<QT, MC>) {
-    if (N < 8192) return 1;
-    const int h = (K / 64 <= 32) ? 2 : 1;
-    return (N >= 65536 ? 4 : 2) * MC / h;
+    const bool half = K / 64 <= 32;  // half-wave launch: a wave covers 2R rows
+    if (N < 8192) return half ? 1 : MC;
+    return half ? 2 : 2 * MC;
   }
   return N < 8192 ? (K >= 8192 ? 2 : 1) : N < 65536 ? 2 : 4;
 }
