@@ -37,7 +37,7 @@ ROTATE_BYTES = 512 << 20
 # (FETCH_SIZE, WRITE_SIZE), each scaled by what the counter reads for a copy
 # of exactly 64 MiB; the summary and commands are in
 # profiles/k_gemv_q4k_gate_up_2x11008x2048_m1.md.
-DOMINANT_TRAFFIC_BYTES = 25510080
+DOMINANT_TRAFFIC_BYTES = 25513160
 
 
 def parse():
@@ -234,7 +234,7 @@ def main():
     result["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
-        "kernel": "k_gemv<Q4_K,MC=1,R=2> grouped gate+up, N=2x11008 K=2048 M=1",
+        "kernel": "k_gemv<Q4_K,MC=1,R=2,H=2> (wide slices, half-wave rows) grouped gate+up, N=2x11008 K=2048 M=1",
         "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3),
     }
     # what a plain streaming read of the same number of bytes achieves
