@@ -29,6 +29,42 @@ SIGNATURES = {
     "ifx_status_string": ([_i32], ctypes.c_char_p),
 }
 
+
+class GgufTensor(ctypes.Structure):
+    """ifx_gguf_tensor (include/ifx_gguf.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("shape", ctypes.c_int64 * 8), ("offset", ctypes.c_uint64),
+                ("byte_size", ctypes.c_uint64), ("host_data", ctypes.c_void_p)]
+
+
+# Every symbol include/ifx_gguf.h declares.
+_u32, _u64, _cp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_char_p
+_pp = ctypes.POINTER(ctypes.c_void_p)
+SIGNATURES.update({
+    "ifx_gguf_open": ([_cp, _pp], _i32),
+    "ifx_gguf_close": ([_vp], None),
+    "ifx_gguf_version": ([_vp], _u32),
+    "ifx_gguf_alignment": ([_vp], _u64),
+    "ifx_gguf_data_offset": ([_vp], _u64),
+    "ifx_gguf_n_tensors": ([_vp], _i64),
+    "ifx_gguf_n_kv": ([_vp], _i64),
+    "ifx_gguf_tensor_info": ([_vp, _i64, ctypes.POINTER(GgufTensor)], _i32),
+    "ifx_gguf_find": ([_vp, _cp], _i64),
+    "ifx_gguf_kv_key": ([_vp, _i64, ctypes.POINTER(_cp), ctypes.POINTER(_i32)], _i32),
+    "ifx_gguf_get_int": ([_vp, _cp, ctypes.POINTER(_i64)], _i32),
+    "ifx_gguf_get_float": ([_vp, _cp, ctypes.POINTER(ctypes.c_double)], _i32),
+    "ifx_gguf_get_string": ([_vp, _cp, _pp, ctypes.POINTER(_u64)], _i32),
+    "ifx_gguf_get_array": ([_vp, _cp, ctypes.POINTER(_i32), ctypes.POINTER(_u64)], _i32),
+    "ifx_gguf_get_array_string": ([_vp, _cp, _u64, _pp, ctypes.POINTER(_u64)], _i32),
+    "ifx_gguf_get_array_data": ([_vp, _cp, _pp, ctypes.POINTER(_i32), ctypes.POINTER(_u64)], _i32),
+    "ifx_gguf_device_bytes": ([_vp, _u64], _u64),
+    "ifx_gguf_upload": ([_vp, _vp, _u64, _u64, ctypes.POINTER(_u64), _vp], _i32),
+    "ifx_gguf_tensor_bytes": ([_i32, ctypes.POINTER(_i64), _i32], _u64),
+    "ifx_gguf_type_name": ([_i32], _cp),
+    "ifx_gguf_parse_name": ([_cp, ctypes.POINTER(_i32), _cp, _u64, _cp, _u64], _i32),
+    "ifx_gguf_status_string": ([_i32], _cp),
+})
+
 _lib = None
 
 

@@ -1,5 +1,5 @@
 """CPU checks of the C ABI: the library loads, exports every entry point
-include/ifx_qgemm.h declares, and its host-side validation answers without
+include/ifx_qgemm.h and include/ifx_gguf.h declare, and its host-side validation answers without
 touching a GPU (the reference's `false` = a positive status)."""
 import ctypes
 import os
@@ -9,11 +9,11 @@ import subprocess
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "ifx_qgemm.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("ifx_qgemm.h", "ifx_gguf.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ifx_\w+)\s*\(", text, re.M)))
 
 
@@ -26,7 +26,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     syms = declared_symbols()
     for s in ("ifx_q8_1_quantize_f32", "ifx_q8_1_quantize_f16", "ifx_qgemv",
-              "ifx_qgemm_prefill", "ifx_dequantize", "ifx_supports"):
+              "ifx_qgemm_prefill", "ifx_dequantize", "ifx_supports", "ifx_gguf_open",
+              "ifx_gguf_upload", "ifx_gguf_tensor_bytes"):
         assert s in syms
 
 
