@@ -21,7 +21,7 @@ namespace inferflux {
 namespace rocm {
 
 // GGUF tensor type ids (runtime/backends/cuda/native/gguf_util.h:48-63).
-enum class TensorType : int { Q8_0 = 8, Q8_1 = 9, Q4_K = 12, Q6_K = 14 };
+enum class TensorType : int { Q8_0 = 8, Q8_1 = 9, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15 };
 
 // Raw quantized weight view (runtime/backends/cuda/native/weight_map.h:17-21).
 // Row r of an [N][K] tensor starts at data + r * (K / QK) * block_bytes.
@@ -134,8 +134,12 @@ class FusedQuantGemm {
                                                   void *act_q8_1_out, int M, int N, int K,
                                                   hipStream_t stream);
 
-  // fused_quant_gemm.h:333.
+  // fused_quant_gemm.h:333: Q4_K, Q6_K, Q8_0 and Q8_K as the reference,
+  // and Q5_K, for which the reference has no fused kernel.
   static bool SupportsQ8_1Activations(int quant_type);
+  // Largest M of the GEMV-only types Q5_K and Q8_K (the reference's Q8_K
+  // dispatch limit, fused_quant_gemm.cu:1740-1747).
+  static constexpr int kMaxGemvOnlyM = 64;
   // fused_quant_gemm.h:343-348 and .cu:830-880, re-derived for gfx950.
   static int GetAdaptiveThreshold(int quant_type);
   static int GetGeometryAwareThreshold(int quant_type, const FusedDispatchGeometry &geometry);

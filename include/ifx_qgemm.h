@@ -33,7 +33,9 @@ enum ifx_quant_type {
   IFX_TYPE_Q8_0 = 8,
   IFX_TYPE_Q8_1 = 9,
   IFX_TYPE_Q4_K = 12,
-  IFX_TYPE_Q6_K = 14
+  IFX_TYPE_Q5_K = 13, /* GEMV kernel family only, M <= 64 (no reference kernel) */
+  IFX_TYPE_Q6_K = 14,
+  IFX_TYPE_Q8_K = 15  /* GEMV kernel family only, M <= 64 (the reference's limit) */
 };
 
 enum ifx_status {

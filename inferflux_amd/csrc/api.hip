@@ -47,6 +47,10 @@ namespace {
 //   M > 32       tiled int8 MFMA    (gemm_mfma.hip)
 constexpr int kMaxGemvMDefault = 2;
 constexpr int kMaxSkinnyM = 32;
+// Q5_K and Q8_K run on the v_dot4 GEMV only, for M <= 64: the reference's
+// Q8_K dispatch stops at 64 (fused_quant_gemm.cu:1740-1747) and it has no
+// fused Q5_K kernel at all (dequantize + cuBLAS); larger M is "not handled".
+constexpr int kMaxGemvOnlyM = 64;
 
 // Largest M the v_dot4 GEMV takes; IFX_GEMV_MAX_M in 0..8 overrides it
 // (tuning; read once).
@@ -73,8 +77,10 @@ bool use_skinny(int M) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
 
+bool gemv_only(int t) { return t == IFX_TYPE_Q5_K || t == IFX_TYPE_Q8_K; }
+
 bool is_weight_type(int t) {
-  return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0;
+  return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0 || gemv_only(t);
 }
 
 int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int out_dtype,
@@ -86,6 +92,7 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   if (mode == IFX_BIAS && !bias) return IFX_NULL_POINTER;
   if (M <= 0 || N <= 0 || K <= 0) return IFX_BAD_GEOMETRY;
   if (K % ifx_block_elems(quant_type) != 0) return IFX_BAD_GEOMETRY;
+  if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return IFX_BAD_GEOMETRY;
   // Kernels address W and A with 32-bit byte offsets (buffer loads).
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
   const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
@@ -102,7 +109,9 @@ extern "C" {
 int ifx_block_bytes(int quant_type) {
   switch (quant_type) {
   case IFX_TYPE_Q4_K: return ifx::kQ4KBytes;
+  case IFX_TYPE_Q5_K: return ifx::kQ5KBytes;
   case IFX_TYPE_Q6_K: return ifx::kQ6KBytes;
+  case IFX_TYPE_Q8_K: return ifx::kQ8KBytes;
   case IFX_TYPE_Q8_0: return ifx::kQ8_0Bytes;
   case IFX_TYPE_Q8_1: return ifx::kQ8_1Bytes;
   default: return 0;
@@ -111,7 +120,7 @@ int ifx_block_bytes(int quant_type) {
 
 int ifx_block_elems(int quant_type) {
   switch (quant_type) {
-  case IFX_TYPE_Q4_K: case IFX_TYPE_Q6_K: return 256;
+  case IFX_TYPE_Q4_K: case IFX_TYPE_Q5_K: case IFX_TYPE_Q6_K: case IFX_TYPE_Q8_K: return 256;
   case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: return 32;
   default: return 0;
   }
@@ -131,6 +140,7 @@ const char *ifx_status_string(int status) {
 int ifx_supports(int quant_type, int M, int N, int K) {
   if (!is_weight_type(quant_type)) return 0;
   if (M <= 0 || N <= 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
+  if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return 0;
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
   const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
                            ifx_block_bytes(quant_type);
@@ -140,6 +150,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
+  if (gemv_only(quant_type)) return 1;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   return M <= kMaxSkinnyM ? 2 : 3;
 }
@@ -184,7 +195,7 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
+  if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
@@ -208,7 +219,7 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
+  if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
         ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
   if (M <= kMaxSkinnyM) {
@@ -251,6 +262,7 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
                       int mode, const void *bias, int M, int N, int K, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
+  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias,
                                          out_dtype == IFX_OUT_F16, M, N, K, mode,
                                          static_cast<hipStream_t>(stream)));

@@ -1,20 +1,33 @@
 // dequant.hip -- whole-tensor dequantization of raw GGUF blocks on gfx950.
 //
-// Replaces the reference's dequantize_{q4_k,q6_k,q8_0} kernels
-// (runtime/backends/cuda/native/kernels/dequantization.cu:14-141) and uses
-// the element formulas of kernels/quant_common.cuh:100-188:
+// Replaces the reference's dequantize_{q4_k,q5_k,q6_k,q8_0,q8_k} kernels
+// (runtime/backends/cuda/native/kernels/dequantization.cu:14-230) and uses
+// the element formulas of kernels/quant_common.cuh:100-199:
 //   Q4_K  w = d*sc*q - dmin*m      Q6_K  w = d*scale*(q-32)     Q8_0  w = d*q
+//   Q5_K  as Q4_K with q = nibble + 16*(bit sb of qh[e])        Q8_K  w = d*q (fp32 d)
 // evaluated left to right in IEEE fp32 (this file is compiled with
 // -ffp-contract=off), so the values are bit-exact with the CPU restatement.
 // The output is fp32, or fp16 (round to nearest even) as the reference
 // emits.  It serves verification and callers that want a dense copy; the
 // GEMV/GEMM kernels never materialise W.
 //
-// Mapping: one lane per 32-element run (a Q4_K sub-block, a Q6_K
-// (group, sub) run, a Q8_0 block); each lane writes 32 contiguous outputs.
+// Mapping: one lane per 32-element run (a Q4_K/Q5_K sub-block, a Q6_K
+// (group, sub) run, a Q8_0 block, a Q8_K 32-value slice); each lane writes
+// 32 contiguous outputs.
 #include "ifx_common.h"
 
 namespace ifx {
+
+// 6-bit scale and min of sub-block sb (quant_common.cuh:83-94).
+__device__ __forceinline__ void scale_min_k4(const uint8_t *s, int sb, int &sc, int &m) {
+  if (sb < 4) {
+    sc = s[sb] & 63;
+    m = s[sb + 4] & 63;
+  } else {
+    sc = (s[sb + 4] & 0xF) | ((s[sb - 4] >> 6) << 4);
+    m = (s[sb + 4] >> 4) | ((s[sb] >> 6) << 4);
+  }
+}
 
 template <int QT, bool F16>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W,
@@ -28,15 +41,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W,
     const uint8_t *b = W + blk * kQ4KBytes;
     const float d = h2f(ldg<uint16_t>(b));
     const float dmin = h2f(ldg<uint16_t>(b + 2));
-    const uint8_t *s = b + 4;
     int sc, m;
-    if (sb < 4) {
-      sc = s[sb] & 63;
-      m = s[sb + 4] & 63;
-    } else {
-      sc = (s[sb + 4] & 0xF) | ((s[sb - 4] >> 6) << 4);
-      m = (s[sb + 4] >> 4) | ((s[sb] >> 6) << 4);
-    }
+    scale_min_k4(b + 4, sb, sc, m);
     const uint8_t *qs = b + 16 + (sb >> 1) * 32;
     const int shift = (sb & 1) * 4;
 #pragma unroll
@@ -44,6 +50,29 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W,
       const int q = (qs[e] >> shift) & 0xF;
       w[e] = d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
     }
+  } else if constexpr (QT == kTypeQ5_K) {
+    const int64_t blk = t >> 3;
+    const int sb = static_cast<int>(t & 7);
+    const uint8_t *b = W + blk * kQ5KBytes;
+    const float d = h2f(ldg<uint16_t>(b));
+    const float dmin = h2f(ldg<uint16_t>(b + 2));
+    int sc, m;
+    scale_min_k4(b + 4, sb, sc, m);
+    const uint8_t *qh = b + 16;
+    const uint8_t *qs = b + 48 + (sb >> 1) * 32;
+    const int shift = (sb & 1) * 4;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const int q = ((qs[e] >> shift) & 0xF) | (((qh[e] >> sb) & 1) << 4);
+      w[e] = d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
+    }
+  } else if constexpr (QT == kTypeQ8_K) {
+    const int64_t blk = t >> 3;
+    const uint8_t *b = W + blk * kQ8KBytes;
+    const float d = ldg<float>(b);
+    const int8_t *qs = reinterpret_cast<const int8_t *>(b + 4) + (t & 7) * 32;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) w[e] = d * static_cast<float>(qs[e]);
   } else if constexpr (QT == kTypeQ6_K) {
     const int64_t blk = t >> 3;
     const int run = static_cast<int>(t & 7);
@@ -97,6 +126,8 @@ hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int6
   case kTypeQ4_K: launch_dq<kTypeQ4_K>(w, out, f16, nruns, stream); break;
   case kTypeQ6_K: launch_dq<kTypeQ6_K>(w, out, f16, nruns, stream); break;
   case kTypeQ8_0: launch_dq<kTypeQ8_0>(w, out, f16, nruns, stream); break;
+  case kTypeQ5_K: launch_dq<kTypeQ5_K>(w, out, f16, nruns, stream); break;
+  case kTypeQ8_K: launch_dq<kTypeQ8_K>(w, out, f16, nruns, stream); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -42,26 +42,40 @@ namespace ifx {
 
 enum OutMode { kOutStore = 0, kOutAccum = 1, kOutBias = 2 };
 
+// Bytes of one weight row of K values.
+__host__ __device__ constexpr int row_bytes(int qt, int K) {
+  return qt == kTypeQ4_K   ? (K >> 8) * kQ4KBytes
+         : qt == kTypeQ5_K ? (K >> 8) * kQ5KBytes
+         : qt == kTypeQ6_K ? (K >> 8) * kQ6KBytes
+         : qt == kTypeQ8_K ? (K >> 8) * kQ8KBytes
+                           : (K >> 5) * kQ8_0Bytes;
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K: slice j (0..7) of super-block b covers qs bytes 16j..16j+15, i.e.
 // values 16h..16h+15 (h = j & 1) of sub-blocks 2p (low nibbles) and 2p+1
 // (high nibbles), p = j >> 1.
 // ---------------------------------------------------------------------------
-template <int MC, int R>
+// Q5 = true: Q5_K (same header and qs as Q4_K, qs at +48, and qh[32] at +16
+// whose bit j of byte e is the fifth bit of value e of sub-block j); the
+// lane also loads qh bytes 16h..16h+15 and ORs the bits in as bit 4 of each
+// code (codes 0..31).
+template <int MC, int R, bool Q5 = false>
 __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
                                           uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
   const int b = s >> 3, j = s & 7, p = j >> 1, h = j & 1;
   // weights first: all R rows in flight before anything waits.  rows[r] is
   // the wave-uniform byte offset of row r; the lane adds its block offset.
-  u32x4 hdr[R], q[R];
-  const uint32_t wo = b * kQ4KBytes;
+  u32x4 hdr[R], q[R], qh[R];
+  const uint32_t wo = b * (Q5 ? kQ5KBytes : kQ4KBytes);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     // the 16-byte header is loaded by one lane of the eight that share the
     // super-block (lane & 7 == 0, i.e. j == 0) and broadcast to the others
     hdr[r] = u32x4{0, 0, 0, 0};
     if (j == 0) hdr[r] = wload<u32x4>(Wr[r], wo, rows[r]);
-    q[r] = wload<u32x4>(Wr[r], wo + 16 + 16 * j, rows[r]);
+    q[r] = wload<u32x4>(Wr[r], wo + (Q5 ? 48 : 16) + 16 * j, rows[r]);
+    if constexpr (Q5) qh[r] = wload<u32x4>(Wr[r], wo + 16 + 16 * h, rows[r]);
   }
   // activations: Q8_1 blocks (b*8 + 2p) and (b*8 + 2p + 1), bytes 16h..16h+15
   i32x4 xa[MC], xb[MC];
@@ -107,10 +121,22 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
     const float dsc1 = d * static_cast<float>((sct >> 8) & 0xFFu);
     const float dm0 = dmin * static_cast<float>(mt & 0xFFu);
     const float dm1 = dmin * static_cast<float>((mt >> 8) & 0xFFu);
-    const int lo0 = q[r].x & 0x0F0F0F0F, hi0 = (q[r].x >> 4) & 0x0F0F0F0F;
-    const int lo1 = q[r].y & 0x0F0F0F0F, hi1 = (q[r].y >> 4) & 0x0F0F0F0F;
-    const int lo2 = q[r].z & 0x0F0F0F0F, hi2 = (q[r].z >> 4) & 0x0F0F0F0F;
-    const int lo3 = q[r].w & 0x0F0F0F0F, hi3 = (q[r].w >> 4) & 0x0F0F0F0F;
+    int lo0 = q[r].x & 0x0F0F0F0F, hi0 = (q[r].x >> 4) & 0x0F0F0F0F;
+    int lo1 = q[r].y & 0x0F0F0F0F, hi1 = (q[r].y >> 4) & 0x0F0F0F0F;
+    int lo2 = q[r].z & 0x0F0F0F0F, hi2 = (q[r].z >> 4) & 0x0F0F0F0F;
+    int lo3 = q[r].w & 0x0F0F0F0F, hi3 = (q[r].w >> 4) & 0x0F0F0F0F;
+    if constexpr (Q5) {
+      // bit 2p of qh -> sub-block 2p (low nibbles), bit 2p+1 -> 2p+1
+      const int sl = 2 * p, sh5 = 2 * p + 1;
+      lo0 |= ((qh[r].x >> sl) & 0x01010101u) << 4;
+      lo1 |= ((qh[r].y >> sl) & 0x01010101u) << 4;
+      lo2 |= ((qh[r].z >> sl) & 0x01010101u) << 4;
+      lo3 |= ((qh[r].w >> sl) & 0x01010101u) << 4;
+      hi0 |= ((qh[r].x >> sh5) & 0x01010101u) << 4;
+      hi1 |= ((qh[r].y >> sh5) & 0x01010101u) << 4;
+      hi2 |= ((qh[r].z >> sh5) & 0x01010101u) << 4;
+      hi3 |= ((qh[r].w >> sh5) & 0x01010101u) << 4;
+    }
 #pragma unroll
     for (int c = 0; c < MC; ++c) {
       int dl = dot4(lo0, xa[c].x, 0);
@@ -372,17 +398,22 @@ __device__ __forceinline__ void q6k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
 // ---------------------------------------------------------------------------
 // Q8_0: slice s is block s of the row (34 bytes: fp16 d, 32 int8 codes).
 // ---------------------------------------------------------------------------
-template <int MC, int R>
+// K8 = true: Q8_K (mmvq.cuh:1019-1070): slice s is codes 32(s&7).. of
+// super-block s>>3 (292 bytes: fp32 d, i8 qs[256], i16 bsums[16]); the
+// fp32 d is shared by the eight slices of a super-block.
+template <int MC, int R, bool K8 = false>
 __device__ __forceinline__ void q8_0_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
                                            uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
   i32x4 w0[R], w1[R];
-  uint16_t dbits[R];
-  const uint32_t wo = s * kQ8_0Bytes;
+  uint32_t dbits[R];
+  const uint32_t wo = K8 ? (s >> 3) * kQ8KBytes : s * kQ8_0Bytes;
+  const uint32_t qo = K8 ? wo + 4 + 32 * (s & 7) : wo + 2;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    dbits[r] = wload<uint16_t>(Wr[r], wo, rows[r]);
-    w0[r] = wload<i32x4>(Wr[r], wo + 2, rows[r]);
-    w1[r] = wload<i32x4>(Wr[r], wo + 18, rows[r]);
+    if constexpr (K8) dbits[r] = wload<uint32_t>(Wr[r], wo, rows[r]);
+    else dbits[r] = wload<uint16_t>(Wr[r], wo, rows[r]);
+    w0[r] = wload<i32x4>(Wr[r], qo, rows[r]);
+    w1[r] = wload<i32x4>(Wr[r], qo + 16, rows[r]);
   }
   i32x4 x0[MC], x1[MC];
   float da[MC];
@@ -400,7 +431,7 @@ __device__ __forceinline__ void q8_0_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, con
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float d = h2f(dbits[r]);
+    const float d = K8 ? __builtin_bit_cast(float, dbits[r]) : h2f(dbits[r] & 0xFFFFu);
 #pragma unroll
     for (int c = 0; c < MC; ++c) {
       int dt = dot4(w0[r].x, x0[c].x, 0);
@@ -470,9 +501,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const int col0 = blockIdx.y * MC;
   const int mvalid = min(MC, M - col0);
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
-  const uint32_t w_row = (QT == kTypeQ4_K)   ? static_cast<uint32_t>(K >> 8) * kQ4KBytes
-                         : (QT == kTypeQ6_K) ? static_cast<uint32_t>(K >> 8) * kQ6KBytes
-                                             : static_cast<uint32_t>(K >> 5) * kQ8_0Bytes;
+  const uint32_t w_row = static_cast<uint32_t>(row_bytes(QT, K));
   // 32-bit ranges (the launcher checks the tensors are below 4 GiB)
   const rsrc_t Wr = make_rsrc(W, w_row * static_cast<uint32_t>(N));
   const rsrc_t Ar = make_rsrc(args.A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
@@ -507,8 +536,12 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       q6k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ4_K)
       q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ5_K)
+      q4k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
       q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ8_K)
+      q8_0_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else
       q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }
@@ -650,6 +683,8 @@ static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStre
   case kTypeQ4_K: launch_type<kTypeQ4_K>(args, f16, stream); break;
   case kTypeQ6_K: launch_type<kTypeQ6_K>(args, f16, stream); break;
   case kTypeQ8_0: launch_type<kTypeQ8_0>(args, f16, stream); break;
+  case kTypeQ5_K: launch_type<kTypeQ5_K>(args, f16, stream); break;
+  case kTypeQ8_K: launch_type<kTypeQ8_K>(args, f16, stream); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -683,9 +718,7 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
   const int mvalid = min(MC, M - col0);
   const int nslice = K >> 5;
   const uint32_t a_row = static_cast<uint32_t>(nslice) * kQ8_1Bytes;
-  const uint32_t w_row = (QT == kTypeQ4_K)   ? static_cast<uint32_t>(K >> 8) * kQ4KBytes
-                         : (QT == kTypeQ6_K) ? static_cast<uint32_t>(K >> 8) * kQ6KBytes
-                                             : static_cast<uint32_t>(nslice) * kQ8_0Bytes;
+  const uint32_t w_row = static_cast<uint32_t>(row_bytes(QT, K));
   const rsrc_t Wgr = make_rsrc(Wg, w_row * static_cast<uint32_t>(N));
   const rsrc_t Wur = make_rsrc(Wu, w_row * static_cast<uint32_t>(N));
   const rsrc_t Ar = make_rsrc(A + static_cast<int64_t>(col0) * a_row, a_row * mvalid);
@@ -701,8 +734,12 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
   for (int s = lane; s < nslice; s += 64) {
     if constexpr (QT == kTypeQ4_K)
       q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ5_K)
+      q4k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
       q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ8_K)
+      q8_0_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else
       q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }
@@ -765,6 +802,8 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   case kTypeQ4_K: launch_swiglu_t<kTypeQ4_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   case kTypeQ6_K: launch_swiglu_t<kTypeQ6_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   case kTypeQ8_0: launch_swiglu_t<kTypeQ8_0>(g, u, a, H, f16h, q, M, N, K, stream); break;
+  case kTypeQ5_K: launch_swiglu_t<kTypeQ5_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
+  case kTypeQ8_K: launch_swiglu_t<kTypeQ8_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -20,9 +20,13 @@ namespace ifx {
 constexpr int kTypeQ8_0 = 8;
 constexpr int kTypeQ8_1 = 9;
 constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ5_K = 13;
 constexpr int kTypeQ6_K = 14;
+constexpr int kTypeQ8_K = 15;
 
 constexpr int kQ4KBytes = 144;
+constexpr int kQ5KBytes = 176;  // u16 d, u16 dmin, scales[12], qh[32], qs[128]
+constexpr int kQ8KBytes = 292;  // f32 d, i8 qs[256], i16 bsums[16]
 constexpr int kQ6KBytes = 210;
 constexpr int kQ8_0Bytes = 34;
 constexpr int kQ8_1Bytes = 36;

@@ -190,8 +190,10 @@ bool FusedQuantGemm::FusedGateUpSiluGemvQ8_1WithEpilogue(const QuantizedWeightIn
 
 bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
   return quant_type == static_cast<int>(TensorType::Q4_K) ||
+         quant_type == static_cast<int>(TensorType::Q5_K) ||
          quant_type == static_cast<int>(TensorType::Q6_K) ||
-         quant_type == static_cast<int>(TensorType::Q8_0);
+         quant_type == static_cast<int>(TensorType::Q8_0) ||
+         quant_type == static_cast<int>(TensorType::Q8_K);
 }
 
 // The reference scales a per-GPU-generation base by 16/bpw and clamps to
@@ -201,7 +203,11 @@ bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
 // bytes than an FP16 copy for Q4_K) and runs at twice the FP16 MFMA rate,
 // so the fallback never wins: the threshold is the path's M limit.
 int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
-  return SupportsQ8_1Activations(quant_type) ? kMaxFusedM : 0;
+  if (!SupportsQ8_1Activations(quant_type)) return 0;
+  if (quant_type == static_cast<int>(TensorType::Q5_K) ||
+      quant_type == static_cast<int>(TensorType::Q8_K))
+    return kMaxGemvOnlyM;  // v_dot4 GEMV only
+  return kMaxFusedM;
 }
 
 int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,

@@ -11,10 +11,10 @@ import torch
 
 from . import _lib
 
-Q8_0, Q8_1, Q4_K, Q6_K = 8, 9, 12, 14
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34, Q8_1: 36}
-BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32}
-TYPE_NAMES = {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0", Q8_1: "Q8_1"}
+Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 8, 9, 12, 13, 14, 15
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_1: 36, Q8_K: 292}
+BLOCK_ELEMS = {Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32, Q8_K: 256}
+TYPE_NAMES = {Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", Q8_1: "Q8_1", Q8_K: "Q8_K"}
 
 STORE, ACCUM, BIAS = 0, 1, 2
 OUT_F32, OUT_F16 = 0, 1

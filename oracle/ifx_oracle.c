@@ -42,11 +42,12 @@
 #define ORC_QK8 32
 
 /* GGUF tensor type ids: native/gguf_util.h:48-63 */
-enum { ORC_Q8_0 = 8, ORC_Q8_1 = 9, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_Q8_K = 15 };
+enum { ORC_Q8_0 = 8, ORC_Q8_1 = 9, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15 };
 
 /* Block byte sizes: native/kernels/dequantization.cuh:17-49,117-138,156-166 */
 enum {
   ORC_Q4_K_BYTES = 144, /* u16 d, u16 dmin, u8 scales[12], u8 qs[128]      */
+  ORC_Q5_K_BYTES = 176, /* u16 d, u16 dmin, u8 scales[12], u8 qh[32], u8 qs[128] */
   ORC_Q6_K_BYTES = 210, /* u8 ql[128], u8 qh[64], i8 scales[16], u16 d LAST */
   ORC_Q8_0_BYTES = 34,  /* u16 d, i8 qs[32]                                 */
   ORC_Q8_1_BYTES = 36,  /* u16 d, u16 s (= d*sum(qs)), i8 qs[32]            */
@@ -56,6 +57,7 @@ enum {
 int orc_block_bytes(int qtype) {
   switch (qtype) {
   case ORC_Q4_K: return ORC_Q4_K_BYTES;
+  case ORC_Q5_K: return ORC_Q5_K_BYTES;
   case ORC_Q6_K: return ORC_Q6_K_BYTES;
   case ORC_Q8_0: return ORC_Q8_0_BYTES;
   case ORC_Q8_1: return ORC_Q8_1_BYTES;
@@ -66,7 +68,7 @@ int orc_block_bytes(int qtype) {
 
 int orc_block_elems(int qtype) {
   switch (qtype) {
-  case ORC_Q4_K: case ORC_Q6_K: case ORC_Q8_K: return ORC_QK_K;
+  case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K: return ORC_QK_K;
   case ORC_Q8_0: case ORC_Q8_1: return ORC_QK8;
   default: return 0;
   }
@@ -177,6 +179,33 @@ static void dequant_q6_k_block(const uint8_t *b, float *out) {
       }
 }
 
+/* native/kernels/quant_common.cuh:114-143 (layout dequantization.cuh:27-37):
+ *   q = nibble of qs[(sb/2)*32 + e] (low when sb even) + 16 * bit sb of
+ *   qh[e]; w = d*sc*q - dmin*m, evaluated as ((d*sc)*q) - (dmin*m).         */
+static void dequant_q5_k_block(const uint8_t *b, float *out) {
+  const float d = orc_f16_to_f32(rd16(b));
+  const float dmin = orc_f16_to_f32(rd16(b + 2));
+  const uint8_t *scales = b + 4, *qh = b + 16, *qs = b + 48;
+  for (int sb = 0; sb < 8; ++sb) {
+    uint8_t sc, m;
+    orc_get_scale_min_k4(sb, scales, &sc, &m);
+    for (int e = 0; e < 32; ++e) {
+      const uint8_t qb = qs[(sb / 2) * 32 + e];
+      const int q = ((sb & 1) ? (qb >> 4) : (qb & 0x0F)) + (((qh[e] >> sb) & 1) ? 16 : 0);
+      out[sb * 32 + e] = d * (float)sc * (float)q - dmin * (float)m;
+    }
+  }
+}
+
+/* native/kernels/quant_common.cuh:196-199 (layout dequantization.cuh:165-176):
+ *   w = d*q with an fp32 d.                                                 */
+static void dequant_q8_k_block(const uint8_t *b, float *out) {
+  float d;
+  memcpy(&d, b, 4);
+  const int8_t *qs = (const int8_t *)(b + 4);
+  for (int e = 0; e < 256; ++e) out[e] = d * (float)qs[e];
+}
+
 /* native/kernels/quant_common.cuh:185-188: w = d*q */
 static void dequant_q8_0_block(const uint8_t *b, float *out) {
   const float d = orc_f16_to_f32(rd16(b));
@@ -190,14 +219,16 @@ static void dequant_q8_0_block(const uint8_t *b, float *out) {
  * success, 1 for an unsupported type or K.                                  */
 int orc_dequantize(int qtype, const void *w, float *out, int64_t n_rows, int64_t K) {
   const int qk = orc_block_elems(qtype), bb = orc_block_bytes(qtype);
-  if (!qk || qtype == ORC_Q8_1 || qtype == ORC_Q8_K || K % qk) return 1;
+  if (!qk || qtype == ORC_Q8_1 || K % qk) return 1;
   const uint8_t *p = (const uint8_t *)w;
   const int64_t nb = n_rows * (K / qk);
   for (int64_t i = 0; i < nb; ++i) {
     const uint8_t *b = p + i * bb;
     float *o = out + i * qk;
     if (qtype == ORC_Q4_K) dequant_q4_k_block(b, o);
+    else if (qtype == ORC_Q5_K) dequant_q5_k_block(b, o);
     else if (qtype == ORC_Q6_K) dequant_q6_k_block(b, o);
+    else if (qtype == ORC_Q8_K) dequant_q8_k_block(b, o);
     else dequant_q8_0_block(b, o);
   }
   return 0;
@@ -337,6 +368,17 @@ static void dequant_row_f64(int qtype, const uint8_t *row, double *out, int64_t 
           o[sb * 32 + e] = d * sc * q - dmin * m;
         }
       }
+    } else if (qtype == ORC_Q5_K) {
+      const double d = orc_f16_to_f32(rd16(b)), dmin = orc_f16_to_f32(rd16(b + 2));
+      for (int sb = 0; sb < 8; ++sb) {
+        uint8_t sc, m;
+        orc_get_scale_min_k4(sb, b + 4, &sc, &m);
+        for (int e = 0; e < 32; ++e) {
+          const uint8_t qb = b[48 + (sb / 2) * 32 + e];
+          const int q = ((sb & 1) ? (qb >> 4) : (qb & 0x0F)) + 16 * ((b[16 + e] >> sb) & 1);
+          o[sb * 32 + e] = d * sc * q - dmin * m;
+        }
+      }
     } else if (qtype == ORC_Q6_K) {
       const double d = orc_f16_to_f32(rd16(b + 208));
       for (int g = 0; g < 2; ++g)
@@ -348,6 +390,10 @@ static void dequant_row_f64(int qtype, const uint8_t *row, double *out, int64_t 
             const int sc = ((const int8_t *)(b + 192))[g * 8 + sub * 2 + e / 16];
             o[g * 128 + sub * 32 + e] = d * sc * ((lv | (hv << 4)) - 32);
           }
+    } else if (qtype == ORC_Q8_K) {
+      float df;
+      memcpy(&df, b, 4);
+      for (int e = 0; e < 256; ++e) o[e] = (double)df * ((const int8_t *)(b + 4))[e];
     } else {
       const double d = orc_f16_to_f32(rd16(b));
       for (int e = 0; e < 32; ++e) o[e] = d * ((const int8_t *)(b + 2))[e];
@@ -391,7 +437,9 @@ static void *gemv_exact_worker(void *arg) {
 }
 
 static int check_geom(int qtype, int M, int N, int K) {
-  if (qtype != ORC_Q4_K && qtype != ORC_Q6_K && qtype != ORC_Q8_0) return 1;
+  if (qtype != ORC_Q4_K && qtype != ORC_Q5_K && qtype != ORC_Q6_K && qtype != ORC_Q8_0 &&
+      qtype != ORC_Q8_K)
+    return 1;
   if (M <= 0 || N <= 0 || K <= 0 || K % orc_block_elems(qtype)) return 1;
   return 0;
 }
@@ -425,6 +473,9 @@ int orc_gemv_exact(int qtype, const void *W, const void *A, double *y, int M, in
 /*   Q4_K: native/kernels/mmvq.cuh:62-127                                     */
 /*   Q6_K: native/kernels/mmvq.cuh:424-474                                    */
 /*   Q8_0: native/kernels/mmvq.cuh:857-891                                    */
+/*   Q8_K: native/kernels/mmvq.cuh:1019-1070 (fp32 d_w times d8 per 32)      */
+/*   Q5_K: no reference kernel (the reference dequantizes Q5_K for cuBLAS); */
+/*         the Q4_K scheme with the 5-bit code q = nibble + 16 * qh bit.    */
 /* Accumulation order is per-row sequential (the reference reduces across     */
 /* lanes); results agree with orc_gemv_exact to ~1e-6 relative.               */
 /* ------------------------------------------------------------------------ */
@@ -447,6 +498,37 @@ static float row_dot_q8_1(int qtype, const uint8_t *row, const uint8_t *a, int K
         const float d8 = orc_f16_to_f32(rd16(ab)), s8 = orc_f16_to_f32(rd16(ab + 2));
         acc += d * (float)sc * d8 * (float)dot;
         acc -= dmin * (float)m * s8;
+      }
+    }
+  } else if (qtype == ORC_Q5_K) {
+    for (int blk = 0; blk < K / 256; ++blk) {
+      const uint8_t *b = row + blk * 176;
+      const float d = orc_f16_to_f32(rd16(b)), dmin = orc_f16_to_f32(rd16(b + 2));
+      for (int sb = 0; sb < 8; ++sb) {
+        uint8_t sc, m;
+        orc_get_scale_min_k4(sb, b + 4, &sc, &m);
+        const uint8_t *ab = a + (blk * 8 + sb) * 36;
+        int dot = 0;
+        for (int e = 0; e < 32; ++e) {
+          const uint8_t qb = b[48 + (sb / 2) * 32 + e];
+          const int q = ((sb & 1) ? (qb >> 4) : (qb & 0x0F)) + 16 * ((b[16 + e] >> sb) & 1);
+          dot += q * (int8_t)ab[4 + e];
+        }
+        const float d8 = orc_f16_to_f32(rd16(ab)), s8 = orc_f16_to_f32(rd16(ab + 2));
+        acc += d * (float)sc * d8 * (float)dot;
+        acc -= dmin * (float)m * s8;
+      }
+    }
+  } else if (qtype == ORC_Q8_K) {
+    for (int blk = 0; blk < K / 256; ++blk) {
+      const uint8_t *b = row + blk * 292;
+      float dw;
+      memcpy(&dw, b, 4);
+      for (int sub = 0; sub < 8; ++sub) {
+        const uint8_t *ab = a + (blk * 8 + sub) * 36;
+        int dot = 0;
+        for (int e = 0; e < 32; ++e) dot += (int8_t)b[4 + sub * 32 + e] * (int8_t)ab[4 + e];
+        acc += dw * orc_f16_to_f32(rd16(ab)) * (float)dot;
       }
     }
   } else if (qtype == ORC_Q6_K) {

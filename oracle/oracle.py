@@ -14,9 +14,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-Q8_0, Q8_1, Q4_K, Q6_K, Q8_K = 8, 9, 12, 14, 15
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34, Q8_1: 36, Q8_K: 292}
-BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32, Q8_K: 256}
+Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 8, 9, 12, 13, 14, 15
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_1: 36, Q8_K: 292}
+BLOCK_ELEMS = {Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32, Q8_K: 256}
 
 _lib = None
 

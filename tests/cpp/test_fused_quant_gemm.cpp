@@ -95,8 +95,11 @@ std::vector<uint8_t> MakeBlocks(int qtype, int N, int K, uint64_t seed) {
       const uint16_t h = orc_f32_to_f16(std::fabs(r.normal()) * 0.01f);
       std::memcpy(blk + off, &h, 2);
     };
-    if (qtype == Q4_K) { put(0); put(2); }
-    else if (qtype == Q6_K) {
+    if (qtype == Q4_K || qtype == 13) { put(0); put(2); }  // Q4_K, Q5_K
+    else if (qtype == 15) {                                   // Q8_K: fp32 d
+      const float d = std::fabs(r.normal()) * 0.01f;
+      std::memcpy(blk, &d, 4);
+    } else if (qtype == Q6_K) {
       for (int j = 0; j < 16; ++j) blk[192 + j] = static_cast<uint8_t>(static_cast<int8_t>(r.next() % 128) - 64);
       put(208);
     } else {
@@ -148,7 +151,17 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SupportsQ8_1Activations(Q8_0));
   EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(Q8_1));
   EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(0));
-  EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(15));
+  EXPECT(FusedQuantGemm::SupportsQ8_1Activations(15));  // Q8_K, as the reference
+  EXPECT(FusedQuantGemm::SupportsQ8_1Activations(13));  // Q5_K (no reference kernel)
+  EXPECT(!FusedQuantGemm::SupportsQ8_1Activations(16));
+  // Q5_K / Q8_K: GEMV only, M <= 64 (the reference's Q8_K limit)
+  EXPECT(FusedQuantGemm::GetAdaptiveThreshold(15) == 64);
+  EXPECT(FusedQuantGemm::ShouldUseFusedPath(15, 64));
+  EXPECT(!FusedQuantGemm::ShouldUseFusedPath(15, 65));
+  EXPECT(!FusedQuantGemm::ShouldUseFusedPath(13, 512));
+  EXPECT(FusedQuantGemm::SelectKernel(13, 32, 4096, 4096) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(15, 64, 4096, 4096) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(15, 65, 4096, 4096) == KernelFamily::kNone);
 
   // thresholds: no crossover to a fallback on gfx950
   EXPECT(FusedQuantGemm::GetAdaptiveThreshold(Q4_K) == FusedQuantGemm::kMaxFusedM);
@@ -371,6 +384,10 @@ int main(int argc, char **argv) {
     TestGpuCase(Q4_K, 5, 200, 1024);
     TestGpuCase(Q6_K, 24, 96, 2048);
     TestGpuCase(Q8_0, 40, 160, 512);
+    TestGpuCase(13, 1, 300, 2048);  // Q5_K
+    TestGpuCase(13, 7, 130, 1024);
+    TestGpuCase(15, 2, 200, 1024);  // Q8_K
+    TestGpuCase(15, 64, 70, 512);
     TestProducers();
     TestGrouped<2>(Q4_K, 1, 2048, {300, 173});
     TestGrouped<3>(Q4_K, 2, 1024, {128, 64, 65});

@@ -7,7 +7,7 @@ shows up as a mismatch here rather than being copied.
 """
 import numpy as np
 
-Q8_0, Q8_1, Q4_K, Q6_K = 8, 9, 12, 14
+Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 8, 9, 12, 13, 14, 15
 
 
 def f16(bytes2):
@@ -64,6 +64,21 @@ def dequant_f64(qtype, w, n_rows, K):
     elif qtype == Q8_0:
         b = w.reshape(-1, 34)
         out = f16(b[:, 0:2])[:, None] * b[:, 2:34].view(np.int8).astype(np.float64)
+    elif qtype == Q5_K:
+        # Q4_K's nibbles plus a fifth bit: bit j of qh[e] belongs to value e
+        # of sub-block j (qh[32] precedes qs[128] in the block)
+        b = w.reshape(-1, 176)
+        d, dmin = f16(b[:, 0:2]), f16(b[:, 2:4])
+        sc, m = unpack_scale_min_k4(b[:, 4:16])
+        qh = b[:, 16:48].astype(np.int64)                           # [nb, e]
+        qs = b[:, 48:176].reshape(-1, 4, 32).astype(np.int64)
+        q = np.stack([qs & 0xF, qs >> 4], axis=2).reshape(-1, 8, 32)
+        q = q + 16 * ((qh[:, None, :] >> np.arange(8)[None, :, None]) & 1)
+        out = d[:, None, None] * sc[:, :, None] * q - dmin[:, None, None] * m[:, :, None]
+    elif qtype == Q8_K:
+        b = w.reshape(-1, 292)
+        d = np.ascontiguousarray(b[:, 0:4]).view(np.float32).astype(np.float64)[:, 0]
+        out = d[:, None] * b[:, 4:260].view(np.int8).astype(np.float64)
     else:
         raise ValueError(qtype)
     return out.reshape(n_rows, K)

@@ -55,7 +55,9 @@ def test_block_geometry(lib):
     assert (lib.ifx_block_bytes(14), lib.ifx_block_elems(14)) == (210, 256)
     assert (lib.ifx_block_bytes(8), lib.ifx_block_elems(8)) == (34, 32)
     assert (lib.ifx_block_bytes(9), lib.ifx_block_elems(9)) == (36, 32)
-    assert lib.ifx_block_bytes(0) == 0 and lib.ifx_block_elems(13) == 0
+    assert (lib.ifx_block_bytes(13), lib.ifx_block_elems(13)) == (176, 256)
+    assert (lib.ifx_block_bytes(15), lib.ifx_block_elems(15)) == (292, 256)
+    assert lib.ifx_block_bytes(0) == 0 and lib.ifx_block_elems(16) == 0
 
 
 def test_supports(lib):
@@ -65,7 +67,11 @@ def test_supports(lib):
     assert lib.ifx_supports(8, 8, 151936, 2048) == 1
     assert lib.ifx_supports(8, 1, 16, 96) == 1        # Q8_0 needs K % 32 only
     assert lib.ifx_supports(12, 1, 16, 96) == 0       # K-quants need K % 256
-    assert lib.ifx_supports(13, 1, 16, 256) == 0      # Q5_K: no kernel
+    assert lib.ifx_supports(13, 1, 16, 256) == 1      # Q5_K: GEMV, M <= 64
+    assert lib.ifx_supports(15, 64, 16, 256) == 1     # Q8_K: GEMV, M <= 64
+    assert lib.ifx_supports(15, 65, 16, 256) == 0     # the reference's limit
+    assert lib.ifx_supports(13, 1, 16, 128) == 0
+    assert lib.ifx_supports(11, 1, 16, 256) == 0      # Q3_K: no kernel
     assert lib.ifx_supports(12, 0, 16, 256) == 0
 
 
@@ -78,7 +84,9 @@ def test_validation_without_launch(lib):
     assert lib.ifx_qgemv(12, fake, fake, fake, 0, 2, None, 1, 16, 256, None) == 3  # bias mode
     assert lib.ifx_q8_1_quantize_f32(None, fake, 1, 32, None) == 3
     # unsupported type / geometry / mode / dtype
-    assert lib.ifx_qgemv(13, fake, fake, fake, 0, 0, None, 1, 16, 256, None) == 1
+    assert lib.ifx_qgemv(11, fake, fake, fake, 0, 0, None, 1, 16, 256, None) == 1
+    assert lib.ifx_qgemv(15, fake, fake, fake, 0, 0, None, 65, 16, 256, None) == 2  # Q8_K, M > 64
+    assert lib.ifx_qgemm_prefill(13, fake, fake, fake, 0, 0, None, 8, 16, 256, None) == 1
     assert lib.ifx_qgemv(12, fake, fake, fake, 0, 0, None, 1, 16, 250, None) == 2
     assert lib.ifx_qgemv(12, fake, fake, fake, 0, 0, None, 0, 16, 256, None) == 2
     assert lib.ifx_qgemv(12, fake, fake, fake, 0, 7, None, 1, 16, 256, None) == 2

@@ -14,7 +14,7 @@ from tests import qref
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 8, 12, 13, 14, 15
 TOL = 1e-3
 
 
@@ -93,7 +93,8 @@ def test_quantize_reference_kat(dev):
 
 
 # ---------------------------------------------------------------- dequant
-@pytest.mark.parametrize("qtype,n,K", [(Q4_K, 33, 2048), (Q6_K, 17, 11008), (Q8_0, 9, 2080)])
+@pytest.mark.parametrize("qtype,n,K", [(Q4_K, 33, 2048), (Q6_K, 17, 11008), (Q8_0, 9, 2080),
+                                      (Q5_K, 9, 2048), (Q8_K, 7, 1024)])
 def test_dequant_bit_exact(orc, dev, qtype, n, K):
     import torch
     from inferflux_amd import ops, synth
@@ -114,6 +115,10 @@ for qt in (Q4_K, Q6_K, Q8_0):
     CASES.append((qt, 1, 37, 5120))
     CASES.append((qt, 8, 129, 11008 if qt != Q6_K else 13824))
 CASES.append((Q8_0, 3, 50, 96))     # K not a multiple of 256
+for qt in (Q5_K, Q8_K):             # GEMV-only types, M <= 64
+    for M in (1, 2, 3, 8, 17, 64):
+        CASES.append((qt, M, 300, 2048))
+    CASES.append((qt, 1, 37, 5120))
 
 
 @pytest.mark.parametrize("qtype,M,N,K", CASES)
@@ -142,7 +147,7 @@ def test_gemv_reference_patterns(orc, dev, qtype):
     check_rows(y, ye)
 
 
-@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0, Q5_K, Q8_K])
 @pytest.mark.parametrize("M", [1, 8, 24])
 def test_epilogues(orc, dev, qtype, M):
     """Accumulate (GemvQ8_1Accum / AccumF32) and bias (GemvQ8_1WithBias),
@@ -248,6 +253,8 @@ def test_config5_prefill(orc, dev, qtype, N, K):
     (Q6_K, 1, 1024, (33, 1, 250)),         # ragged row counts
     (Q8_0, 2, 2080, (7, 129, 64)),         # K not a multiple of 256
     (Q4_K, 8, 2048, (300, 173)),           # M > 2: one MFMA launch per projection
+    (Q5_K, 1, 2048, (300, 173, 64)),
+    (Q8_K, 5, 1024, (129, 77)),
 ])
 def test_grouped_parity(orc, dev, qtype, M, K, Ns):
     import torch
@@ -373,7 +380,8 @@ def test_silu_mul_quantize_exact_kat(orc, dev):
 # ------------------------------- fused gate/up GEMV + SiLU + Q8_1 epilogue
 @pytest.mark.parametrize("qtype,M,N,K", [(Q4_K, 1, 11008, 2048), (Q4_K, 2, 1024, 2048),
                                          (Q6_K, 1, 512, 1024), (Q8_0, 2, 64, 2080),
-                                         (Q4_K, 1, 32, 5120)])
+                                         (Q4_K, 1, 32, 5120), (Q5_K, 1, 1024, 2048),
+                                         (Q8_K, 2, 512, 1024)])
 def test_gate_up_silu_parity(orc, dev, qtype, M, N, K):
     import torch
     from inferflux_amd import ops, synth
@@ -411,3 +419,18 @@ def test_gate_up_silu_not_handled(dev):
         ops.qgemv_gate_up_silu(Q4_K, w, w, a, 3, 32, 256)
     with pytest.raises(ops.NotHandled):
         ops.qgemv_gate_up_silu(Q8_0, w, w, a, 1, 20, 32)
+
+
+def test_gemv_only_types_not_handled(dev):
+    """Q5_K / Q8_K: M > 64 and the prefill entry are not handled (the
+    reference's Q8_K dispatch returns false above M = 64 and it has no fused
+    Q5_K kernel): a positive status, nothing launched."""
+    import torch
+    from inferflux_amd import ops
+    w = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    a = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    for qt in (Q5_K, Q8_K):
+        with pytest.raises(ops.NotHandled):
+            ops.qgemv(qt, w, a, 65, 8, 256)
+        with pytest.raises(ops.NotHandled):
+            ops.qgemv(qt, w, a, 8, 8, 256, prefill=True)

@@ -10,7 +10,7 @@ import pytest
 
 from tests import qref
 
-Q8_0, Q8_1, Q4_K, Q6_K = 8, 9, 12, 14
+Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 8, 9, 12, 13, 14, 15
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
@@ -120,7 +120,54 @@ def test_dequant_q8_0_closed_form(orc):
                           np.arange(-16, 16, dtype=np.float32) / 2)
 
 
-@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0])
+def _q5k_block(d, dmin, sc, m, q):
+    """q in 0..31: nibbles as Q4_K, bit 4 of value e of sub-block j in bit j of qh[e]."""
+    q = np.asarray(q).reshape(8, 32)
+    b4 = _q4k_block(d, dmin, sc, m, q & 0xF)
+    b = np.zeros(176, np.uint8)
+    b[0:16] = b4[0:16]
+    b[48:176] = b4[16:144]
+    for j in range(8):
+        b[16:48] |= ((q[j] >> 4) << j).astype(np.uint8)
+    return b
+
+
+def test_dequant_q5k_closed_form(orc):
+    q = np.arange(256) % 32
+    b = _q5k_block(1.0, 0.0, [1] * 8, [0] * 8, q)
+    assert np.array_equal(orc.dequantize(Q5_K, b, 1, 256)[0], q.astype(np.float32))
+    sc = [1, 2, 3, 4, 63, 32, 17, 5]
+    m = [0, 1, 2, 3, 63, 40, 9, 33]
+    b = _q5k_block(1.0, 1.0, sc, m, q[::-1])
+    want = (np.repeat(sc, 32) * q[::-1] - np.repeat(m, 32)).astype(np.float32)
+    assert np.array_equal(orc.dequantize(Q5_K, b, 1, 256)[0], want)
+
+
+def test_dequant_q5k_reduces_to_q4k(orc):
+    """qh = 0: Q5_K is Q4_K on the same d, dmin, scales and qs; qh all ones
+    adds 16*d*sc to every value (catches a misplaced qh bit or field)."""
+    from inferflux_amd import synth
+    w4 = synth.blocks(Q4_K, 3, 512, seed=21).reshape(-1, 144)
+    w5 = np.zeros((w4.shape[0], 176), np.uint8)
+    w5[:, 0:16], w5[:, 48:176] = w4[:, 0:16], w4[:, 16:144]
+    y4 = orc.dequantize(Q4_K, w4, 3, 512).astype(np.float64)
+    assert np.array_equal(orc.dequantize(Q5_K, w5, 3, 512), orc.dequantize(Q4_K, w4, 3, 512))
+    w5[:, 16:48] = 0xFF
+    d = qref.f16(w4[:, 0:2])
+    sc, _ = qref.unpack_scale_min_k4(w4[:, 4:16])
+    add = (16 * d[:, None] * sc).repeat(32, axis=1).reshape(3, 512)
+    assert np.allclose(orc.dequantize(Q5_K, w5, 3, 512), y4 + add, rtol=1e-6, atol=1e-6)
+
+
+def test_dequant_q8k_closed_form(orc):
+    b = np.zeros(292, np.uint8)
+    b[0:4] = np.array([0.25], np.float32).view(np.uint8)
+    b[4:260] = np.arange(-128, 128, dtype=np.int8).view(np.uint8)
+    assert np.array_equal(orc.dequantize(Q8_K, b, 1, 256)[0],
+                          np.arange(-128, 128, dtype=np.float32) / 4)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K, Q8_0, Q8_K])
 def test_dequant_matches_numpy_statement(orc, qtype):
     from inferflux_amd import synth
     K = 512
@@ -196,7 +243,8 @@ def test_q8_1_properties(orc):
 
 
 # ------------------------------------------------------------------ GEMV
-@pytest.mark.parametrize("qtype,K", [(Q4_K, 512), (Q6_K, 768), (Q8_0, 160)])
+@pytest.mark.parametrize("qtype,K", [(Q4_K, 512), (Q5_K, 512), (Q6_K, 768), (Q8_0, 160),
+                                     (Q8_K, 512)])
 def test_gemv_exact_brute_force(orc, qtype, K):
     from inferflux_amd import synth
     M, N = 3, 9
@@ -207,7 +255,8 @@ def test_gemv_exact_brute_force(orc, qtype, K):
     assert np.allclose(y, want, rtol=1e-12, atol=1e-12)
 
 
-@pytest.mark.parametrize("qtype,K", [(Q4_K, 1024), (Q6_K, 1024), (Q8_0, 1024)])
+@pytest.mark.parametrize("qtype,K", [(Q4_K, 1024), (Q5_K, 1024), (Q6_K, 1024), (Q8_0, 1024),
+                                     (Q8_K, 1024)])
 def test_gemv_q8_1_vs_exact(orc, qtype, K):
     from inferflux_amd import synth
     M, N = 4, 64
