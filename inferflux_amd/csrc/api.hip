@@ -36,6 +36,10 @@ hipError_t launch_mmq_skinny(int qtype, int count, const void *const *W, void *c
                              int K, int mode, hipStream_t stream);
 hipError_t launch_gemm_mfma(int qtype, const void *W, const void *A, void *Y, const void *bias,
                             bool f16, int M, int N, int K, int mode, hipStream_t stream);
+bool gemv_lds_fits(int qtype, int M, int K);
+hipError_t launch_gemv_lds(int count, const void *const *W, void *const *Y, const int *N,
+                           const void *bias, const void *A, bool f16, int M, int K, int mode,
+                           hipStream_t stream);
 }  // namespace ifx
 
 namespace {
@@ -73,6 +77,21 @@ bool use_skinny(int M) {
     return e ? (e[0] == 's' ? 1 : e[0] == 'm' ? 2 : 0) : 0;
   }();
   return v == 1 || (v == 0 && M > 16);
+}
+
+// Q4_K decode batches where the GEMV with activations in LDS
+// (gemv_lds.hip) beats the MFMA kernel, measured on MI355X with cold
+// weights: M = 3 (K <= 5120), and M = 4 on wide launches (K <= 2048, at
+// least 16384 rows).  Its VALU work grows with M, so M >= 5 stays on MFMA.
+// IFX_LDS=0|1 forces it off / on for every shape it fits (tuning; read once).
+bool use_lds(int qtype, int M, int K, int n_total) {
+  static const int v = [] {
+    const char *e = getenv("IFX_LDS");
+    return e ? (e[0] == '1' ? 1 : 0) : -1;
+  }();
+  if (!ifx::gemv_lds_fits(qtype, M, K) || v == 0) return false;
+  if (v == 1) return true;
+  return M == 3 || (M == 4 && K <= 2048 && n_total >= 16384);
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
@@ -150,7 +169,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
-  if (gemv_only(quant_type)) return 1;
+  if (gemv_only(quant_type) || use_lds(quant_type, M, K, N)) return 1;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   return M <= kMaxSkinnyM ? 2 : 3;
 }
@@ -197,6 +216,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   const bool f16 = out_dtype == IFX_OUT_F16;
   if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  if (use_lds(quant_type, M, K, N))
+    return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(
@@ -222,6 +243,10 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
         ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
+  int n_total = 0;
+  for (int i = 0; i < count; ++i) n_total += N[i];
+  if (use_lds(quant_type, M, K, n_total))
+    return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16,

@@ -183,6 +183,10 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 1, 11008, 2048) == KernelFamily::kGemv);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 2, 11008, 2048) == KernelFamily::kGemv);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 8, 11008, 2048) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 3, 11008, 2048) == KernelFamily::kGemv);  // LDS-A GEMV
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 4, 22016, 2048) == KernelFamily::kGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 4, 11008, 2048) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 3, 11008, 2048) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kTiledMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kSkinnyMfma);

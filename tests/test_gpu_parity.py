@@ -115,6 +115,8 @@ for qt in (Q4_K, Q6_K, Q8_0):
     CASES.append((qt, 1, 37, 5120))
     CASES.append((qt, 8, 129, 11008 if qt != Q6_K else 13824))
 CASES.append((Q8_0, 3, 50, 96))     # K not a multiple of 256
+CASES.append((Q4_K, 3, 300, 5120))  # activations-in-LDS GEMV, full-wave rows
+CASES.append((Q4_K, 4, 16400, 2048))  # activations-in-LDS GEMV, M = 4 wide launch
 for qt in (Q5_K, Q8_K):             # GEMV-only types, M <= 64
     for M in (1, 2, 3, 8, 17, 64):
         CASES.append((qt, M, 300, 2048))
@@ -148,7 +150,7 @@ def test_gemv_reference_patterns(orc, dev, qtype):
 
 
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0, Q5_K, Q8_K])
-@pytest.mark.parametrize("M", [1, 8, 24])
+@pytest.mark.parametrize("M", [1, 3, 8, 24])
 def test_epilogues(orc, dev, qtype, M):
     """Accumulate (GemvQ8_1Accum / AccumF32) and bias (GemvQ8_1WithBias),
     fp32 and fp16 outputs."""
@@ -254,6 +256,8 @@ def test_config5_prefill(orc, dev, qtype, N, K):
     (Q8_0, 2, 2080, (7, 129, 64)),         # K not a multiple of 256
     (Q4_K, 8, 2048, (300, 173)),           # M > 2: one MFMA launch per projection
     (Q5_K, 1, 2048, (300, 173, 64)),
+    (Q4_K, 3, 2048, (300, 173)),           # activations-in-LDS GEMV, grouped
+    (Q4_K, 4, 2048, (11008, 11008)),
     (Q8_K, 5, 1024, (129, 77)),
 ])
 def test_grouped_parity(orc, dev, qtype, M, K, Ns):
