@@ -40,6 +40,10 @@ bool gemv_lds_fits(int qtype, int M, int K);
 hipError_t launch_gemv_lds(int count, const void *const *W, void *const *Y, const int *N,
                            const void *bias, const void *A, bool f16, int M, int K, int mode,
                            hipStream_t stream);
+bool gemv_slot_fits(int qtype, int M, int K);
+hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
+                            const int *N, const void *bias, const void *A, bool f16, int M, int K,
+                            int mode, hipStream_t stream);
 }  // namespace ifx
 
 namespace {
@@ -92,6 +96,23 @@ bool use_lds(int qtype, int M, int K, int n_total) {
   if (!ifx::gemv_lds_fits(qtype, M, K) || v == 0) return false;
   if (v == 1) return true;
   return M == 3 || (M == 4 && K <= 2048 && n_total >= 16384);
+}
+
+// Q4_K / Q6_K decode batches on the slot-packed MFMA GEMV (gemv_slot.hip),
+// measured on MI355X with cold weights against the LDS-staged MFMA kernel:
+// 5 <= M <= 8 on launches of at least 8192 rows (gate/up, LM head), and on
+// long-K launches with fp32 outputs (K >= 8192: the down projection), which
+// it splits over several workgroups.  Narrow launches with a short K (Q/K/V,
+// O) stay on mmvq.hip.  IFX_SLOT=0|1 forces it off / on for every M it fits
+// (1..8; tuning; read once).
+bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
+  static const int v = [] {
+    const char *e = getenv("IFX_SLOT");
+    return e ? (e[0] == '1' ? 1 : 0) : -1;
+  }();
+  if (!ifx::gemv_slot_fits(qtype, M, K) || v == 0) return false;
+  if (v == 1) return true;
+  return M >= 5 && (n_total >= 8192 || (K >= 8192 && !f16));
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
@@ -218,6 +239,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (use_lds(quant_type, M, K, N))
     return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  if (use_slot(quant_type, M, K, N, f16))
+    return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(
@@ -247,6 +270,9 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   for (int i = 0; i < count; ++i) n_total += N[i];
   if (use_lds(quant_type, M, K, n_total))
     return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
+  if (use_slot(quant_type, M, K, n_total, f16))
+    return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                           mode, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16,

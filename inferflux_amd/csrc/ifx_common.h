@@ -158,4 +158,12 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// Zeroes up to three fp32 outputs before a split-K launch adds into them
+// (mmq_skinny.hip); blockIdx.y selects the output.
+struct FillArgs {
+  float *y[3];
+  int64_t n[3];
+};
+__global__ void k_fill_zero(const FillArgs f);
+
 }  // namespace ifx

@@ -190,12 +190,8 @@ struct SkArgs {
   int M, K, mode, sb_per;
 };
 
-// Zeroes up to three fp32 outputs (the split-K kernel adds into them);
+// Zeroes up to three fp32 outputs (the split-K kernels add into them);
 // blockIdx.y selects the output.
-struct FillArgs {
-  float *y[3];
-  int64_t n[3];
-};
 __global__ __launch_bounds__(256) void k_fill_zero(const FillArgs f) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < f.n[blockIdx.y]) f.y[blockIdx.y][i] = 0.0f;

@@ -117,6 +117,11 @@ for qt in (Q4_K, Q6_K, Q8_0):
 CASES.append((Q8_0, 3, 50, 96))     # K not a multiple of 256
 CASES.append((Q4_K, 3, 300, 5120))  # activations-in-LDS GEMV, full-wave rows
 CASES.append((Q4_K, 4, 16400, 2048))  # activations-in-LDS GEMV, M = 4 wide launch
+# slot-packed MFMA GEMV (5 <= M <= 16): 8- and 16-row slots, ragged N, one
+# super-block per row, a single row
+CASES += [(Q4_K, 6, 33, 256), (Q6_K, 7, 64, 512), (Q4_K, 12, 1000, 2048),
+          (Q6_K, 16, 1000, 2048), (Q4_K, 16, 31, 5120), (Q6_K, 9, 1, 1024),
+          (Q6_K, 13, 77, 11008)]
 for qt in (Q5_K, Q8_K):             # GEMV-only types, M <= 64
     for M in (1, 2, 3, 8, 17, 64):
         CASES.append((qt, M, 300, 2048))
@@ -173,6 +178,35 @@ def test_epilogues(orc, dev, qtype, M):
     b16 = base.astype(np.float16)
     y16 = ops.qgemv(qtype, W, A, M, N, K, out=up(b16, dev), mode=ops.ACCUM)
     check_rows(down(y16).astype(np.float64), ye + b16.astype(np.float64), tol=2e-3)
+
+
+@pytest.mark.parametrize("qtype,M,N,K", [
+    (Q4_K, 6, 8200, 512),    # slot-packed GEMV, wide launch (ragged last row group)
+    (Q6_K, 8, 8195, 256),    # one super-block per row
+    (Q6_K, 5, 96, 8192),     # long K, few rows: split over workgroups (atomics)
+    (Q4_K, 8, 33, 11008),
+])
+def test_slot_epilogues(orc, dev, qtype, M, N, K):
+    """Store, accumulate and bias modes of the slot-packed MFMA GEMV, with
+    and without the workgroup split of K; fp16 outputs (never split)."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"slot epilogue type={qtype} M={M} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=N + 7)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=K + 1, outlier_frac=0.01))
+    ye = orc.gemv_exact(qtype, w, a, M, N, K)
+    base = np.random.default_rng(5).standard_normal((M, N)).astype(np.float32)
+    bias = np.random.default_rng(6).standard_normal(N).astype(np.float32)
+    W, A = up(w, dev), up(a, dev)
+    # a store after garbage in the output: the split path zeroes it first
+    y = ops.qgemv(qtype, W, A, M, N, K, out=torch.full((M, N), 7.0, device=dev))
+    check_rows(down(y), ye)
+    y = ops.qgemv(qtype, W, A, M, N, K, out=up(base, dev), mode=ops.ACCUM)
+    check_rows(down(y), ye + base)
+    y = ops.qgemv(qtype, W, A, M, N, K, mode=ops.BIAS, bias=up(bias, dev))
+    check_rows(down(y), ye + bias[None, :])
+    y16 = ops.qgemv(qtype, W, A, M, N, K, out_dtype=torch.float16)
+    check_rows(down(y16).astype(np.float64), ye, tol=2e-3)
 
 
 # ------------------------------------------------------------ MFMA GEMM
@@ -259,6 +293,10 @@ def test_config5_prefill(orc, dev, qtype, N, K):
     (Q4_K, 3, 2048, (300, 173)),           # activations-in-LDS GEMV, grouped
     (Q4_K, 4, 2048, (11008, 11008)),
     (Q8_K, 5, 1024, (129, 77)),
+    (Q6_K, 12, 1024, (33, 1, 250)),        # slot-packed MFMA GEMV, grouped
+    (Q4_K, 16, 2048, (2048, 256, 256)),
+    (Q4_K, 7, 2048, (11008, 11008)),       # slot-packed GEMV, grouped wide launch
+    (Q6_K, 8, 8192, (40, 64)),             # slot-packed GEMV, grouped split
 ])
 def test_grouped_parity(orc, dev, qtype, M, K, Ns):
     import torch
