@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE), each scaled by what the counter reads for a copy
@@ -322,12 +323,16 @@ def main():
             x = torch.from_numpy(synth.activations(M, K, seed=5, outlier_frac=0.01)).to(dev)
             A = ops.quantize_q8_1(x)
             Y = torch.empty((M, N), dtype=torch.float32, device=dev)
-            us = time_loop(lambda i: ops.qgemv(qt, w, A, M, N, K, out=Y, prefill=True),
-                           max(10, args.steps // 10), 3)
-            tops = 2.0 * M * N * K / us / 1e6
-            c5[f"{name}_{ops.TYPE_NAMES[qt]}_{N}x{K}"] = {
-                "us": round(us, 1), "int8_TOPS": round(tops, 1),
-                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+            res = {}
+            for kname, kern in (("f16", ops.PREFILL_F16), ("int8", ops.PREFILL_INT8)):
+                us = time_loop(lambda i, kern=kern: ops.qgemm_prefill_kernel(
+                    qt, w, A, M, N, K, kern, out=Y), max(10, args.steps // 10), 3)
+                tops = 2.0 * M * N * K / us / 1e6
+                res[kname] = {"us": round(us, 1), "TOPS": round(tops, 1),
+                              "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+            res["f16"]["frac_f16_peak"] = round(res["f16"]["TOPS"] / F16_PEAK_TFLOPS, 4)
+            res["default"] = "f16" if ops.kernel_family(qt, M, N, K) == 4 else "int8"
+            c5[f"{name}_{ops.TYPE_NAMES[qt]}_{N}x{K}"] = res
             del w
             torch.cuda.empty_cache()
         extras["config5_prefill_M512"] = c5

@@ -56,7 +56,13 @@ struct NativeExecutionPolicy {
 };
 
 // Which gfx950 kernel family a (quant type, M, N, K) runs on.
-enum class KernelFamily : int { kNone = 0, kGemv = 1, kSkinnyMfma = 2, kTiledMfma = 3 };
+enum class KernelFamily : int {
+  kNone = 0,
+  kGemv = 1,
+  kSkinnyMfma = 2,
+  kTiledMfma = 3,
+  kF16DequantMfma = 4  // fp16 MFMA with in-kernel dequant (prefill, M >= 128)
+};
 
 class FusedQuantGemm {
  public:

@@ -119,13 +119,29 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
                            const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
                            int N, int K, void *stream);
 
-/* The prefill GEMM alone (int8 MFMA, fp32 accumulate), for any M >= 1.
- * Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
+/* The prefill GEMM alone, for any M >= 1, fp32 accumulate: the int8 MFMA
+ * GEMM below 128 rows, from 128 rows on the fp16 MFMA GEMM with in-kernel
+ * dequant (see ifx_qgemm_prefill_kernel).  Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
  * (quantized_weight_map.cpp:176-233, cublas_gemm.h:47, called at
  * transformer_forward.cu:1479). */
 int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y,
                       int out_dtype, int mode, const void *bias, int M, int N, int K,
                       void *stream);
+
+/* The prefill GEMM with an explicit kernel: IFX_PREFILL_INT8 is the
+ * integer-exact int8 MFMA GEMM (the MMQ per-block arithmetic of
+ * kernels/mmq.cuh:41-835); IFX_PREFILL_F16 dequantizes W (and the Q8_1
+ * activations) to fp16 inside the kernel and runs fp16 MFMA with fp32
+ * accumulation, the arithmetic of the reference's dequantize + FP16 GEMM
+ * prefill path (quantized_weight_map.cpp:176-233, cublas_gemm.h:47); it
+ * needs K % 256 == 0 (Q8_0: K % 64 == 0).  splits: K split over workgroups
+ * for fp32 outputs (0 = chosen from the shape; ignored by the int8 kernel
+ * and for fp16 outputs).  ifx_qgemm_prefill picks the kernel by M.  No
+ * reference counterpart as a separate entry point (tuning and tests). */
+enum ifx_prefill_kernel { IFX_PREFILL_INT8 = 1, IFX_PREFILL_F16 = 2 };
+int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                             int out_dtype, int mode, const void *bias, int M, int N, int K,
+                             int kernel, int splits, void *stream);
 
 /* Whole-tensor dequantization of n_rows x K weights to fp32 or fp16.
  * Replaces dequantize_q4_k / dequantize_q6_k / dequantize_q8_0
@@ -140,7 +156,8 @@ int ifx_supports(int quant_type, int M, int N, int K);
 
 /* Kernel family ifx_qgemv runs (quant_type, M, N, K) on: 0 = not supported,
  * 1 = v_dot4 GEMV, 2 = skinny int8 MFMA (decode batches), 3 = tiled int8
- * MFMA (prefill).  No reference counterpart (the reference logs the choice,
+ * MFMA, 4 = fp16 MFMA with in-kernel dequant (prefill, M >= 128).  No
+ * reference counterpart (the reference logs the choice,
  * fused_quant_gemm.cu:2104-2117). */
 int ifx_kernel_family(int quant_type, int M, int N, int K);
 

@@ -21,6 +21,7 @@ SIGNATURES = {
     "ifx_qgemv_grouped": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemv_gate_up_silu": ([_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_supports": ([_i32, _i32, _i32, _i32], _i32),

@@ -40,6 +40,10 @@ bool gemv_lds_fits(int qtype, int M, int K);
 hipError_t launch_gemv_lds(int count, const void *const *W, void *const *Y, const int *N,
                            const void *bias, const void *A, bool f16, int M, int K, int mode,
                            hipStream_t stream);
+bool gemm_f16_fits(int qtype, int K);
+hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *Y, const void *bias,
+                           bool f16, int M, int N, int K, int mode, int splits_req,
+                           hipStream_t stream);
 bool gemv_slot_fits(int qtype, int M, int K);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
@@ -53,8 +57,23 @@ namespace {
 //   M <= 2       v_dot4 GEMV        (gemv.hip)
 //   3 <= M <= 32 skinny int8 MFMA   (mmq_skinny.hip), K % 256 == 0
 //   M > 32       tiled int8 MFMA    (gemm_mfma.hip)
+//   M >= 128     fp16 MFMA with in-kernel dequant (gemm_f16.hip), the
+//                reference's FP16 prefill arithmetic
 constexpr int kMaxGemvMDefault = 2;
 constexpr int kMaxSkinnyM = 32;
+constexpr int kMinF16GemmM = 128;
+
+// Prefill kernel for M > 32: the fp16 GEMM from kMinF16GemmM rows on (a
+// 256-row tile is mostly padding below that).  IFX_PREFILL=int8|f16 forces
+// one (tuning; read once).
+bool use_f16_gemm(int qtype, int M, int K) {
+  static const int v = [] {
+    const char *e = getenv("IFX_PREFILL");
+    return e ? (e[0] == 'i' ? 1 : e[0] == 'f' ? 2 : 0) : 0;
+  }();
+  if (!ifx::gemm_f16_fits(qtype, K) || v == 1) return false;
+  return v == 2 || M >= kMinF16GemmM;
+}
 // Q5_K and Q8_K run on the v_dot4 GEMV only, for M <= 64: the reference's
 // Q8_K dispatch stops at 64 (fused_quant_gemm.cu:1740-1747) and it has no
 // fused Q5_K kernel at all (dequantize + cuBLAS); larger M is "not handled".
@@ -191,6 +210,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
   if (gemv_only(quant_type) || use_lds(quant_type, M, K, N)) return 1;
+  if (M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K)) return 4;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   return M <= kMaxSkinnyM ? 2 : 3;
 }
@@ -235,6 +255,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
+  if (!gemv_only(quant_type) && M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K))
+    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, 0, s));
   if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (use_lds(quant_type, M, K, N))
@@ -314,9 +336,26 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
   if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
-  return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias,
-                                         out_dtype == IFX_OUT_F16, M, N, K, mode,
-                                         static_cast<hipStream_t>(stream)));
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (use_f16_gemm(quant_type, M, K))
+    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, 0, s));
+  return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+}
+
+int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                             int out_dtype, int mode, const void *bias, int M, int N, int K,
+                             int kernel, int splits, void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kernel == IFX_PREFILL_INT8)
+    return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  if (kernel != IFX_PREFILL_F16 || splits < 0) return IFX_BAD_GEOMETRY;
+  if (!ifx::gemm_f16_fits(quant_type, K)) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, splits, s));
 }
 
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,

@@ -242,6 +242,7 @@ const char *FusedQuantGemm::KernelFamilyName(KernelFamily family) {
   case KernelFamily::kGemv: return "v_dot4 GEMV";
   case KernelFamily::kSkinnyMfma: return "skinny int8 MFMA";
   case KernelFamily::kTiledMfma: return "tiled int8 MFMA";
+  case KernelFamily::kF16DequantMfma: return "fp16 MFMA, in-kernel dequant";
   default: return "none";
   }
 }

@@ -128,6 +128,28 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     return out
 
 
+PREFILL_INT8, PREFILL_F16 = 1, 2
+
+
+def qgemm_prefill_kernel(qtype, W, A, M, N, K, kernel, splits=0, out=None,
+                         out_dtype=torch.float32, mode=STORE, bias=None, stream=None):
+    """The prefill GEMM on an explicit kernel (PREFILL_INT8: integer-exact
+    int8 MFMA; PREFILL_F16: in-kernel dequant to fp16 + fp16 MFMA).  splits
+    forces the K split of the fp16 kernel (0 = chosen from the shape)."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, N, K) or A.numel() < M * (K // 32) * 36 \
+            or out.numel() < M * N:
+        raise ValueError("W, A or out is smaller than the shape")
+    bptr = _dev(bias, "bias") if bias is not None else None
+    rc = _lib.load().ifx_qgemm_prefill_kernel(qtype, _dev(W, "W"), _dev(A, "A"),
+                                              _dev(out, "out"), od, mode, bptr, M, N, K,
+                                              kernel, splits, _stream(stream))
+    _check(rc, "ifx_qgemm_prefill_kernel")
+    return out
+
+
 def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mode=STORE,
                   stream=None):
     """Sibling projections over one Q8_1 A: [W_i . a for W_i in Ws], one launch
@@ -193,3 +215,8 @@ def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None):
 
 def supports(qtype, M, N, K):
     return bool(_lib.load().ifx_supports(qtype, M, N, K))
+
+
+def kernel_family(qtype, M, N, K):
+    """Kernel family ifx_qgemv runs the shape on (include/ifx_qgemm.h)."""
+    return int(_lib.load().ifx_kernel_family(qtype, M, N, K))

@@ -188,7 +188,9 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 4, 11008, 2048) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 3, 11008, 2048) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kSkinnyMfma);
-  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kTiledMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kF16DequantMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 64, 27648, 5120) == KernelFamily::kTiledMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 512, 64, 2080) == KernelFamily::kGemv);  // K % 64 != 0
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 40, 64, 2080) == KernelFamily::kGemv);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 1, 64, 100) == KernelFamily::kNone);

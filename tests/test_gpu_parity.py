@@ -226,6 +226,68 @@ def test_gemm_parity(orc, dev, qtype, M, N, K):
     check_rows(down(ops.qgemv(qtype, W, A, M, N, K, prefill=True)), ye)
 
 
+@pytest.mark.parametrize("qtype,M,N,K", [
+    (Q4_K, 130, 300, 768), (Q6_K, 200, 129, 512), (Q8_0, 64, 77, 512),
+])
+def test_gemm_int8_kernel_parity(orc, dev, qtype, M, N, K):
+    """The integer-exact int8 MFMA GEMM, which the dispatch no longer picks
+    from 128 rows on, stays reachable and correct."""
+    from inferflux_amd import ops, synth
+    note(f"gemm int8 type={qtype} M={M} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=N * 3 + K)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=M, outlier_frac=0.01))
+    ye = orc.gemv_exact(qtype, w, a, M, N, K)
+    y = ops.qgemm_prefill_kernel(qtype, up(w, dev), up(a, dev), M, N, K, ops.PREFILL_INT8)
+    check_rows(down(y), ye)
+
+
+# fp16 GEMM with in-kernel dequant: ragged M/N edges, one-stage K, forced
+# K splits (fp32 atomics), every output mode and fp16 output.
+@pytest.mark.parametrize("qtype,M,N,K,splits", [
+    (Q4_K, 1, 64, 256, 0), (Q4_K, 256, 256, 256, 0), (Q4_K, 300, 513, 1024, 0),
+    (Q4_K, 77, 100, 2048, 3), (Q6_K, 129, 257, 512, 0), (Q6_K, 512, 64, 2048, 5),
+    (Q8_0, 200, 300, 192, 0), (Q8_0, 33, 64, 512, 2), (Q6_K, 40, 300, 256, 4),
+])
+def test_gemm_f16_parity(orc, dev, qtype, M, N, K, splits):
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemm f16 type={qtype} M={M} N={N} K={K} splits={splits}")
+    w = synth.blocks(qtype, N, K, seed=N * 7 + K)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=M + 1, outlier_frac=0.01))
+    ye = orc.gemv_exact(qtype, w, a, M, N, K)
+    W, A = up(w, dev), up(a, dev)
+    rng = np.random.default_rng(M)
+    base = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    f = ops.PREFILL_F16
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, f, splits,
+                                 out=torch.full((M, N), 7.0, device=dev))
+    check_rows(down(y), ye)
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, f, splits, out=up(base, dev),
+                                 mode=ops.ACCUM)
+    check_rows(down(y), ye + base)
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, f, splits, mode=ops.BIAS,
+                                 bias=up(bias, dev))
+    check_rows(down(y), ye + bias[None, :])
+    y16 = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, f, splits, out_dtype=torch.float16)
+    check_rows(down(y16).astype(np.float64), ye, tol=2e-3)
+    b16 = up(bias.astype(np.float16), dev)
+    y16 = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, f, splits, out_dtype=torch.float16,
+                                   mode=ops.BIAS, bias=b16)
+    check_rows(down(y16).astype(np.float64), ye + bias.astype(np.float16)[None, :], tol=2e-3)
+
+
+def test_gemm_f16_rejects_ragged_k(dev):
+    import torch
+    from inferflux_amd import ops
+    W = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    A = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    # Q8_0 with K % 64 != 0 has no fp16 stage layout: not handled
+    with pytest.raises(ops.NotHandled) as e:
+        ops.qgemm_prefill_kernel(Q8_0, W, A, 2, 4, 96, ops.PREFILL_F16)
+    assert e.value.status == 2
+
+
 def test_prefill_small_m_via_prefill_entry(orc, dev):
     from inferflux_amd import ops, synth
     qtype, M, N, K = Q4_K, 3, 64, 512
