@@ -61,7 +61,8 @@ enum class KernelFamily : int {
   kGemv = 1,
   kSkinnyMfma = 2,
   kTiledMfma = 3,
-  kF16DequantMfma = 4  // fp16 MFMA with in-kernel dequant (prefill, M >= 128)
+  kF16DequantMfma = 4,  // fp16 MFMA with in-kernel dequant (prefill, M >= 128)
+  kF16DequantGemv = 5   // fp16 dequant MFMA GEMV (decode batches 17 <= M <= 32)
 };
 
 class FusedQuantGemm {

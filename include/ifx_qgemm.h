@@ -134,11 +134,13 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
  * activations) to fp16 inside the kernel and runs fp16 MFMA with fp32
  * accumulation, the arithmetic of the reference's dequantize + FP16 GEMM
  * prefill path (quantized_weight_map.cpp:176-233, cublas_gemm.h:47); it
- * needs K % 256 == 0 (Q8_0: K % 64 == 0).  splits: K split over workgroups
+ * needs K % 256 == 0 (Q8_0: K % 64 == 0).  IFX_DECODE_DQ_F16 is the
+ * decode-batch kernel with the same fp16 arithmetic (1 <= M <= 32,
+ * K % 256 == 0).  splits: K split over workgroups
  * for fp32 outputs (0 = chosen from the shape; ignored by the int8 kernel
  * and for fp16 outputs).  ifx_qgemm_prefill picks the kernel by M.  No
  * reference counterpart as a separate entry point (tuning and tests). */
-enum ifx_prefill_kernel { IFX_PREFILL_INT8 = 1, IFX_PREFILL_F16 = 2 };
+enum ifx_prefill_kernel { IFX_PREFILL_INT8 = 1, IFX_PREFILL_F16 = 2, IFX_DECODE_DQ_F16 = 3 };
 int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
                              int out_dtype, int mode, const void *bias, int M, int N, int K,
                              int kernel, int splits, void *stream);
@@ -156,7 +158,8 @@ int ifx_supports(int quant_type, int M, int N, int K);
 
 /* Kernel family ifx_qgemv runs (quant_type, M, N, K) on: 0 = not supported,
  * 1 = v_dot4 GEMV, 2 = skinny int8 MFMA (decode batches), 3 = tiled int8
- * MFMA, 4 = fp16 MFMA with in-kernel dequant (prefill, M >= 128).  No
+ * MFMA, 4 = fp16 MFMA with in-kernel dequant (prefill, M >= 128), 5 = fp16
+ * dequant MFMA GEMV (decode batches 17 <= M <= 32).  No
  * reference counterpart (the reference logs the choice,
  * fused_quant_gemm.cu:2104-2117). */
 int ifx_kernel_family(int quant_type, int M, int N, int K);

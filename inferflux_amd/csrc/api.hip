@@ -44,6 +44,11 @@ bool gemm_f16_fits(int qtype, int K);
 hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *Y, const void *bias,
                            bool f16, int M, int N, int K, int mode, int splits_req,
                            hipStream_t stream);
+bool gemv_dq_fits(int qtype, int M, int K);
+bool gemv_dq_fits_f16(int M, int K);
+hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
+                          const int *N, const void *bias, const void *A, bool f16, int M, int K,
+                          int mode, int splits_req, hipStream_t stream);
 bool gemv_slot_fits(int qtype, int M, int K);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
@@ -134,6 +139,23 @@ bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
   return M >= 5 && (n_total >= 8192 || (K >= 8192 && !f16));
 }
 
+// Decode batches 17 <= M <= 32 on the fp16-dequant MFMA GEMV (gemv_dq.hip),
+// measured on MI355X with cold weights against mmq_skinny.hip: 14B gate
+// 13824 x 5120 Q4_K M = 32: 25.6 us (33.8); 14B down 5120 x 13824 Q6_K:
+// 30.3 us (53.3); 3B gate 11008 x 2048: 12.5 us (15.8).  Its VALU work per
+// weight does not grow with M; below M = 17 the integer kernels are faster.
+// IFX_DQ=0|1 forces it off / on for every M it fits (1..32; tuning; read
+// once).
+bool use_dq(int qtype, int M, int K, bool f16) {
+  static const int v = [] {
+    const char *e = getenv("IFX_DQ");
+    return e ? (e[0] == '1' ? 1 : 0) : -1;
+  }();
+  if (!ifx::gemv_dq_fits(qtype, M, K) || (f16 && !ifx::gemv_dq_fits_f16(M, K)) || v == 0)
+    return false;
+  return v == 1 || M > 16;
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int>(e); }
 
 bool gemv_only(int t) { return t == IFX_TYPE_Q5_K || t == IFX_TYPE_Q8_K; }
@@ -212,6 +234,7 @@ int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (gemv_only(quant_type) || use_lds(quant_type, M, K, N)) return 1;
   if (M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K)) return 4;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
+  if (!use_slot(quant_type, M, K, N, false) && use_dq(quant_type, M, K, false)) return 5;
   return M <= kMaxSkinnyM ? 2 : 3;
 }
 
@@ -263,6 +286,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
     return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   if (use_slot(quant_type, M, K, N, f16))
     return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  if (use_dq(quant_type, M, K, f16))
+    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(
@@ -295,6 +320,9 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   if (use_slot(quant_type, M, K, n_total, f16))
     return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                            mode, s));
+  if (use_dq(quant_type, M, K, f16))
+    return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                         mode, 0, s));
   if (M <= kMaxSkinnyM) {
     if (use_skinny(M) && K % 256 == 0)
       return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16,
@@ -353,6 +381,12 @@ int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, 
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (kernel == IFX_PREFILL_INT8)
     return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  if (kernel == IFX_DECODE_DQ_F16) {
+    if (!ifx::gemv_dq_fits(quant_type, M, K) || splits < 0) return IFX_BAD_GEOMETRY;
+    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
+    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode,
+                                         splits, s));
+  }
   if (kernel != IFX_PREFILL_F16 || splits < 0) return IFX_BAD_GEOMETRY;
   if (!ifx::gemm_f16_fits(quant_type, K)) return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, splits, s));

@@ -1,0 +1,454 @@
+// gemv_dq.hip -- decode-batch GEMV (3 <= M <= 32) on the fp16 matrix cores
+// of gfx950: each wave dequantizes its 32 weight rows straight into fp16
+// MFMA operands, so the VALU work per weight does not grow with M.
+//
+// y[m][n] (op)= sum_k W[n][k] * x[m][k], W raw GGUF Q4_K / Q6_K / Q8_0, x
+// given as Q8_1 blocks.  The integer-dot kernels (mmvq.hip, mmq_skinny.hip)
+// rescale every 32-value block result per output, which is VALU work that
+// grows with M (two to three operations per output per block) and at M = 32
+// costs as much as the weights take to stream.  Here the weights become fp16
+// once, as in the reference's FP16 dequantize path
+// (runtime/backends/cuda/native/kernels/quant_common.cuh:100-188):
+//   Q4_K  w = fp16(d*sc) * q - fp16(dmin*m)
+//   Q6_K  w = fp16(d*sc) * (q - 32)
+//   Q8_0  w = fp16(d) * q
+// and x = fp16(d_a) * q_a; v_mfma_f32_32x32x16_f16 accumulates in fp32.
+// The fp16 rounding of w and x (relative 2^-11) stays far inside the
+// contract's 1e-3 * ||y_row|| tolerance at every decode shape.
+//
+// Mapping: MFMA A operand = 32 batch rows (rows >= M read a zero row),
+// B operand = 32 weight rows; lane l supplies row / column l % 32 for the
+// 8-value K group l / 32 and receives column n = l % 32, rows
+// 8*(i/4) + 4*(l/32) + (i%4).  Both lanes of a weight row (l, l + 32) load
+// 16-byte pieces of it side by side (32 contiguous bytes per row and load
+// instruction): Q4_K 16 B of each 32-byte qs chunk plus the header; the
+// eight values an MFMA takes from a lane are 16*h + (0..7 or 8..15) of one
+// sub-block, in the order (0, 2, 1, 3) of each group of four that the
+// packed conversion produces; the activations are staged in that order.
+//
+// Workgroup: 4 waves = 128 weight rows over a range of super-blocks (K split
+// over gridDim.y with fp32 atomics when the rows alone cannot fill the
+// chip).  Per super-block the workgroup converts the batch rows' Q8_1
+// blocks into a double-buffered LDS stage (M x 256 fp16) that all four
+// waves read; the next super-block's weight bytes are loaded while the
+// current one is computed.
+#include "ifx_common.h"
+
+#include <stdlib.h>
+
+namespace ifx {
+
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWaves = 4;
+constexpr int kRowsPerWg = 32 * kWaves;
+constexpr int kMaxM = 32;
+constexpr int kLdsBytes = 65536;  // activation stage: two workgroups per CU
+constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
+
+struct DqSeg {
+  const uint8_t *W;
+  void *Y;
+  const void *bias;
+  int N;
+  int blk_begin;
+};
+struct DqArgs {
+  DqSeg seg[3];
+  int nseg;
+  const uint8_t *A;
+  int M, K, mode, sb_per;
+};
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ h2 splat(float f) {
+  const _Float16 h = static_cast<_Float16>(f);
+  return h2{h, h};
+}
+
+// Signed byte codes (four per word) times d -> fp16 pairs of values (0, 2)
+// and (1, 3): (0x6400 | (q ^ 0x80)) - 1152 = q exactly, one rounding.
+__device__ __forceinline__ void i8x4_to_h(uint32_t x, h2 d, uint32_t &p02, uint32_t &p13) {
+  x ^= 0x80808080u;
+  const h2 off = splat(-1152.0f);
+  p02 = as_u32((as_h2((x & 0x00FF00FFu) | kMagic) + off) * d);
+  p13 = as_u32((as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + off) * d);
+}
+
+// Byte codes v (< 1024, four per word) -> fp16 pairs (v + bias) * d - mn of
+// values (0, 2) and (1, 3).
+__device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint32_t &p02,
+                                          uint32_t &p13) {
+  const h2 a = as_h2((x & 0x00FF00FFu) | kMagic) + bias;
+  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + bias;
+  p02 = as_u32(__builtin_elementwise_fma(a, d, -mn));
+  p13 = as_u32(__builtin_elementwise_fma(b, d, -mn));
+}
+
+// Nibble codes (shift 0: low, 4: high) of two words of packed 4-bit codes
+// -> one 8-value operand (q + bias) * d - mn, one and-or per pair.
+__device__ __forceinline__ h8 op_q4(uint32_t x0, uint32_t x1, int sh, h2 bias, h2 d, h2 mn) {
+  const uint32_t w[4] = {((x0 >> sh) & 0x000F000Fu) | kMagic, ((x0 >> (sh + 8)) & 0x000F000Fu) | kMagic,
+                         ((x1 >> sh) & 0x000F000Fu) | kMagic, ((x1 >> (sh + 8)) & 0x000F000Fu) | kMagic};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = as_u32(__builtin_elementwise_fma(as_h2(w[i]) + bias, d, -mn));
+  return __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// Two words of byte codes -> one 8-value operand.
+__device__ __forceinline__ h8 op_u8(uint32_t x0, uint32_t x1, h2 bias, h2 d, h2 mn) {
+  uint32_t o[4];
+  u8x4_to_h(x0, bias, d, mn, o[0], o[1]);
+  u8x4_to_h(x1, bias, d, mn, o[2], o[3]);
+  return __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
+}
+__device__ __forceinline__ h8 op_i8(uint32_t x0, uint32_t x1, h2 d) {
+  uint32_t o[4];
+  i8x4_to_h(x0, d, o[0], o[1]);
+  i8x4_to_h(x1, d, o[2], o[3]);
+  return __builtin_bit_cast(h8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// One super-block of a lane's weight row in registers.
+template <int QT>
+struct RawW;
+template <>
+struct RawW<kTypeQ4_K> {  // header, qs bytes 32p + 16h .. +15 for p = 0..3
+  u32x4 hdr, qs[4];
+};
+template <>
+struct RawW<kTypeQ6_K> {  // ql bytes 32c + 16h .. (c = 0..3), qh 32g + 16h .., scales, d
+  u32x4 ql[4], qh[2], sc;
+  uint32_t d;
+};
+template <>
+struct RawW<kTypeQ8_0> {  // codes 16h .. 16h+15 and d of the 8 blocks
+  u32x4 q[8];
+  uint32_t d[8];
+};
+
+template <int QT>
+__device__ __forceinline__ void fetch_w(RawW<QT> &r, rsrc_t Wr, uint32_t row_off, int sb, int h) {
+  if constexpr (QT == kTypeQ4_K) {
+    const uint32_t o = row_off + sb * kQ4KBytes;
+    r.hdr = wload<u32x4>(Wr, o, 0);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.qs[p] = wload<u32x4>(Wr, o + 16 + 32 * p + 16 * h, 0);
+  } else if constexpr (QT == kTypeQ6_K) {
+    const uint32_t o = row_off + sb * kQ6KBytes;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.ql[c] = wload<u32x4>(Wr, o + 32 * c + 16 * h, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) r.qh[g] = wload<u32x4>(Wr, o + 128 + 32 * g + 16 * h, 0);
+    r.sc = wload<u32x4>(Wr, o + 192, 0);
+    r.d = wload<uint16_t>(Wr, o + 208, 0);
+  } else {
+    const uint32_t o = row_off + sb * 8 * kQ8_0Bytes;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      r.d[b] = wload<uint16_t>(Wr, o + b * kQ8_0Bytes, 0);
+      r.q[b] = wload<u32x4>(Wr, o + b * kQ8_0Bytes + 2 + 16 * h, 0);
+    }
+  }
+}
+
+// Activation operand: 8 halves of the staged row at value offset `v` of the
+// super-block.
+__device__ __forceinline__ h8 act(const _Float16 *row, int v) {
+  return *reinterpret_cast<const h8 *>(row + v);
+}
+
+__device__ __forceinline__ f32x16 mfma(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// 16 MFMAs of one super-block into acc0 / acc1 (two chains).
+template <int QT>
+__device__ __forceinline__ void compute(const RawW<QT> &r, const _Float16 *sa, int h,
+                                        f32x16 &acc0, f32x16 &acc1) {
+  const int e0 = 16 * h;
+  if constexpr (QT == kTypeQ4_K) {
+    // get_scale_min_k4 (quant_common.cuh:83-94), all eight sub-blocks
+    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+    const uint32_t S0 = r.hdr.y, S1 = r.hdr.z, S2 = r.hdr.w;
+    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, m_lo = S1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+    const h2 bias = splat(-1024.0f);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t scw = p < 2 ? sc_lo : sc_hi, mw = p < 2 ? m_lo : m_hi;
+      const int sh = 16 * (p & 1);
+      const h2 d0 = splat(d * static_cast<float>((scw >> sh) & 0xFFu));
+      const h2 d1 = splat(d * static_cast<float>((scw >> (sh + 8)) & 0xFFu));
+      const h2 n0 = splat(dmin * static_cast<float>((mw >> sh) & 0xFFu));
+      const h2 n1 = splat(dmin * static_cast<float>((mw >> (sh + 8)) & 0xFFu));
+      const u32x4 q = r.qs[p];
+      const int b0 = 64 * p + e0, b1 = 64 * p + 32 + e0;  // value offsets of the two sub-blocks
+      acc0 = mfma(act(sa, b0), op_q4(q.x, q.y, 0, bias, d0, n0), acc0);
+      acc1 = mfma(act(sa, b0 + 8), op_q4(q.z, q.w, 0, bias, d0, n0), acc1);
+      acc0 = mfma(act(sa, b1), op_q4(q.x, q.y, 4, bias, d1, n1), acc0);
+      acc1 = mfma(act(sa, b1 + 8), op_q4(q.z, q.w, 4, bias, d1, n1), acc1);
+    }
+  } else if constexpr (QT == kTypeQ6_K) {
+    // dequant_q6k_element (quant_common.cuh:161-177): chunk c = (g, hf)
+    // holds sub-blocks hf (low nibbles, qh bits 2hf..) and hf + 2 (high
+    // nibbles, qh bits 2hf + 4 ..) of 128-value half g; the 16 values of a
+    // lane share scale g*8 + 2*sub + h.
+    const float d = h2f(r.d);
+    const uint32_t scb[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    const h2 bias = splat(-1056.0f), zero = splat(0.0f);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int g = c >> 1, hf = c & 1;
+      const int ilo = g * 8 + 2 * hf + h, ihi = g * 8 + 2 * (hf + 2) + h;
+      const float slo = static_cast<float>(static_cast<int8_t>((scb[ilo >> 2] >> (8 * (ilo & 3))) & 0xFFu));
+      const float shi = static_cast<float>(static_cast<int8_t>((scb[ihi >> 2] >> (8 * (ihi & 3))) & 0xFFu));
+      const h2 dl = splat(d * slo), dh = splat(d * shi);
+      const u32x4 ql = r.ql[c];
+      u32x4 y = r.qh[g];
+      y = u32x4{y.x >> (2 * hf), y.y >> (2 * hf), y.z >> (2 * hf), y.w >> (2 * hf)};
+      const uint32_t lo[4] = {(ql.x & 0x0F0F0F0Fu) | ((y.x << 4) & 0x30303030u),
+                              (ql.y & 0x0F0F0F0Fu) | ((y.y << 4) & 0x30303030u),
+                              (ql.z & 0x0F0F0F0Fu) | ((y.z << 4) & 0x30303030u),
+                              (ql.w & 0x0F0F0F0Fu) | ((y.w << 4) & 0x30303030u)};
+      const uint32_t hi[4] = {((ql.x >> 4) & 0x0F0F0F0Fu) | (y.x & 0x30303030u),
+                              ((ql.y >> 4) & 0x0F0F0F0Fu) | (y.y & 0x30303030u),
+                              ((ql.z >> 4) & 0x0F0F0F0Fu) | (y.z & 0x30303030u),
+                              ((ql.w >> 4) & 0x0F0F0F0Fu) | (y.w & 0x30303030u)};
+      const int blo = g * 128 + hf * 32 + e0, bhi = g * 128 + (hf + 2) * 32 + e0;
+      acc0 = mfma(act(sa, blo), op_u8(lo[0], lo[1], bias, dl, zero), acc0);
+      acc1 = mfma(act(sa, blo + 8), op_u8(lo[2], lo[3], bias, dl, zero), acc1);
+      acc0 = mfma(act(sa, bhi), op_u8(hi[0], hi[1], bias, dh, zero), acc0);
+      acc1 = mfma(act(sa, bhi + 8), op_u8(hi[2], hi[3], bias, dh, zero), acc1);
+    }
+  } else {
+    // dequant_q8_0_element (quant_common.cuh:185-188)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const h2 d = splat(h2f(r.d[b]));
+      const u32x4 q = r.q[b];
+      const int v = 32 * b + e0;
+      if (b & 1) {
+        acc1 = mfma(act(sa, v), op_i8(q.x, q.y, d), acc1);
+        acc1 = mfma(act(sa, v + 8), op_i8(q.z, q.w, d), acc1);
+      } else {
+        acc0 = mfma(act(sa, v), op_i8(q.x, q.y, d), acc0);
+        acc0 = mfma(act(sa, v + 8), op_i8(q.z, q.w, d), acc0);
+      }
+    }
+  }
+}
+
+// Stage the activations of super-blocks [sb0, sb0 + cnt) as fp16: row m at
+// sa + m * pitch, values in the order (0, 2, 1, 3) of each group of four.
+// Up to 4 Q8_1 blocks per thread, all loads issued before any conversion.
+__device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint32_t a_row, int M,
+                                        int sb0, int cnt, int tid) {
+  const int items = M * 8 * cnt;
+  uint32_t ds[4];
+  u32x4 q0[4], q1[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int it = tid + 256 * u;
+    if (it < items) {
+      const int m = it / (8 * cnt), j = it - m * 8 * cnt;
+      const uint32_t o = m * a_row + (sb0 * 8 + j) * kQ8_1Bytes;
+      ds[u] = bload<uint32_t>(Ar, o, 0);
+      q0[u] = bload<u32x4>(Ar, o + 4, 0);
+      q1[u] = bload<u32x4>(Ar, o + 20, 0);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int it = tid + 256 * u;
+    if (it < items) {
+      const int m = it / (8 * cnt), j = it - m * 8 * cnt;
+      const h2 d = splat(h2f(ds[u] & 0xFFFFu));
+      u32x4 *dst = reinterpret_cast<u32x4 *>(sa + m * pitch + 32 * j);
+      const uint32_t in[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t o[4];
+        i8x4_to_h(in[2 * k], d, o[0], o[1]);
+        i8x4_to_h(in[2 * k + 1], d, o[2], o[3]);
+        dst[k] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+}
+
+}  // namespace
+
+__global__ void k_fill_zero(const FillArgs f);
+
+// grid: x = row groups of 128 (all projections), y = super-block splits.
+// Dynamic LDS: (M + 1) rows of pitch = sb_per * 256 + 8 halves (row M zero).
+template <int QT, bool F16OUT, bool ATOMIC>
+__global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int bx = blockIdx.x;
+  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+                 : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
+  const DqSeg &sg = args.seg[si];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int M = args.M, K = args.K, N = sg.N;
+  const int nsb = K >> 8;
+  const int sb_begin = blockIdx.y * args.sb_per;
+  const int cnt = min(nsb, sb_begin + args.sb_per) - sb_begin;
+  const int pitch = args.sb_per * 256 + 8;  // halves; 4 dwords mod 64 banks
+
+  const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
+  const uint32_t w_row = static_cast<uint32_t>(
+      QT == kTypeQ8_0 ? (K >> 5) * kQ8_0Bytes : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
+  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(N));
+  const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
+  const int n = (bx - sg.blk_begin) * kRowsPerWg + wave * 32 + l32;
+  const uint32_t row_off = static_cast<uint32_t>(min(n, N - 1)) * w_row;
+  // batch rows past M read the zero row M
+  const _Float16 *arow = lds + (l32 < M ? l32 : M) * pitch;
+
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
+
+  // Three super-blocks of weights in flight per wave (register ring), the
+  // first two issued before the activation stage is built.
+  RawW<QT> w0, w1, w2;
+  if (cnt > 0) fetch_w<QT>(w0, Wr, row_off, sb_begin, h);
+  if (cnt > 1) fetch_w<QT>(w1, Wr, row_off, sb_begin + 1, h);
+  for (int i = tid; i < pitch / 8; i += 64 * kWaves)
+    reinterpret_cast<u32x4 *>(lds + M * pitch)[i] = u32x4{0, 0, 0, 0};
+  stage_a(lds, pitch, Ar, a_row, M, sb_begin, cnt, tid);
+  __syncthreads();
+
+  auto step = [&](const RawW<QT> &cur, RawW<QT> &fut, int i) {
+    if (i + 2 < cnt) fetch_w<QT>(fut, Wr, row_off, sb_begin + i + 2, h);
+    compute<QT>(cur, arow + 256 * i, h, acc0, acc1);
+  };
+  for (int i = 0; i < cnt; i += 3) {
+    step(w0, w2, i);
+    if (i + 1 < cnt) step(w1, w0, i + 1);
+    if (i + 2 < cnt) step(w2, w1, i + 2);
+  }
+
+  if (n >= N) return;
+  // lane holds column n and batch rows 8*(i/4) + 4*h + (i%4)
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    if (m >= M) continue;
+    const int64_t o = static_cast<int64_t>(m) * N + n;
+    float y = acc0[i] + acc1[i];
+    if constexpr (ATOMIC) {
+      if (args.mode == 2 && blockIdx.y == 0) y += static_cast<const float *>(sg.bias)[n];
+      atomicAdd(static_cast<float *>(sg.Y) + o, y);
+    } else if constexpr (F16OUT) {
+      uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
+      if (args.mode == 1) y += h2f(Yh[o]);
+      else if (args.mode == 2) y += h2f(static_cast<const uint16_t *>(sg.bias)[n]);
+      Yh[o] = static_cast<uint16_t>(f2h_bits(y));
+    } else {
+      float *Yf = static_cast<float *>(sg.Y);
+      if (args.mode == 1) y += Yf[o];
+      else if (args.mode == 2) y += static_cast<const float *>(sg.bias)[n];
+      Yf[o] = y;
+    }
+  }
+}
+
+namespace {
+
+// Largest K range (super-blocks) whose fp16 activation stage fits kLdsBytes.
+int dq_sb_max(int M) { return max(1, (kLdsBytes / 2 / (M + 1) - 8) / 256); }
+
+// Super-block splits: at least what the activation stage needs, and enough
+// workgroups for two per CU on 256 CUs; fp16 outputs take one split when
+// the stage allows.  IFX_DQ_WGS sets the workgroup target (tuning; read
+// once).
+int dq_splits(int groups, int nsb, int M, bool f16) {
+  static const int target = [] {
+    const char *e = getenv("IFX_DQ_WGS");
+    return e && atoi(e) > 0 ? atoi(e) : 512;
+  }();
+  const int need = (nsb + dq_sb_max(M) - 1) / dq_sb_max(M);
+  if (f16) return need;
+  return max(need, min(nsb, (target + groups - 1) / groups));
+}
+
+template <int QT>
+hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
+  int groups = 0;
+  for (int i = 0; i < args.nseg; ++i) {
+    args.seg[i].blk_begin = groups;
+    groups += (args.seg[i].N + kRowsPerWg - 1) / kRowsPerWg;
+  }
+  const int nsb = args.K >> 8;
+  const int need = (nsb + dq_sb_max(args.M) - 1) / dq_sb_max(args.M);
+  int ks = (splits_req > 0 && !f16) ? max(need, min(splits_req, nsb))
+                                    : dq_splits(groups, nsb, args.M, f16);
+  if (f16 && ks > 1) return hipErrorInvalidValue;  // fp16 outputs cannot be split
+  args.sb_per = (nsb + ks - 1) / ks;
+  ks = (nsb + args.sb_per - 1) / args.sb_per;
+  const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
+  const dim3 grid(groups, ks), block(64 * kWaves);
+  if (f16) {
+    hipLaunchKernelGGL((k_gemv_dq<QT, true, false>), grid, block, shm, s, args);
+  } else if (ks == 1) {
+    hipLaunchKernelGGL((k_gemv_dq<QT, false, false>), grid, block, shm, s, args);
+  } else {
+    if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
+      FillArgs f{};
+      int64_t nmax = 0;
+      for (int i = 0; i < args.nseg; ++i) {
+        f.y[i] = static_cast<float *>(args.seg[i].Y);
+        f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
+        nmax = max(nmax, f.n[i]);
+      }
+      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 255) / 256), args.nseg),
+                         dim3(256), 0, s, f);
+    }
+    hipLaunchKernelGGL((k_gemv_dq<QT, false, true>), grid, block, shm, s, args);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// fp16 outputs are not split: their K must fit one activation stage.
+bool gemv_dq_fits(int qtype, int M, int K) {
+  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ8_0) && M >= 1 &&
+         M <= kMaxM && K % 256 == 0;
+}
+
+bool gemv_dq_fits_f16(int M, int K) { return M <= kMaxM && K / 256 <= dq_sb_max(M); }
+
+// count projections (1..3) of one quant type share A; bias only with
+// count == 1.  splits_req: 0 = chosen from the shape.
+hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
+                          const int *N, const void *bias, const void *A, bool f16, int M, int K,
+                          int mode, int splits_req, hipStream_t stream) {
+  if (!gemv_dq_fits(qtype, M, K) || count < 1 || count > 3) return hipErrorInvalidValue;
+  DqArgs args{};
+  for (int i = 0; i < count; ++i)
+    args.seg[i] = DqSeg{static_cast<const uint8_t *>(W[i]), Y[i], i == 0 ? bias : nullptr, N[i], 0};
+  args.nseg = count;
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = mode;
+  switch (qtype) {
+  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(args, f16, splits_req, stream);
+  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(args, f16, splits_req, stream);
+  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(args, f16, splits_req, stream);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ifx

@@ -243,6 +243,7 @@ const char *FusedQuantGemm::KernelFamilyName(KernelFamily family) {
   case KernelFamily::kSkinnyMfma: return "skinny int8 MFMA";
   case KernelFamily::kTiledMfma: return "tiled int8 MFMA";
   case KernelFamily::kF16DequantMfma: return "fp16 MFMA, in-kernel dequant";
+  case KernelFamily::kF16DequantGemv: return "fp16 dequant MFMA GEMV";
   default: return "none";
   }
 }

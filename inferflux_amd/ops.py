@@ -128,7 +128,7 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     return out
 
 
-PREFILL_INT8, PREFILL_F16 = 1, 2
+PREFILL_INT8, PREFILL_F16, DECODE_DQ_F16 = 1, 2, 3
 
 
 def qgemm_prefill_kernel(qtype, W, A, M, N, K, kernel, splits=0, out=None,

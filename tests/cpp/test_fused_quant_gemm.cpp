@@ -187,7 +187,8 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 4, 22016, 2048) == KernelFamily::kGemv);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 4, 11008, 2048) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 3, 11008, 2048) == KernelFamily::kSkinnyMfma);
-  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kSkinnyMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 32, 5120, 13824) == KernelFamily::kF16DequantGemv);
+  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 16, 5120, 13824) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kF16DequantMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 64, 27648, 5120) == KernelFamily::kTiledMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 512, 64, 2080) == KernelFamily::kGemv);  // K % 64 != 0

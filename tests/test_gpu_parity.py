@@ -277,6 +277,44 @@ def test_gemm_f16_parity(orc, dev, qtype, M, N, K, splits):
     check_rows(down(y16).astype(np.float64), ye + bias.astype(np.float16)[None, :], tol=2e-3)
 
 
+# decode-batch fp16 dequant kernel: every M up to 32, forced K splits
+# (fp32 atomics after a zero fill), all output modes and fp16 output.
+@pytest.mark.parametrize("qtype,M,N,K,splits", [
+    (Q4_K, 1, 64, 256, 0), (Q4_K, 3, 300, 1024, 0), (Q4_K, 8, 1000, 2048, 0),
+    (Q4_K, 16, 129, 512, 2), (Q4_K, 32, 256, 1536, 3), (Q4_K, 13, 77, 768, 1),
+    (Q6_K, 5, 130, 512, 0), (Q6_K, 16, 256, 2048, 4), (Q6_K, 32, 65, 256, 0),
+    (Q8_0, 4, 200, 512, 0), (Q8_0, 24, 129, 1024, 2), (Q8_0, 32, 64, 256, 1),
+])
+def test_gemv_dq_parity(orc, dev, qtype, M, N, K, splits):
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemv dq type={qtype} M={M} N={N} K={K} splits={splits}")
+    w = synth.blocks(qtype, N, K, seed=N * 5 + K + M)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=M + 7, outlier_frac=0.01))
+    ye = orc.gemv_exact(qtype, w, a, M, N, K)
+    W, A = up(w, dev), up(a, dev)
+    rng = np.random.default_rng(M + N)
+    base = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    kern = ops.DECODE_DQ_F16
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits,
+                                 out=torch.full((M, N), 7.0, device=dev))
+    check_rows(down(y), ye)
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits, out=up(base, dev),
+                                 mode=ops.ACCUM)
+    check_rows(down(y), ye + base)
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits, mode=ops.BIAS,
+                                 bias=up(bias, dev))
+    check_rows(down(y), ye + bias[None, :])
+    if (K // 256) * 256 * (M + 1) * 2 <= 65536 - 16 * (M + 1):  # one activation stage
+        y16 = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits,
+                                       out_dtype=torch.float16)
+        check_rows(down(y16).astype(np.float64), ye, tol=2e-3)
+    else:  # fp16 outputs cannot be split over K
+        with pytest.raises(ops.NotHandled):
+            ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits, out_dtype=torch.float16)
+
+
 def test_gemm_f16_rejects_ragged_k(dev):
     import torch
     from inferflux_amd import ops
