@@ -52,6 +52,10 @@ def parse():
     p.add_argument("--profile", action="store_true",
                    help="profiling run: only the dominant GEMV (eager launches), the HBM "
                         "read probe and a copy of known size for counter calibration")
+    p.add_argument("--profile-kernels", action="store_true",
+                   help="profiling run of the batch kernels: the 32B prefill GEMMs (fp16 and "
+                        "int8 kernels, M = 512) and the 14B gate+up / down decode launches at "
+                        "M = 32 (fp16-dequant GEMV), eager launches, plus the 64 MiB copy")
     return p.parse_args()
 
 
@@ -77,6 +81,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.profile:
         profile_run(args, dev)
+        return
+    if args.profile_kernels:
+        profile_kernels_run(args, dev)
         return
 
     def ev():
@@ -426,6 +433,66 @@ def profile_run(args, dev):
                       "kernel": "k_gemv Q4_K grouped gate+up N=2x11008 K=2048 M=1",
                       "launches": args.steps, "event_us_per_launch": round(gemv_us, 3),
                       "copy_bytes": big.numel(), "read_probe_bytes": nbytes}), flush=True)
+
+
+def profile_kernels_run(args, dev):
+    """Eager launches for rocprofv3 counter runs of the batch kernels:
+    `steps` launches each of the config-5 prefill GEMMs on the fp16 kernel
+    and (a quarter as many) on the int8 kernel, and of the config-4 14B
+    grouped gate+up and down launches at M = 32 (weights rotating over
+    >= 512 MB of replicas), then 20 copies of exactly 64 MiB for counter
+    calibration.  Prints one JSON line of event timings."""
+    import torch
+
+    from inferflux_amd import ops, synth, workloads
+
+    def timed(fn, n):
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        return round(a.elapsed_time(b) * 1e3 / n, 2)
+
+    out = {"profile": "batch kernels"}
+    M = 512
+    for name, qt, N, K in workloads.PREFILL_32B:
+        w = torch.from_numpy(synth.blocks(qt, N, K, seed=5)).to(dev)
+        A = ops.quantize_q8_1(torch.from_numpy(
+            synth.activations(M, K, seed=5, outlier_frac=0.01)).to(dev))
+        Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        for kname, kern, n in (("f16", ops.PREFILL_F16, args.steps),
+                               ("int8", ops.PREFILL_INT8, max(1, args.steps // 4))):
+            out[f"prefill_{name}_{kname}_us"] = timed(
+                lambda i, kern=kern: ops.qgemm_prefill_kernel(qt, w, A, M, N, K, kern, out=Y), n)
+        del w
+    M = 32
+    layer = {n: (qt, N, K) for n, qt, N, K in workloads.QWEN14B_LAYER}
+    for launch, names in (("gate_up", ["gate", "up"]), ("down", ["down"])):
+        qt, _, K = layer[names[0]]
+        Ns = [layer[n][1] for n in names]
+        ws = [torch.from_numpy(synth.blocks(qt, N, K, seed=7 + j)).to(dev)
+              for j, N in enumerate(Ns)]
+        R = max(2, -(-ROTATE_BYTES // sum(w.numel() for w in ws)))
+        reps = [ws] + [[w.clone() for w in ws] for _ in range(R - 1)]
+        A = ops.quantize_q8_1(torch.from_numpy(synth.activations(M, K, seed=8)).to(dev))
+        Ys = [torch.empty((M, N), dtype=torch.float32, device=dev) for N in Ns]
+        out[f"decode14b_{launch}_m32_us"] = timed(
+            lambda i: ops.qgemv_grouped(qt, reps[i % R], A, M, Ns, K, outs=Ys), args.steps)
+        del reps, ws
+        torch.cuda.empty_cache()
+    lib = probe_lib()
+    big = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(big)
+    for _ in range(20):
+        assert lib.ifx_probe_copy(dst.data_ptr(), big.data_ptr(), big.numel(), 8192,
+                                  torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    print(json.dumps(out), flush=True)
 
 
 def cpu_baseline(budget_s):

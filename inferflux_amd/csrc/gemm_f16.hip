@@ -57,9 +57,11 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kPitch = kBK + 8;  // halves per staged row (144 B: conflict-free b128 reads)
-constexpr int kThreads = 512;
 #ifndef IFX_F16_VALU_PER_MFMA
 #define IFX_F16_VALU_PER_MFMA 5
+#endif
+#ifndef IFX_F16_WAVES
+#define IFX_F16_WAVES 8
 #endif
 
 struct Smem {
@@ -154,8 +156,8 @@ __device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint
 
 // Convert one stage's raw bytes and store them in LDS buffer `buf`.
 template <int QT>
-__device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int tid) {
-  const int row = tid >> 1, part = tid & 1;
+__device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int item) {
+  const int row = item >> 1, part = item & 1;
 #ifdef IFX_F16_EXPT_NOACT
   if (false)
 #endif
@@ -255,20 +257,28 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
 
 }  // namespace
 
-// grid.x = n_tiles * splits * m_tiles (remapped per XCD), block 512.
+// grid.x = n_tiles * splits * m_tiles (remapped per XCD), block 64 * WV.
+// WV = 8: waves 4 (m) x 2 (n), each 64 x 128 (2 x 4 MFMA tiles);
+// WV = 4: waves 2 x 2, each 128 x 128 (4 x 4 tiles, accumulators in AGPRs),
+// a third less LDS operand traffic per MFMA and twice the conversion work
+// per thread.
 // Each workgroup covers K stages [split * cps, min(nst, (split + 1) * cps)).
-template <int QT, bool F16OUT, bool ATOMIC>
-__global__ __launch_bounds__(kThreads, 1) void k_gemm_f16(const uint8_t *__restrict__ W,
-                                                          const uint8_t *__restrict__ A,
-                                                          void *__restrict__ Y,
-                                                          const void *__restrict__ bias, int M,
-                                                          int N, int K, int mode, int m_tiles,
-                                                          int splits, int cps) {
+template <int QT, int WV, bool F16OUT, bool ATOMIC>
+__global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restrict__ W,
+                                                         const uint8_t *__restrict__ A,
+                                                         void *__restrict__ Y,
+                                                         const void *__restrict__ bias, int M,
+                                                         int N, int K, int mode, int m_tiles,
+                                                         int splits, int cps) {
+  constexpr int kT = 64 * WV;            // threads
+  constexpr int kFM = WV == 8 ? 2 : 4;   // MFMA tiles per wave along m
+  constexpr int kWM = 32 * kFM;          // wave rows along m
+  constexpr int kIpt = 2 * kBN / kT;     // (row, half) items per thread
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
+  const int wm = WV == 8 ? (wave & 3) : (wave & 1), wn = WV == 8 ? (wave >> 2) : (wave >> 1);
   const int l32 = lane & 31, h = lane >> 5;
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
@@ -291,40 +301,53 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_f16(const uint8_t *__restr
                                             : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
   const rsrc_t Wr = make_rsrc(W, w_row * static_cast<uint32_t>(N));
   const rsrc_t Ar = make_rsrc(A, a_row * static_cast<uint32_t>(M));
-  const int row = tid >> 1, part = tid & 1;
+  const int part = tid & 1;
   // Rows past M or N repeat the last row: their outputs are never stored.
-  const uint32_t a_off = min(m0 + row, M - 1) * a_row;
-  const uint32_t w_off = min(n0 + row, N - 1) * w_row;
-
-  f32x16 acc[2][4];
+  uint32_t a_off[kIpt], w_off[kIpt];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int u = 0; u < kIpt; ++u) {
+    const int row = (tid >> 1) + (kT / 2) * u;
+    a_off[u] = min(m0 + row, M - 1) * a_row;
+    w_off[u] = min(n0 + row, N - 1) * w_row;
+  }
+
+  f32x16 acc[kFM][4];
+#pragma unroll
+  for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto fetch_stage = [&](Raw<QT> &r, int c) {
-    fetch<QT>(r, Wr, Ar, w_off, a_off, c, part);
-    if constexpr (QT == kTypeQ4_K) r.wx0 = static_cast<uint32_t>(c & 3);
-    if constexpr (QT == kTypeQ6_K) {
-      const int hf = c & 1;
-      r.w1 = u32x4{r.w1.x >> (2 * hf), r.w1.y >> (2 * hf), r.w1.z >> (2 * hf), r.w1.w >> (2 * hf)};
+  auto fetch_stage = [&](Raw<QT> *r, int c) {
+#pragma unroll
+    for (int u = 0; u < kIpt; ++u) {
+      fetch<QT>(r[u], Wr, Ar, w_off[u], a_off[u], c, part);
+      if constexpr (QT == kTypeQ4_K) r[u].wx0 = static_cast<uint32_t>(c & 3);
+      if constexpr (QT == kTypeQ6_K) {
+        const int hf = c & 1;
+        r[u].w1 = u32x4{r[u].w1.x >> (2 * hf), r[u].w1.y >> (2 * hf), r[u].w1.z >> (2 * hf),
+                        r[u].w1.w >> (2 * hf)};
+      }
     }
+  };
+  auto commit_stage = [&](int buf, const Raw<QT> *r) {
+#pragma unroll
+    for (int u = 0; u < kIpt; ++u) commit<QT>(sm, buf, r[u], tid + kT * u);
   };
 
   // Stage c+1 is converted into the idle buffer and stage c+2 is fetched in
   // every step, branch-free (past the end they repeat the last stage and
   // fill a buffer nobody reads), so that one basic block holds the MFMAs and
   // the conversion and the scheduler can interleave them.
-  Raw<QT> raw;
+  Raw<QT> raw[kIpt];
   const int c_last = max(c_begin, c_end - 1);
   fetch_stage(raw, c_begin);
-  commit<QT>(sm, 0, raw, tid);
+  commit_stage(0, raw);
   fetch_stage(raw, min(c_begin + 1, c_last));
   __syncthreads();
 
-  const int arow = wm * 64 + l32;   // + 32 * i
+  const int arow = wm * kWM + l32;  // + 32 * i
   const int brow = wn * 128 + l32;  // + 32 * j
   for (int c = c_begin; c < c_end; ++c) {
     const int buf = (c - c_begin) & 1;
@@ -332,24 +355,24 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_f16(const uint8_t *__restr
     const _Float16 *sw = sm.w[buf];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      h8 fa[2], fb[4];
+      h8 fa[kFM], fb[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kFM; ++i)
         fa[i] = *reinterpret_cast<const h8 *>(sa + (arow + 32 * i) * kPitch + ks * 16 + 8 * h);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         fb[j] = *reinterpret_cast<const h8 *>(sw + (brow + 32 * j) * kPitch + ks * 16 + 8 * h);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kFM; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    commit<QT>(sm, buf ^ 1, raw, tid);
+    commit_stage(buf ^ 1, raw);
     fetch_stage(raw, min(c + 2, c_last));
     // issue order: each MFMA followed by a few VALU conversion instructions
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 4 * kFM * 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, IFX_F16_VALU_PER_MFMA, 0);  // VALU
     }
@@ -358,14 +381,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_f16(const uint8_t *__restr
 
   // Epilogue: lane holds column n and rows 8*(e/4) + 4*h + (e%4) of each tile.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + wn * 128 + 32 * j + l32;
       if (n >= N) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        const int m = m0 + wm * kWM + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
         if (m >= M) continue;
         const int64_t o = static_cast<int64_t>(m) * N + n;
         float y = acc[i][j][e];
@@ -389,11 +412,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_f16(const uint8_t *__restr
 
 namespace {
 
-template <int QT, bool F16OUT, bool ATOMIC>
+template <int QT, bool F16OUT, bool ATOMIC, int WV = IFX_F16_WAVES>
 hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, int M, int N,
                     int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
                     hipStream_t s) {
-  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, F16OUT, ATOMIC>);
+  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC>);
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -402,7 +425,7 @@ hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bia
     attr_set = true;
   }
   const dim3 grid(static_cast<unsigned>(m_tiles * n_tiles * splits));
-  hipLaunchKernelGGL((k_gemm_f16<QT, F16OUT, ATOMIC>), grid, dim3(kThreads), sizeof(Smem), s, W,
+  hipLaunchKernelGGL((k_gemm_f16<QT, WV, F16OUT, ATOMIC>), grid, dim3(64 * WV), sizeof(Smem), s, W,
                      A, Y, bias, M, N, K, mode, m_tiles, splits, cps);
   return hipGetLastError();
 }
