@@ -48,8 +48,6 @@
 
 namespace ifx {
 
-__global__ void k_fill_zero(float *__restrict__ y, int64_t n);
-
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -452,9 +450,10 @@ hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *Y, const void *bi
   splits = (nst + cps - 1) / cps;
   if (splits > 1) {
     if (mode != 1) {  // store / bias: the workgroups add into a zeroed Y
-      const int64_t n = static_cast<int64_t>(M) * N;
-      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                         s, static_cast<float *>(Y), n);
+      FillArgs f{};
+      f.y[0] = static_cast<float *>(Y);
+      f.n[0] = static_cast<int64_t>(M) * N;
+      if (launch_fill_zero(f, 1, s) != hipSuccess) return hipGetLastError();
     }
     return launch_k<QT, false, true>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits, cps,
                                      s);

@@ -285,8 +285,6 @@ __device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint
 
 }  // namespace
 
-__global__ void k_fill_zero(const FillArgs f);
-
 // grid: x = row groups of 128 (all projections), y = super-block splits.
 // Dynamic LDS: (M + 1) rows of pitch = sb_per * 256 + 8 halves (row M zero).
 template <int QT, bool F16OUT, bool ATOMIC>
@@ -405,14 +403,11 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
-      int64_t nmax = 0;
       for (int i = 0; i < args.nseg; ++i) {
         f.y[i] = static_cast<float *>(args.seg[i].Y);
         f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
-        nmax = max(nmax, f.n[i]);
       }
-      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 255) / 256), args.nseg),
-                         dim3(256), 0, s, f);
+      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return hipGetLastError();
     }
     hipLaunchKernelGGL((k_gemv_dq<QT, false, true>), grid, block, shm, s, args);
   }

@@ -421,14 +421,12 @@ void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t 
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
-      int64_t nmax = 0;
       for (int i = 0; i < args.nseg; ++i) {
         f.y[i] = static_cast<float *>(args.seg[i].Y);
         f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
-        nmax = max(nmax, f.n[i]);
       }
-      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 255) / 256), args.nseg),
-                         dim3(256), 0, s, f);
+      // a failed fill stays set for the caller's hipGetLastError
+      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return;
     }
     slot_launch<QT, MP, KW, false, true>(args, blocks, ks, s);
   }

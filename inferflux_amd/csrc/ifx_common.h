@@ -165,5 +165,8 @@ struct FillArgs {
   int64_t n[3];
 };
 __global__ void k_fill_zero(const FillArgs f);
+// Zeroes the first nseg outputs of f (one launch).  Returns the launch
+// status without clearing it (hipPeekAtLastError).
+hipError_t launch_fill_zero(const FillArgs &f, int nseg, hipStream_t s);
 
 }  // namespace ifx

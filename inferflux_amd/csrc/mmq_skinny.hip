@@ -169,11 +169,6 @@ __device__ __forceinline__ void store_stage(uint8_t *as, uint8_t *ws, const Stag
 
 }  // namespace
 
-__global__ __launch_bounds__(256) void k_fill_zero(float *__restrict__ y, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) y[i] = 0.0f;
-}
-
 // Up to three projections over the same activations (grouped launches):
 // workgroups [seg[i].blk_begin, seg[i + 1].blk_begin) belong to projection i.
 struct SkSeg {
@@ -191,10 +186,27 @@ struct SkArgs {
 };
 
 // Zeroes up to three fp32 outputs (the split-K kernels add into them);
-// blockIdx.y selects the output.
+// blockIdx.y selects the output.  Four floats per thread, one 16-byte store
+// where the output is 16-byte aligned.
 __global__ __launch_bounds__(256) void k_fill_zero(const FillArgs f) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < f.n[blockIdx.y]) f.y[blockIdx.y][i] = 0.0f;
+  float *__restrict__ y = f.y[blockIdx.y];
+  const int64_t n = f.n[blockIdx.y];
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if ((reinterpret_cast<uintptr_t>(y) & 15) == 0 && i + 4 <= n) {
+    *reinterpret_cast<f32x4 *>(y + i) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  } else {
+    for (int64_t j = i; j < n && j < i + 4; ++j) y[j] = 0.0f;
+  }
+}
+
+hipError_t launch_fill_zero(const FillArgs &f, int nseg, hipStream_t s) {
+  int64_t nmax = 0;
+  for (int i = 0; i < nseg; ++i) nmax = max(nmax, f.n[i]);
+  if (nmax == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 1023) / 1024), nseg),
+                     dim3(256), 0, s, f);
+  return hipPeekAtLastError();  // left set for the caller's hipGetLastError
 }
 
 // grid: x = row groups of 64 (all projections), y = super-block splits.
@@ -433,14 +445,11 @@ hipError_t launch_mt(SkArgs args, bool f16, hipStream_t s) {
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
-      int64_t nmax = 0;
       for (int i = 0; i < args.nseg; ++i) {
         f.y[i] = static_cast<float *>(args.seg[i].Y);
         f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
-        nmax = max(nmax, f.n[i]);
       }
-      hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 255) / 256), args.nseg),
-                         dim3(256), 0, s, f);
+      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return hipGetLastError();
     }
     hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, true>), grid, dim3(64 * kWaves), shm, s, args);
   }
