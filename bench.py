@@ -129,12 +129,14 @@ def main():
         del g
         return a.elapsed_time(b) * 1e3 / steps  # us per call
 
-    def decode_layer_runner(layer, M, seed):
+    def decode_layer_runner(layer, M, seed, fused=False):
         """One decode layer at batch M as a chain over an fp32 residual
         stream: RMSNorm+Q8_1 -> grouped QKV -> Q8_1 of the attention output
         (synthetic: attention itself is not on this path) -> O accumulated
         into the residual -> RMSNorm+Q8_1 -> grouped gate/up -> SiLU*up+Q8_1
-        -> down accumulated into the residual.  4 producers + 4 GEMVs."""
+        -> down accumulated into the residual.  4 producers + 4 GEMVs.
+        fused: the two RMSNorm+Q8_1 producers run inside the QKV and gate/up
+        launches (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 2 + 4 launches."""
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
         rng = np.random.default_rng(seed)
         resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
@@ -163,21 +165,28 @@ def main():
                                   [layer[p][1] for p in projs], K,
                                   outs=[Y[p] for p in projs], mode=mode)
 
+        def gemv_norm(lname, r, nw):
+            _, projs, _, _ = launches[lname]
+            qt, _, K, _ = layer[projs[0]]
+            ops.qgemv_grouped_rmsnorm(qt, [layer[p][3][r] for p in projs], resid, nw, M,
+                                      [layer[p][1] for p in projs], K,
+                                      outs=[Y[p] for p in projs])
+
         def run(i, which=None):
             r = i % R
             prod = which is None or which == "producers"
-            if prod:
+            if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["attn"], out=A["attn_in"])
             if which is None or which == "qkv":
-                gemv("qkv", r)
+                gemv_norm("qkv", r, norm_w["attn"]) if fused else gemv("qkv", r)
             if prod:
                 ops.quantize_q8_1(attn, out=A["attn_out"])
             if which is None or which == "o":
                 gemv("o", r)
-            if prod:
+            if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["ffn"], out=A["ffn_in"])
             if which is None or which == "gate_up":
-                gemv("gate_up", r)
+                gemv_norm("gate_up", r, norm_w["ffn"]) if fused else gemv("gate_up", r)
             if prod:
                 ops.silu_mul_quantize_q8_1(Y["gate"], Y["up"], out=A["ffn_act"])
             if which is None or which == "down":
@@ -220,8 +229,20 @@ def main():
             "kernel_us": {k: round(v, 2) for k, v in kern.items()},
             "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_layer * 1e-6), 1),
         }
+        if M <= 2:
+            # the same layer with the RMSNorm producers fused into QKV and gate/up
+            runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=True)
+            us_fused = time_loop(runf, steps, args.warmup)
+            per_m[M]["fused_norm"] = {
+                "us_per_layer": round(us_fused, 2),
+                "kernel_us": {n: round(time_loop(lambda i, n=n: runf(i, n), steps, args.warmup), 2)
+                              for n in ("qkv", "gate_up", "producers")},
+                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_fused * 1e-6), 1),
+            }
         if M == 1:
-            ms_per_step = us_layer / 1e3
+            ms_per_step = min(us_layer, us_fused) / 1e3
+            step_is = ("layer with the RMSNorm producers fused into the QKV and gate/up launches"
+                       if us_fused < us_layer else "layer as the reference launches it")
             headline = q4_bytes / q4_us / 1e3
     extras["qwen3b_layer"] = per_m
 
@@ -365,6 +386,7 @@ def main():
         "config": {"workload": "qwen2.5-3b Q4_K_M decode layer, M=1 (BASELINE config 2)",
                    "M": 1, "hidden": 2048, "ffn": 11008, "weight_replicas": R3,
                    "launches": [l[0] for l in workloads.DECODE_LAUNCHES],
+                   "step": step_is,
                    "value_is": "HBM GB/s of the layer's Q4_K GEMV launches (QKV, O, gate+up)",
                    "frac_of_hbm_peak": round(headline / HBM_PEAK_GBS, 4)},
         "roofline": result["roofline"],

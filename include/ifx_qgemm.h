@@ -104,6 +104,24 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
                       const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                       void *stream);
 
+/* RMSNorm + Q8_1 fused into the grouped GEMV that consumes it: for each
+ * batch row m, a[m] = Q8_1((x[m] * rms(x[m])) * norm_weight), exactly as
+ * ifx_rmsnorm_quantize_q8_1 computes it, then y_i (op)= W_i . a as
+ * ifx_qgemv_grouped.  Every workgroup rebuilds a in LDS after issuing its
+ * first weight loads, so the producer's launch and the Q8_1 round trip
+ * through memory disappear from the decode layer.  residual [M][K] fp32 or
+ * fp16 (residual_dtype: ifx_out_dtype), norm_weight fp16 [K].  Handles
+ * Q4_K, 1 <= M <= 2, M * K/32 * 36 <= 65536; other shapes return
+ * IFX_BAD_GEOMETRY (not handled: use the two calls).  mode: IFX_STORE or
+ * IFX_ACCUM.  No reference counterpart as one call: it fuses
+ * FusedQuantGemm::FusedRmsNormQuantizeQ8_1 (fused_quant_gemm.h:131-150)
+ * with GemvQ8_1Pair / GemvQ8_1Triple (fused_quant_gemm.h:272-276, 309-313),
+ * the sequence of transformer_forward.cu:524-559. */
+int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, void *const *Y,
+                              const int *N, const void *residual, int residual_dtype,
+                              const uint16_t *norm_weight, float eps, int out_dtype, int mode,
+                              int M, int K, void *stream);
+
 /* Fused gate/up GEMV with SiLU: h[m][o] = silu(W_gate[o] . a[m]) *
  * (W_up[o] . a[m]), written to H [M][N] (fp32 or fp16, h_dtype; may be
  * NULL) and/or quantized to Q8_1 blocks of 32 consecutive outputs in

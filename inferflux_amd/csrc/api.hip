@@ -44,6 +44,9 @@ bool gemm_f16_fits(int qtype, int K);
 hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *Y, const void *bias,
                            bool f16, int M, int N, int K, int mode, int splits_req,
                            hipStream_t stream);
+hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, const int *N,
+                               const void *x, bool x_f16, const uint16_t *norm_w, float eps,
+                               bool f16, int M, int K, int mode, hipStream_t stream);
 bool gemv_dq_fits(int qtype, int M, int K);
 bool gemv_dq_fits_f16(int M, int K);
 hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
@@ -337,6 +340,31 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
     if (rc != IFX_OK) return rc;
   }
   return IFX_OK;
+}
+
+int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, void *const *Y,
+                              const int *N, const void *residual, int residual_dtype,
+                              const uint16_t *norm_weight, float eps, int out_dtype, int mode,
+                              int M, int K, void *stream) {
+  if (!W || !Y || !N || !residual || !norm_weight) return IFX_NULL_POINTER;
+  if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
+  if (mode != IFX_STORE && mode != IFX_ACCUM) return IFX_BAD_GEOMETRY;
+  if (residual_dtype != IFX_OUT_F32 && residual_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (!(eps >= 0.0f)) return IFX_BAD_GEOMETRY;
+  for (int i = 0; i < count; ++i) {
+    // geometry and 32-bit range checks of the GEMV (the activation pointer
+    // stands in for the Q8_1 tensor the kernel builds in LDS)
+    const int rc = check_gemm_args(quant_type, W[i], residual, Y[i], out_dtype, mode, nullptr, M,
+                                   N[i], K);
+    if (rc != IFX_OK) return rc;
+  }
+  if (quant_type != IFX_TYPE_Q4_K || M > 2 ||
+      static_cast<int64_t>(M) * (K / 32) * ifx::kQ8_1Bytes > 65536)
+    return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_gemv_rmsnorm(count, W, Y, N, residual,
+                                            residual_dtype == IFX_OUT_F16, norm_weight, eps,
+                                            out_dtype == IFX_OUT_F16, M, K, mode,
+                                            static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,

@@ -162,21 +162,51 @@ __device__ __forceinline__ void q4k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, cons
 // of load r is at voff[r] + soff[r] (one of the two is zero: per-lane rows
 // in half-wave mode, wave-uniform rows otherwise).
 // ---------------------------------------------------------------------------
-template <int MC, int R>
-__device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
-                                         const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
-                                         int s, float (&acc)[R][MC]) {
-  const int b = s >> 2, w = s & 3;
+// Activation sources of the slice functions: the caller's Q8_1 tensor
+// (buffer loads) or a copy of it in LDS (the GEMV with a fused RMSNorm).
+struct AGlobal {
+  rsrc_t r;
+  uint32_t a_row;
+  template <typename T>
+  __device__ __forceinline__ T get(uint32_t o, int c) const {
+    return bload<T>(r, o, c * a_row);
+  }
+};
+struct ALds {
+  const uint8_t *p;
+  uint32_t a_row;
+  template <typename T>
+  __device__ __forceinline__ T get(uint32_t o, int c) const {
+    return ldg<T>(p + c * a_row + o);
+  }
+};
+
+// The weight bytes of wide slice s of R rows, loaded before their use.
+template <int R>
+struct Q4Wide {
   u32x4 hdr[R], q0[R], q1[R];
+};
+
+template <int R>
+__device__ __forceinline__ void q4k_wide_load(Q4Wide<R> &wt, const rsrc_t Wr,
+                                              const uint32_t (&voff)[R], const uint32_t (&soff)[R],
+                                              int s) {
+  const int b = s >> 2, w = s & 3;
   const uint32_t wo = b * kQ4KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     // header: every lane loads its super-block's 16-byte header itself (no
     // branch, no broadcast; the four lanes' requests hit the same line)
-    hdr[r] = wload<u32x4>(Wr, voff[r] + wo, soff[r]);
-    q0[r] = wload<u32x4>(Wr, voff[r] + wo + 16 + 32 * w, soff[r]);
-    q1[r] = wload<u32x4>(Wr, voff[r] + wo + 32 + 32 * w, soff[r]);
+    wt.hdr[r] = wload<u32x4>(Wr, voff[r] + wo, soff[r]);
+    wt.q0[r] = wload<u32x4>(Wr, voff[r] + wo + 16 + 32 * w, soff[r]);
+    wt.q1[r] = wload<u32x4>(Wr, voff[r] + wo + 32 + 32 * w, soff[r]);
   }
+}
+
+template <int MC, int R, typename AS>
+__device__ __forceinline__ void q4k_wide_compute(const Q4Wide<R> &wt, const AS &as, int mvalid,
+                                                 int s, float (&acc)[R][MC]) {
+  const int b = s >> 2, w = s & 3;
   // activations: Q8_1 blocks 8b + 2w and 8b + 2w + 1, all 32 codes of each
   i32x4 xa0[MC], xa1[MC], xb0[MC], xb1[MC];
   float da[MC], db[MC], sa[MC], sbv[MC];
@@ -184,12 +214,12 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
   for (int c = 0; c < MC; ++c) {
     if (c == 0 || c < mvalid) {  // mvalid >= 1
       const uint32_t ao = (b * 8 + 2 * w) * kQ8_1Bytes;
-      const uint32_t dsa = bload<uint32_t>(Ar, ao, c * a_row);
-      const uint32_t dsb = bload<uint32_t>(Ar, ao + kQ8_1Bytes, c * a_row);
-      xa0[c] = bload<i32x4>(Ar, ao + 4, c * a_row);
-      xa1[c] = bload<i32x4>(Ar, ao + 20, c * a_row);
-      xb0[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 4, c * a_row);
-      xb1[c] = bload<i32x4>(Ar, ao + kQ8_1Bytes + 20, c * a_row);
+      const uint32_t dsa = as.template get<uint32_t>(ao, c);
+      const uint32_t dsb = as.template get<uint32_t>(ao + kQ8_1Bytes, c);
+      xa0[c] = as.template get<i32x4>(ao + 4, c);
+      xa1[c] = as.template get<i32x4>(ao + 20, c);
+      xb0[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 4, c);
+      xb1[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 20, c);
       da[c] = h2f(dsa & 0xFFFFu);
       db[c] = h2f(dsb & 0xFFFFu);
       sa[c] = h2f(dsa >> 16);
@@ -204,10 +234,10 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
   const uint32_t top_mask = w < 2 ? 0u : 0x30303030u;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float d = h2f(hdr[r].x & 0xFFFFu);
-    const float dmin = h2f(hdr[r].x >> 16);
+    const float d = h2f(wt.hdr[r].x & 0xFFFFu);
+    const float dmin = h2f(wt.hdr[r].x >> 16);
     // 6-bit scale/min unpack (quant_common.cuh:83-94), branch-free
-    const uint32_t S0 = hdr[r].y, S1 = hdr[r].z, S2 = hdr[r].w;
+    const uint32_t S0 = wt.hdr[r].y, S1 = wt.hdr[r].z, S2 = wt.hdr[r].w;
     const uint32_t scw = ((w < 2 ? S0 : S2) & lo_mask) | ((S0 >> 2) & top_mask);
     const uint32_t mw = ((w < 2 ? S1 : (S2 >> 4)) & lo_mask) | ((S1 >> 2) & top_mask);
     const uint32_t sct = scw >> shift, mt = mw >> shift;
@@ -215,7 +245,8 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
     const float dsc1 = d * static_cast<float>((sct >> 8) & 0xFFu);
     const float dm0 = dmin * static_cast<float>(mt & 0xFFu);
     const float dm1 = dmin * static_cast<float>((mt >> 8) & 0xFFu);
-    const uint32_t qv[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+    const uint32_t qv[8] = {wt.q0[r].x, wt.q0[r].y, wt.q0[r].z, wt.q0[r].w,
+                            wt.q1[r].x, wt.q1[r].y, wt.q1[r].z, wt.q1[r].w};
 #pragma unroll
     for (int c = 0; c < MC; ++c) {
       const int xa[8] = {xa0[c].x, xa0[c].y, xa0[c].z, xa0[c].w, xa1[c].x, xa1[c].y, xa1[c].z, xa1[c].w};
@@ -230,6 +261,15 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
                    (dm0 * sa[c] + dm1 * sbv[c]);
     }
   }
+}
+
+template <int MC, int R>
+__device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
+                                         const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
+                                         int s, float (&acc)[R][MC]) {
+  Q4Wide<R> wt;
+  q4k_wide_load<R>(wt, Wr, voff, soff, s);
+  q4k_wide_compute<MC, R>(wt, AGlobal{Ar, a_row}, mvalid, s, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -469,6 +509,11 @@ struct GemvArgs {
   int nseg;
   const uint8_t *A;
   int M, K, mode;
+  // fused RMSNorm producer (NORM != 0): residual x [M][K] (fp32 or fp16)
+  // and norm weight [K] fp16; A is not read
+  const void *x;
+  const uint16_t *norm_w;
+  float eps;
 };
 
 // Q4_K with MC <= 2 and Q6_K with MC = 1 use the wide (64-value) slices
@@ -478,9 +523,18 @@ struct GemvArgs {
 template <int QT, int MC>
 constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) || (QT == kTypeQ6_K && MC == 1);
 
-template <int QT, int MC, int R, int G, int P, bool F16OUT, int H>
+// NORM = 1 / 2: the activations are produced in the kernel from an fp32 /
+// fp16 residual (RMSNorm then Q8_1, the standalone producer's exact
+// arithmetic) into LDS.  For K <= 2048 the residual and norm-weight loads
+// are issued first, then the first slice's weight loads, and the norm is
+// computed while the weights stream in (a wave's loads complete in order);
+// larger K runs the norm before the first weight load.  Wide Q4_K slices and
+// 256-thread workgroups only.
+template <int QT, int MC, int R, int G, int P, bool F16OUT, int H, int NORM = 0>
 __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   static_assert(H == 1 || (G == 1 && kWide<QT, MC>), "half-wave mode: wide slices, one wave per row group");
+  static_assert(NORM == 0 || (QT == kTypeQ4_K && kWide<QT, MC> && 64 * G * P == 256),
+                "fused RMSNorm: wide Q4_K slices, 256 threads");
   constexpr int V = R * MC;  // partial sums per lane; a power of two <= 64
   constexpr int LPR = 64 / H;                       // lanes per row set
   constexpr int SV = kWide<QT, MC> ? 64 : 32;       // values per slice
@@ -529,6 +583,43 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
     for (int c = 0; c < MC; ++c) acc[r][c] = 0.0f;
 
   const int nslice = K / SV;
+  if constexpr (NORM != 0) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // [MC][K/32] Q8_1
+    __shared__ float npart[4 * MC];
+    const int s0 = gw * LPR + lt;
+    Q4Wide<R> wt;
+    if (K <= 2048) {
+      // residual and norm weight first, then the first slice's weights:
+      // the norm's inputs arrive without waiting for the weight stream
+      f32x4 xr[MC][2];
+      u32x2 wr[MC][2];
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid)
+          rmsnorm_row_load<NORM == 2, 2>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w,
+                                         K, threadIdx.x, xr[c], wr[c]);
+      if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid)
+          rmsnorm_row_finish<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
+                                threadIdx.x);
+    } else {
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid)
+          rmsnorm_quantize_row<NORM == 2>(args.x, static_cast<int64_t>(col0 + c) * K,
+                                          args.norm_w, a_lds + c * a_row, K, args.eps,
+                                          npart + 4 * c, threadIdx.x);
+      if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
+    }
+    __syncthreads();
+    const ALds as{a_lds, a_row};
+    for (int s = s0; s < nslice; s += LPR * G) {
+      if (s != s0) q4k_wide_load<R>(wt, Wr, voff, soff, s);
+      q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);
+    }
+  } else
   for (int s = gw * LPR + lt; s < nslice; s += LPR * G) {
     if constexpr (kWide<QT, MC> && QT == kTypeQ4_K)
       q4k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
@@ -667,6 +758,49 @@ static void launch_r(const GemvArgs &args, bool f16, hipStream_t s) {
   case 2: launch_g<QT, MC, 2>(args, f16, s); break;
   case 8: launch_g<QT, MC, 8>(args, f16, s); break;
   default: launch_g<QT, MC, 4>(args, f16, s); break;
+  }
+}
+
+// The GEMV with the fused RMSNorm producer (Q4_K wide slices, M <= 2):
+// the row geometry of launch_g, 256-thread workgroups (3 waves per row
+// group become 4), the Q8_1 activations of the MC columns in dynamic LDS.
+template <int MC, int R, int G, int H, int NORM>
+static void launch_norm_t(GemvArgs args, bool f16, hipStream_t s) {
+  constexpr int P = 4 / G;
+  int blocks = 0;
+  for (int i = 0; i < args.nseg; ++i) {
+    args.seg[i].blk_begin = blocks;
+    const int groups = (args.seg[i].N + H * R - 1) / (H * R);
+    blocks += (groups + P - 1) / P;
+  }
+  const dim3 grid(blocks, (args.M + MC - 1) / MC);
+  const size_t shm = static_cast<size_t>(MC) * (args.K >> 5) * kQ8_1Bytes;
+  if (f16)
+    hipLaunchKernelGGL((k_gemv<kTypeQ4_K, MC, R, G, P, true, H, NORM>), grid, dim3(256), shm, s,
+                       args);
+  else
+    hipLaunchKernelGGL((k_gemv<kTypeQ4_K, MC, R, G, P, false, H, NORM>), grid, dim3(256), shm, s,
+                       args);
+}
+
+template <int MC, int R, int NORM>
+static void launch_norm_g(const GemvArgs &args, bool f16, hipStream_t s) {
+  const int nslice = args.K / 64;
+  const int g = (nslice + 63) / 64;
+  if (nslice <= 32) launch_norm_t<MC, R, 1, 2, NORM>(args, f16, s);
+  else if (g <= 1) launch_norm_t<MC, R, 1, 1, NORM>(args, f16, s);
+  else if (g == 2) launch_norm_t<MC, R, 2, 1, NORM>(args, f16, s);
+  else launch_norm_t<MC, R, 4, 1, NORM>(args, f16, s);
+}
+
+template <int MC, int NORM>
+static void launch_norm_r(const GemvArgs &args, bool f16, hipStream_t s) {
+  int n_total = 0;
+  for (int i = 0; i < args.nseg; ++i) n_total += args.seg[i].N;
+  switch (rows_per_wave<kTypeQ4_K, MC>(n_total, args.K)) {
+  case 1: launch_norm_g<MC, 1, NORM>(args, f16, s); break;
+  case 2: launch_norm_g<MC, 2, NORM>(args, f16, s); break;
+  default: launch_norm_g<MC, 4, NORM>(args, f16, s); break;
   }
 }
 
@@ -838,6 +972,34 @@ hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void 
   args.K = K;
   args.mode = mode;
   return launch_args(qtype, args, f16, stream);
+}
+
+// The grouped Q4_K GEMV for 1 <= M <= 2 with the RMSNorm + Q8_1 producer
+// fused in (checked by the caller: Q4_K, K % 256 == 0, M <= 2, the Q8_1
+// copy of M rows fits 64 KiB of LDS).
+hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, const int *N,
+                               const void *x, bool x_f16, const uint16_t *norm_w, float eps,
+                               bool f16, int M, int K, int mode, hipStream_t stream) {
+  if (count < 1 || count > kMaxSeg || M < 1 || M > 2) return hipErrorInvalidValue;
+  GemvArgs args{};
+  for (int i = 0; i < count; ++i)
+    args.seg[i] = GemvSeg{static_cast<const uint8_t *>(W[i]), Y[i], nullptr, N[i], 0};
+  args.nseg = count;
+  args.A = nullptr;
+  args.M = M;
+  args.K = K;
+  args.mode = mode;
+  args.x = x;
+  args.norm_w = norm_w;
+  args.eps = eps;
+  if (M == 1) {
+    if (x_f16) launch_norm_r<1, 2>(args, f16, stream);
+    else launch_norm_r<1, 1>(args, f16, stream);
+  } else {
+    if (x_f16) launch_norm_r<2, 2>(args, f16, stream);
+    else launch_norm_r<2, 1>(args, f16, stream);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace ifx

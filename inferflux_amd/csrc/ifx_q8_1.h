@@ -7,7 +7,8 @@
 //   amax = max|x|; d = amax / 127; inv = amax > 0 ? 127 / amax : 0;
 //   q = clamp(rint(x * inv), -128, 127); ds = {f16(d), f16(d * sum(q))}
 // in IEEE fp32 with no contraction, so codes and scales are bit-exact with
-// the CPU restatement.  The 8 lanes of a block must be active together.
+// the CPU restatement.  The 8 lanes of a block must be active together and
+// aligned to 8 within the wave (the DPP moves stay inside each 8 lanes).
 #pragma once
 
 #include "ifx_common.h"
@@ -17,10 +18,14 @@ namespace ifx {
 #pragma clang fp contract(off)
 __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, float x3,
                                                 uint8_t *blk, int l) {
+  // max and the integer sum over the 8 lanes of the block: DPP moves
+  // (VALU, no LDS round trip): swap pairs, swap pairs of pairs, then the
+  // mirror within each 8 lanes pairs every lane with one of the other quad.
+  // Both reductions are exact, so the order does not matter.
   float amax = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, dppf<0xB1>(amax));   // quad_perm [1,0,3,2]
+  amax = fmaxf(amax, dppf<0x4E>(amax));   // quad_perm [2,3,0,1]
+  amax = fmaxf(amax, dppf<0x141>(amax));  // row_half_mirror
   const float d = amax / 127.0f;
   const float inv = (amax > 0.0f) ? 127.0f / amax : 0.0f;
   int q0 = static_cast<int>(__builtin_rintf(x0 * inv));
@@ -32,9 +37,9 @@ __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, fl
   q2 = min(127, max(-128, q2));
   q3 = min(127, max(-128, q3));
   int sum = q0 + q1 + q2 + q3;
-  sum += __shfl_xor(sum, 4);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 1);
+  sum += static_cast<int>(dpp<0xB1>(0u, static_cast<uint32_t>(sum)));
+  sum += static_cast<int>(dpp<0x4E>(0u, static_cast<uint32_t>(sum)));
+  sum += static_cast<int>(dpp<0x141>(0u, static_cast<uint32_t>(sum)));
   const uint32_t packed = (static_cast<uint32_t>(q0) & 0xFFu) |
                           ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
                           ((static_cast<uint32_t>(q2) & 0xFFu) << 16) |
@@ -44,6 +49,106 @@ __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, fl
     const float s = materialize_f32(d * static_cast<float>(sum));  // fp32 first, then fp16
     const uint32_t ds = f2h_bits(d) | (f2h_bits(s) << 16);
     *reinterpret_cast<uint32_t *>(blk) = ds;
+  }
+}
+
+// fp32 or fp16 (IEEE binary16 bits) activations, four at element i.
+template <bool F16>
+__device__ __forceinline__ f32x4 load4(const void *p, int64_t i) {
+  if constexpr (F16) {
+    const u32x2 v = ldg<u32x2>(static_cast<const uint16_t *>(p) + i);
+    return f32x4{h2f(v.x & 0xFFFFu), h2f(v.x >> 16), h2f(v.y & 0xFFFFu), h2f(v.y >> 16)};
+  } else {
+    return ldg<f32x4>(static_cast<const float *>(p) + i);
+  }
+}
+
+// RMSNorm then Q8_1 of one row (fused_dequant_gemv.cuh:736-904) by a
+// workgroup of exactly 256 threads: rms = 1 / sqrt(sum(x^2) / K + eps),
+// y = (x * rms) * w, quantized per 32 values into orow (global or LDS).
+// The sum of squares is reduced with DPP within each wave and through
+// part[0..3] (LDS) across the four waves; then 8 lanes per Q8_1 block apply
+// the norm and quantize (a second, cache-resident read of the row, which
+// keeps the register count of the GEMV that fuses this low).  Every caller
+// (the standalone producer and that GEMV) runs this same code, so their
+// codes are identical.  The square root and division are correctly
+// rounded (the reference evaluates rsqrtf).
+template <bool F16>
+__device__ __forceinline__ void rmsnorm_quantize_row(const void *x, int64_t base,
+                                                     const uint16_t *w, uint8_t *orow, int K,
+                                                     float eps, float *part, int tid) {
+  float ss = 0.0f;
+  for (int i = 4 * tid; i < K; i += 4 * 256) {
+    const f32x4 v = load4<F16>(x, base + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum_to63(ss);
+  if ((tid & 63) == 63) part[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
+  const int nblk = K >> 5;
+  // whole 8-lane groups per block: every shuffle partner is live
+  for (int b = tid >> 3; b < nblk; b += 32) {
+    const int l = tid & 7;
+    const int i = b * 32 + l * 4;
+    const f32x4 v = load4<F16>(x, base + i);
+    const u32x2 wv = ldg<u32x2>(w + i);
+    const float y0 = materialize_f32(v.x * rms) * h2f(wv.x & 0xFFFFu);
+    const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
+    const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
+    const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
+    quantize4_store(y0, y1, y2, y3, orow + b * kQ8_1Bytes, l);
+  }
+}
+
+// The same row in two phases for a kernel that must issue other loads in
+// between (a wave's loads complete in issue order, so data loaded after a
+// long weight prefetch waits for all of it): rmsnorm_row_load reads the
+// thread's elements 4t + 1024j (j < NIT) of x and of the norm weight into
+// registers, rmsnorm_row_finish computes exactly what rmsnorm_quantize_row
+// computes from them.  Requires K <= 1024 * NIT.
+template <bool F16, int NIT>
+__device__ __forceinline__ void rmsnorm_row_load(const void *x, int64_t base, const uint16_t *w,
+                                                 int K, int tid, f32x4 (&xr)[NIT],
+                                                 u32x2 (&wr)[NIT]) {
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int i = 4 * tid + 1024 * j;
+    if (i < K) {
+      xr[j] = load4<F16>(x, base + i);
+      wr[j] = ldg<u32x2>(w + i);
+    }
+  }
+}
+
+template <int NIT>
+__device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
+                                                   uint8_t *orow, int K, float eps, float *part,
+                                                   int tid) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NIT; ++j)
+    if (4 * tid + 1024 * j < K)
+      ss += xr[j].x * xr[j].x + xr[j].y * xr[j].y + xr[j].z * xr[j].z + xr[j].w * xr[j].w;
+  ss = wave_sum_to63(ss);
+  if ((tid & 63) == 63) part[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
+  const int l = tid & 7;
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int i = 4 * tid + 1024 * j;  // = 32 * block + 4 * l
+    if (i < K) {
+      const f32x4 v = xr[j];
+      const u32x2 wv = wr[j];
+      const float y0 = materialize_f32(v.x * rms) * h2f(wv.x & 0xFFFFu);
+      const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
+      const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
+      const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
+      quantize4_store(y0, y1, y2, y3, orow + (i >> 5) * kQ8_1Bytes, l);
+    }
   }
 }
 

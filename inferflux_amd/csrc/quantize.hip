@@ -48,16 +48,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1_f16(const uint16_t *__res
 // decode layer), with the quantizer above as their last step.
 // ---------------------------------------------------------------------------
 
-template <bool F16>
-__device__ __forceinline__ f32x4 load4(const void *p, int64_t i) {
-  if constexpr (F16) {
-    const u32x2 v = ldg<u32x2>(static_cast<const uint16_t *>(p) + i);
-    return f32x4{h2f(v.x & 0xFFFFu), h2f(v.x >> 16), h2f(v.y & 0xFFFFu), h2f(v.y >> 16)};
-  } else {
-    return ldg<f32x4>(static_cast<const float *>(p) + i);
-  }
-}
-
 // RMSNorm then Q8_1 (fused_dequant_gemv.cuh:736-904): per row,
 // rms = 1 / sqrt(sum(x^2) / K + eps), y = (x * rms) * w, quantized per 32.
 // One workgroup of 256 threads per row: the sum of squares is reduced with
@@ -72,32 +62,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantize_q8_1(const void *__res
                                                                float eps) {
   __shared__ float part[4];
   const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int64_t base = row * K;
-  float ss = 0.0f;
-  for (int i = 4 * tid; i < K; i += 4 * 256) {
-    const f32x4 v = load4<F16>(x, base + i);
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-  }
-  ss = wave_sum_to63(ss);
-  if ((tid & 63) == 63) part[tid >> 6] = ss;
-  __syncthreads();
-  const float total = (part[0] + part[1]) + (part[2] + part[3]);
-  const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
-  const int nblk = K >> 5;
-  uint8_t *orow = out + row * nblk * kQ8_1Bytes;
-  // whole 8-lane groups per block: every shuffle partner is live
-  for (int b = tid >> 3; b < nblk; b += 32) {
-    const int l = tid & 7;
-    const int i = b * 32 + l * 4;
-    const f32x4 v = load4<F16>(x, base + i);
-    const u32x2 wv = ldg<u32x2>(w + i);
-    const float y0 = materialize_f32(v.x * rms) * h2f(wv.x & 0xFFFFu);
-    const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
-    const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
-    const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
-    quantize4_store(y0, y1, y2, y3, orow + b * kQ8_1Bytes, l);
-  }
+  rmsnorm_quantize_row<F16>(x, row * K, w, out + row * (K >> 5) * kQ8_1Bytes, K, eps, part,
+                            threadIdx.x);
 }
 
 // SiLU(gate) * up then Q8_1 (fused_dequant_gemv.cuh:657-734):

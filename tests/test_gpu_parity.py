@@ -416,6 +416,60 @@ def test_grouped_parity(orc, dev, qtype, M, K, Ns):
         check_rows(down(y) - 0.25, orc.gemv_exact(qtype, w, a, M, n, K))
 
 
+# ---------------------- RMSNorm + Q8_1 producer fused into the grouped GEMV
+@pytest.mark.parametrize("M,K,Ns,x_dtype", [
+    (1, 2048, (300, 173), "f32"),        # half-wave rows (K <= 2048)
+    (2, 2048, (64, 129, 200), "f16"),
+    (1, 5120, (256, 77), "f32"),         # two waves per row group
+    (2, 3072, (100,), "f32"),            # one wave per row group
+    (1, 9216, (64, 40), "f16"),          # three waves per row group, run as four
+    (2, 14336, (33,), "f32"),            # M * K/32 * 36 = 32 KB of LDS
+])
+def test_gemv_rmsnorm_fused_parity(orc, dev, M, K, Ns, x_dtype):
+    """Same activations as the standalone producer (bitwise: one shared
+    code path), so the fused launch equals producer + grouped GEMV bit for
+    bit where the slice distribution over waves is the same, and is within
+    the GEMV bar of the fp64 oracle on those activations everywhere."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemv+rmsnorm M={M} K={K} N={Ns} {x_dtype}")
+    rng = np.random.default_rng(M * K + 1)
+    x = (rng.standard_normal((M, K)) * 4).astype(np.float32)
+    if x_dtype == "f16":
+        x = x.astype(np.float16)
+    nw = rng.uniform(0.2, 2.0, K).astype(np.float16)
+    ws = [synth.blocks(Q4_K, n, K, seed=13 * i + n) for i, n in enumerate(Ns)]
+    W = [up(w, dev) for w in ws]
+    X, NW = up(x, dev), up(nw, dev)
+    outs = ops.qgemv_grouped_rmsnorm(Q4_K, W, X, NW, M, list(Ns), K, eps=1e-6)
+    A = ops.rmsnorm_quantize_q8_1(X, NW, eps=1e-6)
+    ref = ops.qgemv_grouped(Q4_K, W, A, M, list(Ns), K)
+    a = down(A)
+    same_order = (K // 64 + 63) // 64 != 3  # the 3-wave row group runs as 4 waves
+    for w, n, y, yr in zip(ws, Ns, outs, ref):
+        y, yr = down(y), down(yr)
+        if same_order:
+            assert np.array_equal(y, yr), "fused launch differs from producer + GEMV"
+        check_rows(y, orc.gemv_exact(Q4_K, w, a, M, n, K))
+    # accumulate mode
+    base = [torch.full_like(y, 0.5) for y in outs]
+    ops.qgemv_grouped_rmsnorm(Q4_K, W, X, NW, M, list(Ns), K, eps=1e-6, outs=base, mode=ops.ACCUM)
+    for w, n, y in zip(ws, Ns, base):
+        check_rows(down(y) - 0.5, orc.gemv_exact(Q4_K, w, a, M, n, K))
+
+
+def test_gemv_rmsnorm_fused_not_handled(dev):
+    import torch
+    from inferflux_amd import ops
+    W = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    x = torch.zeros((4, 2048), dtype=torch.float32, device=dev)
+    nw = torch.ones(2048, dtype=torch.float16, device=dev)
+    for qtype, M in ((Q6_K, 1), (Q4_K, 3)):  # other types, M > 2: two calls instead
+        with pytest.raises(ops.NotHandled) as e:
+            ops.qgemv_grouped_rmsnorm(qtype, [W], x, nw, M, [8], 2048)
+        assert e.value.status == 2
+
+
 def test_host_cpp_gpu():
     """The C++ FusedQuantGemm mirror on the GPU (tests/cpp, vs the oracle)."""
     import subprocess
