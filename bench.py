@@ -135,8 +135,9 @@ def main():
         (synthetic: attention itself is not on this path) -> O accumulated
         into the residual -> RMSNorm+Q8_1 -> grouped gate/up -> SiLU*up+Q8_1
         -> down accumulated into the residual.  4 producers + 4 GEMVs.
-        fused: the two RMSNorm+Q8_1 producers run inside the QKV and gate/up
-        launches (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 2 + 4 launches."""
+        fused: the two RMSNorm+Q8_1 producers and the Q8_1 quantize of the
+        attention output run inside the QKV, gate/up and O launches
+        (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 1 producer + 4 GEMVs."""
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
         rng = np.random.default_rng(seed)
         resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
@@ -165,12 +166,13 @@ def main():
                                   [layer[p][1] for p in projs], K,
                                   outs=[Y[p] for p in projs], mode=mode)
 
-        def gemv_norm(lname, r, nw):
-            _, projs, _, _ = launches[lname]
+        def gemv_norm(lname, r, x, nw):
+            _, projs, _, accum = launches[lname]
             qt, _, K, _ = layer[projs[0]]
-            ops.qgemv_grouped_rmsnorm(qt, [layer[p][3][r] for p in projs], resid, nw, M,
+            ops.qgemv_grouped_rmsnorm(qt, [layer[p][3][r] for p in projs], x, nw, M,
                                       [layer[p][1] for p in projs], K,
-                                      outs=[Y[p] for p in projs])
+                                      outs=[Y[p] for p in projs],
+                                      mode=ops.ACCUM if accum else ops.STORE)
 
         def run(i, which=None):
             r = i % R
@@ -178,15 +180,15 @@ def main():
             if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["attn"], out=A["attn_in"])
             if which is None or which == "qkv":
-                gemv_norm("qkv", r, norm_w["attn"]) if fused else gemv("qkv", r)
-            if prod:
+                gemv_norm("qkv", r, resid, norm_w["attn"]) if fused else gemv("qkv", r)
+            if prod and not fused:
                 ops.quantize_q8_1(attn, out=A["attn_out"])
             if which is None or which == "o":
-                gemv("o", r)
+                gemv_norm("o", r, attn, None) if fused else gemv("o", r)
             if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["ffn"], out=A["ffn_in"])
             if which is None or which == "gate_up":
-                gemv_norm("gate_up", r, norm_w["ffn"]) if fused else gemv("gate_up", r)
+                gemv_norm("gate_up", r, resid, norm_w["ffn"]) if fused else gemv("gate_up", r)
             if prod:
                 ops.silu_mul_quantize_q8_1(Y["gate"], Y["up"], out=A["ffn_act"])
             if which is None or which == "down":
@@ -236,12 +238,12 @@ def main():
             per_m[M]["fused_norm"] = {
                 "us_per_layer": round(us_fused, 2),
                 "kernel_us": {n: round(time_loop(lambda i, n=n: runf(i, n), steps, args.warmup), 2)
-                              for n in ("qkv", "gate_up", "producers")},
+                              for n in ("qkv", "o", "gate_up", "producers")},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_fused * 1e-6), 1),
             }
         if M == 1:
             ms_per_step = min(us_layer, us_fused) / 1e3
-            step_is = ("layer with the RMSNorm producers fused into the QKV and gate/up launches"
+            step_is = ("layer with the Q8_1 producers of QKV, O and gate/up fused into them"
                        if us_fused < us_layer else "layer as the reference launches it")
             headline = q4_bytes / q4_us / 1e3
     extras["qwen3b_layer"] = per_m

@@ -107,10 +107,12 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
 /* RMSNorm + Q8_1 fused into the grouped GEMV that consumes it: for each
  * batch row m, a[m] = Q8_1((x[m] * rms(x[m])) * norm_weight), exactly as
  * ifx_rmsnorm_quantize_q8_1 computes it, then y_i (op)= W_i . a as
- * ifx_qgemv_grouped.  Every workgroup rebuilds a in LDS after issuing its
+ * ifx_qgemv_grouped.  norm_weight == NULL: a[m] = Q8_1(x[m]), exactly as
+ * ifx_q8_1_quantize_f32/_f16 compute it (the reference's QuantizeRowQ8_1
+ * + GemvQ8_1AccumF32 of the O projection, transformer_forward.cu:609-726).  Every workgroup rebuilds a in LDS after issuing its
  * first weight loads, so the producer's launch and the Q8_1 round trip
  * through memory disappear from the decode layer.  residual [M][K] fp32 or
- * fp16 (residual_dtype: ifx_out_dtype), norm_weight fp16 [K].  Handles
+ * fp16 (residual_dtype: ifx_out_dtype), norm_weight fp16 [K] or NULL.  Handles
  * Q4_K, 1 <= M <= 2, M * K/32 * 36 <= 65536; other shapes return
  * IFX_BAD_GEOMETRY (not handled: use the two calls).  mode: IFX_STORE or
  * IFX_ACCUM.  No reference counterpart as one call: it fuses

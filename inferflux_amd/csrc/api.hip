@@ -346,7 +346,7 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
                               const int *N, const void *residual, int residual_dtype,
                               const uint16_t *norm_weight, float eps, int out_dtype, int mode,
                               int M, int K, void *stream) {
-  if (!W || !Y || !N || !residual || !norm_weight) return IFX_NULL_POINTER;
+  if (!W || !Y || !N || !residual) return IFX_NULL_POINTER;
   if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
   if (mode != IFX_STORE && mode != IFX_ACCUM) return IFX_BAD_GEOMETRY;
   if (residual_dtype != IFX_OUT_F32 && residual_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;

@@ -525,7 +525,8 @@ constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) || (QT == kTypeQ6_K && MC ==
 
 // NORM = 1 / 2: the activations are produced in the kernel from an fp32 /
 // fp16 residual (RMSNorm then Q8_1, the standalone producer's exact
-// arithmetic) into LDS.  For K <= 2048 the residual and norm-weight loads
+// arithmetic) into LDS; NORM = 3 / 4: from fp32 / fp16 activations by the
+// plain Q8_1 quantizer (the standalone quantizer's blocks, bit for bit).  For K <= 2048 the residual and norm-weight loads
 // are issued first, then the first slice's weight loads, and the norm is
 // computed while the weights stream in (a wave's loads complete in order);
 // larger K runs the norm before the first weight load.  Wide Q4_K slices and
@@ -584,33 +585,44 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
 
   const int nslice = K / SV;
   if constexpr (NORM != 0) {
+    constexpr bool kXF16 = NORM == 2 || NORM == 4, kRms = NORM <= 2;
     extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // [MC][K/32] Q8_1
     __shared__ float npart[4 * MC];
     const int s0 = gw * LPR + lt;
     Q4Wide<R> wt;
     if (K <= 2048) {
-      // residual and norm weight first, then the first slice's weights:
-      // the norm's inputs arrive without waiting for the weight stream
+      // activations (and norm weight) first, then the first slice's
+      // weights: the producer's inputs arrive without waiting for the
+      // weight stream
       f32x4 xr[MC][2];
       u32x2 wr[MC][2];
 #pragma unroll
       for (int c = 0; c < MC; ++c)
         if (c < mvalid)
-          rmsnorm_row_load<NORM == 2, 2>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w,
-                                         K, threadIdx.x, xr[c], wr[c]);
+          rmsnorm_row_load<kXF16, 2>(args.x, static_cast<int64_t>(col0 + c) * K,
+                                     kRms ? args.norm_w : nullptr, K, threadIdx.x, xr[c], wr[c]);
       if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
 #pragma unroll
       for (int c = 0; c < MC; ++c)
-        if (c < mvalid)
-          rmsnorm_row_finish<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
-                                threadIdx.x);
+        if (c < mvalid) {
+          if constexpr (kRms)
+            rmsnorm_row_finish<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
+                                  threadIdx.x);
+          else
+            quantize_row_finish<2>(xr[c], a_lds + c * a_row, K, threadIdx.x);
+        }
     } else {
 #pragma unroll
       for (int c = 0; c < MC; ++c)
-        if (c < mvalid)
-          rmsnorm_quantize_row<NORM == 2>(args.x, static_cast<int64_t>(col0 + c) * K,
-                                          args.norm_w, a_lds + c * a_row, K, args.eps,
-                                          npart + 4 * c, threadIdx.x);
+        if (c < mvalid) {
+          if constexpr (kRms)
+            rmsnorm_quantize_row<kXF16>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w,
+                                        a_lds + c * a_row, K, args.eps, npart + 4 * c,
+                                        threadIdx.x);
+          else
+            quantize_row<kXF16>(args.x, static_cast<int64_t>(col0 + c) * K, a_lds + c * a_row, K,
+                                threadIdx.x);
+        }
       if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
     }
     __syncthreads();
@@ -980,6 +992,7 @@ hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void 
 hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, const int *N,
                                const void *x, bool x_f16, const uint16_t *norm_w, float eps,
                                bool f16, int M, int K, int mode, hipStream_t stream) {
+  // norm_w == nullptr: the plain quantizer
   if (count < 1 || count > kMaxSeg || M < 1 || M > 2) return hipErrorInvalidValue;
   GemvArgs args{};
   for (int i = 0; i < count; ++i)
@@ -992,12 +1005,21 @@ hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, 
   args.x = x;
   args.norm_w = norm_w;
   args.eps = eps;
+  const int kind = (norm_w ? 1 : 3) + (x_f16 ? 1 : 0);
   if (M == 1) {
-    if (x_f16) launch_norm_r<1, 2>(args, f16, stream);
-    else launch_norm_r<1, 1>(args, f16, stream);
+    switch (kind) {
+    case 1: launch_norm_r<1, 1>(args, f16, stream); break;
+    case 2: launch_norm_r<1, 2>(args, f16, stream); break;
+    case 3: launch_norm_r<1, 3>(args, f16, stream); break;
+    default: launch_norm_r<1, 4>(args, f16, stream); break;
+    }
   } else {
-    if (x_f16) launch_norm_r<2, 2>(args, f16, stream);
-    else launch_norm_r<2, 1>(args, f16, stream);
+    switch (kind) {
+    case 1: launch_norm_r<2, 1>(args, f16, stream); break;
+    case 2: launch_norm_r<2, 2>(args, f16, stream); break;
+    case 3: launch_norm_r<2, 3>(args, f16, stream); break;
+    default: launch_norm_r<2, 4>(args, f16, stream); break;
+    }
   }
   return hipGetLastError();
 }

@@ -117,7 +117,7 @@ __device__ __forceinline__ void rmsnorm_row_load(const void *x, int64_t base, co
     const int i = 4 * tid + 1024 * j;
     if (i < K) {
       xr[j] = load4<F16>(x, base + i);
-      wr[j] = ldg<u32x2>(w + i);
+      if (w) wr[j] = ldg<u32x2>(w + i);  // w == nullptr: plain quantize, no norm weight
     }
   }
 }
@@ -149,6 +149,30 @@ __device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const
       const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
       quantize4_store(y0, y1, y2, y3, orow + (i >> 5) * kQ8_1Bytes, l);
     }
+  }
+}
+
+// Plain Q8_1 of one row (no norm) in the same element-to-thread mapping:
+// thread t quantizes elements 4t + 1024j as one of the 8 lanes of their
+// block, which is exactly what the standalone quantizer computes per block.
+template <int NIT>
+__device__ __forceinline__ void quantize_row_finish(const f32x4 (&xr)[NIT], uint8_t *orow, int K,
+                                                    int tid) {
+  const int l = tid & 7;
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int i = 4 * tid + 1024 * j;
+    if (i < K) quantize4_store(xr[j].x, xr[j].y, xr[j].z, xr[j].w, orow + (i >> 5) * kQ8_1Bytes, l);
+  }
+}
+
+template <bool F16>
+__device__ __forceinline__ void quantize_row(const void *x, int64_t base, uint8_t *orow, int K,
+                                             int tid) {
+  const int l = tid & 7;
+  for (int i = 4 * tid; i < K; i += 1024) {
+    const f32x4 v = load4<F16>(x, base + i);
+    quantize4_store(v.x, v.y, v.z, v.w, orow + (i >> 5) * kQ8_1Bytes, l);
   }
 }
 

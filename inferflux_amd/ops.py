@@ -180,14 +180,15 @@ def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mo
 def qgemv_grouped_rmsnorm(qtype, Ws, x, norm_weight, M, Ns, K, eps=1e-6, outs=None,
                           out_dtype=torch.float32, mode=STORE, stream=None):
     """RMSNorm + Q8_1 of the residual x [M, K] (fp32/fp16) fused into the
-    grouped GEMV over Ws (Q4_K, M <= 2).  Returns the list of outputs."""
+    grouped GEMV over Ws (Q4_K, M <= 2); norm_weight None: the plain Q8_1
+    quantizer instead.  Returns the list of outputs."""
     import ctypes
     count = len(Ws)
     if outs is None:
         outs = [torch.empty((M, N), dtype=out_dtype, device=Ws[0].device) for N in Ns]
     od = OUT_F16 if outs[0].dtype == torch.float16 else OUT_F32
     xd = OUT_F16 if x.dtype == torch.float16 else OUT_F32
-    if x.numel() < M * K or norm_weight.numel() < K:
+    if x.numel() < M * K or (norm_weight is not None and norm_weight.numel() < K):
         raise ValueError("x or norm_weight is smaller than the shape")
     for W, N, Y in zip(Ws, Ns, outs):
         if W.numel() < weight_bytes(qtype, N, K) or Y.numel() < M * N:
@@ -195,9 +196,9 @@ def qgemv_grouped_rmsnorm(qtype, Ws, x, norm_weight, M, Ns, K, eps=1e-6, outs=No
     wp = (ctypes.c_void_p * count)(*[_dev(w, "W") for w in Ws])
     yp = (ctypes.c_void_p * count)(*[_dev(y, "out") for y in outs])
     npp = (ctypes.c_int * count)(*Ns)
+    nwp = _dev(norm_weight, "norm_weight") if norm_weight is not None else None
     rc = _lib.load().ifx_qgemv_grouped_rmsnorm(qtype, count, wp, yp, npp, _dev(x, "x"), xd,
-                                               _dev(norm_weight, "norm_weight"), eps, od, mode,
-                                               M, K, _stream(stream))
+                                               nwp, eps, od, mode, M, K, _stream(stream))
     _check(rc, "ifx_qgemv_grouped_rmsnorm")
     return outs
 

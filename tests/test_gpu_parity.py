@@ -458,6 +458,30 @@ def test_gemv_rmsnorm_fused_parity(orc, dev, M, K, Ns, x_dtype):
         check_rows(down(y) - 0.5, orc.gemv_exact(Q4_K, w, a, M, n, K))
 
 
+@pytest.mark.parametrize("M,K,N,x_dtype", [(1, 2048, 2048, "f32"), (2, 2048, 300, "f16"),
+                                           (1, 5120, 129, "f32"), (2, 4096, 64, "f16")])
+def test_gemv_quantize_fused_parity(orc, dev, M, K, N, x_dtype):
+    """norm_weight None: the plain quantizer fused in; bitwise equal to
+    ifx_q8_1_quantize + the GEMV (same blocks, same kernel geometry)."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemv+quantize M={M} K={K} N={N} {x_dtype}")
+    x = synth.activations(M, K, seed=K + M, outlier_frac=0.01)
+    if x_dtype == "f16":
+        x = x.astype(np.float16)
+    w = synth.blocks(Q4_K, N, K, seed=N + 5)
+    W, X = up(w, dev), up(x, dev)
+    base = torch.full((M, N), 0.25, device=dev)
+    y = ops.qgemv_grouped_rmsnorm(Q4_K, [W], X, None, M, [N], K, outs=[base.clone()],
+                                  mode=ops.ACCUM)[0]
+    A = ops.quantize_q8_1(X)
+    yr = ops.qgemv_grouped(Q4_K, [W], A, M, [N], K, outs=[base.clone()], mode=ops.ACCUM)[0]
+    assert np.array_equal(down(y), down(yr))
+    a = down(A)
+    assert np.array_equal(a, orc.quantize_q8_1(x.astype(np.float32)))
+    check_rows(down(y) - 0.25, orc.gemv_exact(Q4_K, w, a, M, N, K))
+
+
 def test_gemv_rmsnorm_fused_not_handled(dev):
     import torch
     from inferflux_amd import ops
