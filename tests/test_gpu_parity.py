@@ -185,6 +185,8 @@ def test_epilogues(orc, dev, qtype, M):
     (Q6_K, 8, 8195, 256),    # one super-block per row
     (Q6_K, 5, 96, 8192),     # long K, few rows: split over workgroups (atomics)
     (Q4_K, 8, 33, 11008),
+    (Q6_K, 3, 200, 11008),   # long K at M = 3 / 4 (the down projection)
+    (Q6_K, 4, 64, 8192),
 ])
 def test_slot_epilogues(orc, dev, qtype, M, N, K):
     """Store, accumulate and bias modes of the slot-packed MFMA GEMV, with
