@@ -52,8 +52,9 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1_f16(const uint16_t *__res
 // rms = 1 / sqrt(sum(x^2) / K + eps), y = (x * rms) * w, quantized per 32.
 // One workgroup of 256 threads per row: the sum of squares is reduced with
 // DPP within each wave and through LDS across the four waves; then 8 lanes
-// per Q8_1 block apply the norm and quantize (L2-resident second read of
-// the row).  The reference evaluates rsqrtf (an approximation); here the
+// per Q8_1 block apply the norm and quantize (for K <= 2048 from registers
+// loaded with the norm weight in one round trip, else an L2-resident second
+// read of the row).  The reference evaluates rsqrtf (an approximation); here the
 // square root and division are correctly rounded.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_rmsnorm_quantize_q8_1(const void *__restrict__ x,
@@ -62,8 +63,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantize_q8_1(const void *__res
                                                                float eps) {
   __shared__ float part[4];
   const int64_t row = blockIdx.x;
-  rmsnorm_quantize_row<F16>(x, row * K, w, out + row * (K >> 5) * kQ8_1Bytes, K, eps, part,
-                            threadIdx.x);
+  uint8_t *orow = out + row * (K >> 5) * kQ8_1Bytes;
+  if (K <= 2048) {
+    // one round trip to memory: the row and the norm weight are loaded
+    // together into registers (the same arithmetic as the two-pass form)
+    f32x4 xr[2];
+    u32x2 wr[2];
+    rmsnorm_row_load<F16, 2>(x, row * K, w, K, threadIdx.x, xr, wr);
+    rmsnorm_row_finish<2>(xr, wr, orow, K, eps, part, threadIdx.x);
+  } else {
+    rmsnorm_quantize_row<F16>(x, row * K, w, orow, K, eps, part, threadIdx.x);
+  }
 }
 
 // SiLU(gate) * up then Q8_1 (fused_dequant_gemv.cuh:657-734):
