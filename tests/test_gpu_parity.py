@@ -426,6 +426,8 @@ def test_grouped_parity(orc, dev, qtype, M, K, Ns):
     (2, 3072, (100,), "f32"),            # one wave per row group
     (1, 9216, (64, 40), "f16"),          # three waves per row group, run as four
     (2, 14336, (33,), "f32"),            # M * K/32 * 36 = 32 KB of LDS
+    (1, 1280, (64,), "f32"),             # K not a multiple of 1024 (partial second pass)
+    (2, 256, (40, 8, 17), "f16"),        # one super-block, three projections
 ])
 def test_gemv_rmsnorm_fused_parity(orc, dev, M, K, Ns, x_dtype):
     """Same activations as the standalone producer (bitwise: one shared
@@ -482,6 +484,23 @@ def test_gemv_quantize_fused_parity(orc, dev, M, K, N, x_dtype):
     a = down(A)
     assert np.array_equal(a, orc.quantize_q8_1(x.astype(np.float32)))
     check_rows(down(y) - 0.25, orc.gemv_exact(Q4_K, w, a, M, N, K))
+
+
+def test_gemv_rmsnorm_fused_f16_out(orc, dev):
+    """fp16 outputs of the fused launch: equal to producer + GEMV with fp16 out."""
+    import torch
+    from inferflux_amd import ops, synth
+    M, K, Ns = 2, 2048, [96, 200]
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float16)
+    ws = [up(synth.blocks(Q4_K, n, K, seed=n), dev) for n in Ns]
+    X, NW = up(x, dev), up(nw, dev)
+    y = ops.qgemv_grouped_rmsnorm(Q4_K, ws, X, NW, M, Ns, K, eps=1e-5, out_dtype=torch.float16)
+    A = ops.rmsnorm_quantize_q8_1(X, NW, eps=1e-5)
+    yr = ops.qgemv_grouped(Q4_K, ws, A, M, Ns, K, out_dtype=torch.float16)
+    for a, b in zip(y, yr):
+        assert np.array_equal(down(a), down(b))
 
 
 def test_gemv_rmsnorm_fused_not_handled(dev):
