@@ -156,9 +156,6 @@ __device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint
 template <int QT>
 __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int item) {
   const int row = item >> 1, part = item & 1;
-#ifdef IFX_F16_EXPT_NOACT
-  if (false)
-#endif
   {  // activations: 32 values of block `part` at slots 32*part ..
     const h2 d = splat(h2f(r.ads & 0xFFFFu));
     uint32_t o[16];
@@ -170,14 +167,6 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
   }
   _Float16 *wrow = &sm.w[buf][row * kPitch];
-#ifdef IFX_F16_EXPT_NOW
-  if (true) {
-    u32x4 *d = reinterpret_cast<u32x4 *>(wrow + 16 * part);
-    d[0] = r.w0; d[1] = r.w1; d[4] = r.w0; d[5] = r.w1;
-    return;
-  }
-#endif
-  const h2 zero = {static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
   if constexpr (QT == kTypeQ4_K) {
     // 16 qs bytes: values 16*part .. +15 of sub-blocks 2p (low nibbles) and
     // 2p + 1 (high nibbles); get_scale_min_k4 (quant_common.cuh:83-94).
@@ -210,7 +199,6 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     dlo[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
     dhi[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
     dhi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
-    (void)zero;
   } else if constexpr (QT == kTypeQ6_K) {
     // ql (w0) and qh (w1) bytes of values 16*part .. +15 of sub-blocks hf
     // (low nibbles, qh bits 2hf..2hf+1) and hf + 2 (high nibbles, qh bits
@@ -220,7 +208,7 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     const float s_lo = static_cast<float>(static_cast<int8_t>((scb >> (8 * part)) & 0xFFu));
     const float s_hi = static_cast<float>(static_cast<int8_t>((scb >> (16 + 8 * part)) & 0xFFu));
     const h2 dl = splat(d * s_lo), dh = splat(d * s_hi);
-    const h2 b = splat(-1056.0f);
+    const h2 b = splat(-1056.0f), zero = splat(0.0f);
     const uint32_t ql[4] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w};
     const uint32_t qh[4] = {r.w1.x, r.w1.y, r.w1.z, r.w1.w};
     uint32_t lo[8], hi[8];
@@ -249,7 +237,6 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     u32x4 *dst = reinterpret_cast<u32x4 *>(wrow + 32 * part);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
-    (void)zero;
   }
 }
 
