@@ -362,6 +362,23 @@ def main():
                               "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
             res["f16"]["frac_f16_peak"] = round(res["f16"]["TOPS"] / F16_PEAK_TFLOPS, 4)
             res["default"] = "f16" if ops.kernel_family(qt, M, N, K) == 4 else "int8"
+            # The reference's prefill path recreated on this GPU: dequantize W
+            # to an FP16 scratch copy (ifx_dequantize, the counterpart of
+            # dequantize_q4_k / q6_k) and multiply it with the vendor
+            # library's FP16 GEMM (torch.matmul -> hipBLASLt / rocBLAS,
+            # fp32 accumulate) by fp16 activations.
+            w16 = torch.empty((N, K), dtype=torch.float16, device=dev)
+            x16 = x.to(torch.float16)
+            y16 = torch.empty((M, N), dtype=torch.float16, device=dev)
+            deq_us = time_loop(lambda i: ops.dequantize(qt, w, N, K, out=w16),
+                               max(10, args.steps // 10), 3)
+            gemm_us = time_loop(lambda i: torch.matmul(x16, w16.t(), out=y16),
+                                max(10, args.steps // 10), 3)
+            res["reference_path"] = {
+                "dequant_fp16_us": round(deq_us, 1), "library_fp16_gemm_us": round(gemm_us, 1),
+                "total_us": round(deq_us + gemm_us, 1),
+                "fused_f16_speedup": round((deq_us + gemm_us) / res["f16"]["us"], 2)}
+            del w16, x16, y16
             c5[f"{name}_{ops.TYPE_NAMES[qt]}_{N}x{K}"] = res
             del w
             torch.cuda.empty_cache()

@@ -427,6 +427,8 @@ int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int6
   if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (out_dtype != IFX_OUT_F32 && out_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   if (n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return IFX_BAD_GEOMETRY;
+  if (n_rows * static_cast<int64_t>((K / ifx_block_elems(quant_type)) * ifx_block_bytes(quant_type)) >= (int64_t{1} << 32))
+    return IFX_BAD_GEOMETRY;  // buffer offsets are 32-bit
   return status_of(ifx::launch_dequantize(quant_type, W, out, out_dtype == IFX_OUT_F16,
                                           n_rows * static_cast<int64_t>(K),
                                           static_cast<hipStream_t>(stream)));

@@ -11,123 +11,141 @@
 // emits.  It serves verification and callers that want a dense copy; the
 // GEMV/GEMM kernels never materialise W.
 //
-// Mapping: one lane per 32-element run (a Q4_K/Q5_K sub-block, a Q6_K
-// (group, sub) run, a Q8_0 block, a Q8_K 32-value slice); each lane writes
-// 32 contiguous outputs.
+// Mapping: one lane per 8 consecutive outputs, so a wave's stores are
+// contiguous (16 bytes per lane for fp16, 32 for fp32); the lane reads the
+// 8 codes it needs with one buffer load (unaligned offsets are served) and
+// its block's header.
 #include "ifx_common.h"
 
 namespace ifx {
 
-// 6-bit scale and min of sub-block sb (quant_common.cuh:83-94).
-__device__ __forceinline__ void scale_min_k4(const uint8_t *s, int sb, int &sc, int &m) {
+// 6-bit scale and min of sub-block sb from the 12 scale bytes as three
+// little-endian words (quant_common.cuh:83-94).
+__device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int sb,
+                                             int &sc, int &m) {
+  const uint32_t by[12] = {s0 & 0xFF, (s0 >> 8) & 0xFF, (s0 >> 16) & 0xFF, s0 >> 24,
+                           s1 & 0xFF, (s1 >> 8) & 0xFF, (s1 >> 16) & 0xFF, s1 >> 24,
+                           s2 & 0xFF, (s2 >> 8) & 0xFF, (s2 >> 16) & 0xFF, s2 >> 24};
   if (sb < 4) {
-    sc = s[sb] & 63;
-    m = s[sb + 4] & 63;
+    sc = static_cast<int>(by[sb] & 63);
+    m = static_cast<int>(by[sb + 4] & 63);
   } else {
-    sc = (s[sb + 4] & 0xF) | ((s[sb - 4] >> 6) << 4);
-    m = (s[sb + 4] >> 4) | ((s[sb] >> 6) << 4);
+    sc = static_cast<int>((by[sb + 4] & 0xF) | ((by[sb - 4] >> 6) << 4));
+    m = static_cast<int>((by[sb + 4] >> 4) | ((by[sb] >> 6) << 4));
   }
 }
 
+__device__ __forceinline__ int byte_of(u32x2 v, int i) {
+  return static_cast<int>(((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFFu);
+}
+
+// t = index of the 8-output group; element i = 8t .. 8t+7 of the tensor,
+// all in one 32-value run of one block.
 template <int QT, bool F16>
-__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W,
-                                                 void *__restrict__ out, int64_t nruns) {
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W, uint32_t w_bytes,
+                                                 void *__restrict__ out, int64_t ngroups) {
+  const rsrc_t Wr = make_rsrc(W, w_bytes);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= nruns) return;
-  float w[32];
-  if constexpr (QT == kTypeQ4_K) {
-    const int64_t blk = t >> 3;
-    const int sb = static_cast<int>(t & 7);
-    const uint8_t *b = W + blk * kQ4KBytes;
-    const float d = h2f(ldg<uint16_t>(b));
-    const float dmin = h2f(ldg<uint16_t>(b + 2));
+  if (t >= ngroups) return;
+  float w[8];
+  if constexpr (QT == kTypeQ4_K || QT == kTypeQ5_K) {
+    constexpr int kB = QT == kTypeQ4_K ? kQ4KBytes : kQ5KBytes;
+    const uint32_t blk = static_cast<uint32_t>(t >> 5);
+    const int i = static_cast<int>(t & 31) * 8;  // element within the super-block
+    const int sb = i >> 5, e = i & 31;
+    const uint32_t o = blk * kB;
+    const u32x4 hdr = bload<u32x4>(Wr, o, 0);
+    const float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
     int sc, m;
-    scale_min_k4(b + 4, sb, sc, m);
-    const uint8_t *qs = b + 16 + (sb >> 1) * 32;
+    scale_min_k4(hdr.y, hdr.z, hdr.w, sb, sc, m);
+    const uint32_t qs_off = (QT == kTypeQ4_K ? 16 : 48) + (sb >> 1) * 32 + e;
+    const u32x2 qv = bload<u32x2>(Wr, o + qs_off, 0);
+    u32x2 hv = {0, 0};
+    if constexpr (QT == kTypeQ5_K) hv = bload<u32x2>(Wr, o + 16 + e, 0);
     const int shift = (sb & 1) * 4;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const int q = (qs[e] >> shift) & 0xF;
-      w[e] = d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
-    }
-  } else if constexpr (QT == kTypeQ5_K) {
-    const int64_t blk = t >> 3;
-    const int sb = static_cast<int>(t & 7);
-    const uint8_t *b = W + blk * kQ5KBytes;
-    const float d = h2f(ldg<uint16_t>(b));
-    const float dmin = h2f(ldg<uint16_t>(b + 2));
-    int sc, m;
-    scale_min_k4(b + 4, sb, sc, m);
-    const uint8_t *qh = b + 16;
-    const uint8_t *qs = b + 48 + (sb >> 1) * 32;
-    const int shift = (sb & 1) * 4;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const int q = ((qs[e] >> shift) & 0xF) | (((qh[e] >> sb) & 1) << 4);
-      w[e] = d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
+    for (int k = 0; k < 8; ++k) {
+      int q = (byte_of(qv, k) >> shift) & 0xF;
+      if constexpr (QT == kTypeQ5_K) q |= ((byte_of(hv, k) >> sb) & 1) << 4;
+      w[k] = d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
     }
   } else if constexpr (QT == kTypeQ8_K) {
-    const int64_t blk = t >> 3;
-    const uint8_t *b = W + blk * kQ8KBytes;
-    const float d = ldg<float>(b);
-    const int8_t *qs = reinterpret_cast<const int8_t *>(b + 4) + (t & 7) * 32;
+    const uint32_t blk = static_cast<uint32_t>(t >> 5);
+    const int i = static_cast<int>(t & 31) * 8;
+    const uint32_t o = blk * kQ8KBytes;
+    const float d = __builtin_bit_cast(float, bload<uint32_t>(Wr, o, 0));
+    const u32x2 qv = bload<u32x2>(Wr, o + 4 + i, 0);
 #pragma unroll
-    for (int e = 0; e < 32; ++e) w[e] = d * static_cast<float>(qs[e]);
+    for (int k = 0; k < 8; ++k)
+      w[k] = d * static_cast<float>(static_cast<int8_t>(byte_of(qv, k)));
   } else if constexpr (QT == kTypeQ6_K) {
-    const int64_t blk = t >> 3;
-    const int run = static_cast<int>(t & 7);
-    const int g = run >> 2, sub = run & 3;
-    const uint8_t *b = W + blk * kQ6KBytes;
-    const float d = h2f(ldg<uint16_t>(b + 208));
-    const uint8_t *ql = b + g * 64 + (sub & 1) * 32;
-    const uint8_t *qh = b + 128 + g * 32;
-    const int8_t *sc = reinterpret_cast<const int8_t *>(b + 192) + g * 8 + sub * 2;
+    const uint32_t blk = static_cast<uint32_t>(t >> 5);
+    const int i = static_cast<int>(t & 31) * 8;
+    const int g = i >> 7, sub = (i >> 5) & 3, e = i & 31;
+    const uint32_t o = blk * kQ6KBytes;
+    const float d = h2f(bload<uint16_t>(Wr, o + 208, 0));
+    const u32x2 lv = bload<u32x2>(Wr, o + g * 64 + (sub & 1) * 32 + e, 0);
+    const u32x2 hv = bload<u32x2>(Wr, o + 128 + g * 32 + e, 0);
+    const uint32_t sc2 = bload<uint16_t>(Wr, o + 192 + g * 8 + sub * 2, 0);  // even offset
+    const float sc = static_cast<float>(static_cast<int8_t>(sc2 >> (8 * (e >> 4))));
     const int lshift = (sub >= 2) ? 4 : 0;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const int q = (((ql[e] >> lshift) & 0xF) | (((qh[e] >> (2 * sub)) & 3) << 4)) - 32;
-      w[e] = d * static_cast<float>(sc[e >> 4]) * static_cast<float>(q);
+    for (int k = 0; k < 8; ++k) {
+      const int q = (((byte_of(lv, k) >> lshift) & 0xF) | (((byte_of(hv, k) >> (2 * sub)) & 3) << 4)) - 32;
+      w[k] = d * sc * static_cast<float>(q);
     }
   } else {
-    const uint8_t *b = W + t * kQ8_0Bytes;
-    const float d = h2f(ldg<uint16_t>(b));
-    const int8_t *qs = reinterpret_cast<const int8_t *>(b + 2);
+    const uint32_t blk = static_cast<uint32_t>(t >> 2);
+    const int e = static_cast<int>(t & 3) * 8;
+    const uint32_t o = blk * kQ8_0Bytes;
+    const float d = h2f(bload<uint16_t>(Wr, o, 0));
+    const u32x2 qv = bload<u32x2>(Wr, o + 2 + e, 0);
 #pragma unroll
-    for (int e = 0; e < 32; ++e) w[e] = d * static_cast<float>(qs[e]);
+    for (int k = 0; k < 8; ++k) w[k] = d * static_cast<float>(static_cast<int8_t>(byte_of(qv, k)));
   }
   if constexpr (F16) {
-    uint32_t *o = reinterpret_cast<uint32_t *>(static_cast<uint16_t *>(out) + t * 32);
+    // fp32 value first, then fp16 (no fused multiply-convert)
+    uint32_t h[4];
 #pragma unroll
-    for (int e = 0; e < 32; e += 2)  // fp32 value first, then fp16 (no fused multiply-convert)
-      o[e >> 1] = f2h_bits(materialize_f32(w[e])) | (f2h_bits(materialize_f32(w[e + 1])) << 16);
+    for (int k = 0; k < 4; ++k)
+      h[k] = f2h_bits(materialize_f32(w[2 * k])) | (f2h_bits(materialize_f32(w[2 * k + 1])) << 16);
+    *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(out) + t * 8) = u32x4{h[0], h[1], h[2], h[3]};
   } else {
-    f32x4 *o = reinterpret_cast<f32x4 *>(static_cast<float *>(out) + t * 32);
-#pragma unroll
-    for (int e = 0; e < 32; e += 4) o[e >> 2] = f32x4{w[e], w[e + 1], w[e + 2], w[e + 3]};
+    f32x4 *o = reinterpret_cast<f32x4 *>(static_cast<float *>(out) + t * 8);
+    o[0] = f32x4{w[0], w[1], w[2], w[3]};
+    o[1] = f32x4{w[4], w[5], w[6], w[7]};
   }
 }
 
 template <int QT>
-static void launch_dq(const uint8_t *W, void *out, bool f16, int64_t nruns, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((nruns + 255) / 256));
+static void launch_dq(const uint8_t *W, uint32_t w_bytes, void *out, bool f16, int64_t ngroups,
+                      hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((ngroups + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL((k_dequant<QT, true>), grid, dim3(256), 0, s, W, out, nruns);
+    hipLaunchKernelGGL((k_dequant<QT, true>), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
   else
-    hipLaunchKernelGGL((k_dequant<QT, false>), grid, dim3(256), 0, s, W, out, nruns);
+    hipLaunchKernelGGL((k_dequant<QT, false>), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
 }
 
-// n_elems must be a multiple of the block size of qtype (checked by caller).
+// n_elems must be a multiple of the block size of qtype and the tensor
+// below 4 GiB (checked by the caller).
 hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int64_t n_elems,
                              hipStream_t stream) {
-  const int64_t nruns = n_elems / 32;
-  if (nruns == 0) return hipSuccess;
+  const int64_t ngroups = n_elems / 8;
+  if (ngroups == 0) return hipSuccess;
   const uint8_t *w = static_cast<const uint8_t *>(W);
+  const int64_t bytes = qtype == kTypeQ8_0 ? n_elems / 32 * kQ8_0Bytes
+                        : n_elems / 256 * (qtype == kTypeQ4_K   ? kQ4KBytes
+                                           : qtype == kTypeQ5_K ? kQ5KBytes
+                                           : qtype == kTypeQ6_K ? kQ6KBytes
+                                                                : kQ8KBytes);
+  const uint32_t wb = static_cast<uint32_t>(bytes);
   switch (qtype) {
-  case kTypeQ4_K: launch_dq<kTypeQ4_K>(w, out, f16, nruns, stream); break;
-  case kTypeQ6_K: launch_dq<kTypeQ6_K>(w, out, f16, nruns, stream); break;
-  case kTypeQ8_0: launch_dq<kTypeQ8_0>(w, out, f16, nruns, stream); break;
-  case kTypeQ5_K: launch_dq<kTypeQ5_K>(w, out, f16, nruns, stream); break;
-  case kTypeQ8_K: launch_dq<kTypeQ8_K>(w, out, f16, nruns, stream); break;
+  case kTypeQ4_K: launch_dq<kTypeQ4_K>(w, wb, out, f16, ngroups, stream); break;
+  case kTypeQ6_K: launch_dq<kTypeQ6_K>(w, wb, out, f16, ngroups, stream); break;
+  case kTypeQ8_0: launch_dq<kTypeQ8_0>(w, wb, out, f16, ngroups, stream); break;
+  case kTypeQ5_K: launch_dq<kTypeQ5_K>(w, wb, out, f16, ngroups, stream); break;
+  case kTypeQ8_K: launch_dq<kTypeQ8_K>(w, wb, out, f16, ngroups, stream); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -228,11 +228,12 @@ def qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, h_out=None, q8_1_out=None, wan
     return h_out, q8_1_out
 
 
-def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None):
-    out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)
-    od = OUT_F16 if out_dtype == torch.float16 else OUT_F32
-    if W.numel() < weight_bytes(qtype, n_rows, K):
-        raise ValueError("W is smaller than n_rows x K blocks")
+def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None, out=None):
+    if out is None:
+        out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, n_rows, K) or out.numel() < n_rows * K:
+        raise ValueError("W or out is smaller than n_rows x K")
     rc = _lib.load().ifx_dequantize(qtype, _dev(W, "W"), _dev(out, "out"), od, n_rows, K,
                                     _stream(stream))
     _check(rc, "ifx_dequantize")

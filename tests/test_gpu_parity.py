@@ -94,7 +94,7 @@ def test_quantize_reference_kat(dev):
 
 # ---------------------------------------------------------------- dequant
 @pytest.mark.parametrize("qtype,n,K", [(Q4_K, 33, 2048), (Q6_K, 17, 11008), (Q8_0, 9, 2080),
-                                      (Q5_K, 9, 2048), (Q8_K, 7, 1024)])
+                                      (Q5_K, 9, 2048), (Q8_K, 7, 1024), (Q8_0, 3, 96)])
 def test_dequant_bit_exact(orc, dev, qtype, n, K):
     import torch
     from inferflux_amd import ops, synth
