@@ -137,7 +137,10 @@ def main():
         -> down accumulated into the residual.  4 producers + 4 GEMVs.
         fused: the two RMSNorm+Q8_1 producers and the Q8_1 quantize of the
         attention output run inside the QKV, gate/up and O launches
-        (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 1 producer + 4 GEMVs."""
+        (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 1 producer + 4 GEMVs.
+        fused == "swiglu": in addition gate/up computes SiLU(gate)*up and
+        writes its Q8_1 blocks for down itself
+        (ifx_qgemv_gate_up_silu_rmsnorm): 4 launches, no producer."""
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
         rng = np.random.default_rng(seed)
         resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
@@ -188,8 +191,16 @@ def main():
             if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["ffn"], out=A["ffn_in"])
             if which is None or which == "gate_up":
-                gemv_norm("gate_up", r, resid, norm_w["ffn"]) if fused else gemv("gate_up", r)
-            if prod:
+                if fused == "swiglu":
+                    qt, N, K, _ = layer["gate"]
+                    ops.qgemv_gate_up_silu_rmsnorm(qt, layer["gate"][3][r], layer["up"][3][r],
+                                                   resid, norm_w["ffn"], M, N, K, want_h=False,
+                                                   q8_1_out=A["ffn_act"])
+                elif fused:
+                    gemv_norm("gate_up", r, resid, norm_w["ffn"])
+                else:
+                    gemv("gate_up", r)
+            if prod and fused != "swiglu":
                 ops.silu_mul_quantize_q8_1(Y["gate"], Y["up"], out=A["ffn_act"])
             if which is None or which == "down":
                 gemv("down", r)
@@ -241,10 +252,24 @@ def main():
                               for n in ("qkv", "o", "gate_up", "producers")},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_fused * 1e-6), 1),
             }
+            # and with SiLU*up + Q8_1 fused into gate/up as well
+            runs = decode_layer_runner(layer3b, M, seed=10 + M, fused="swiglu")
+            us_swiglu = time_loop(runs, steps, args.warmup)
+            per_m[M]["fused_norm_swiglu"] = {
+                "us_per_layer": round(us_swiglu, 2),
+                "kernel_us": {n: round(time_loop(lambda i, n=n: runs(i, n), steps, args.warmup), 2)
+                              for n in ("qkv", "o", "gate_up", "down")},
+                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_swiglu * 1e-6), 1),
+            }
         if M == 1:
-            ms_per_step = min(us_layer, us_fused) / 1e3
-            step_is = ("layer with the Q8_1 producers of QKV, O and gate/up fused into them"
-                       if us_fused < us_layer else "layer as the reference launches it")
+            variants = {
+                "layer as the reference launches it": us_layer,
+                "layer with the Q8_1 producers of QKV, O and gate/up fused into them": us_fused,
+                "layer with the Q8_1 producers fused and SiLU*up + Q8_1 in the gate/up epilogue":
+                    us_swiglu,
+            }
+            step_is = min(variants, key=variants.get)
+            ms_per_step = variants[step_is] / 1e3
             headline = q4_bytes / q4_us / 1e3
     extras["qwen3b_layer"] = per_m
 

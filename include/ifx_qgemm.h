@@ -139,6 +139,20 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
                            const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
                            int N, int K, void *stream);
 
+/* ifx_qgemv_gate_up_silu with the RMSNorm + Q8_1 producer of its input
+ * fused in: a = Q8_1(rmsnorm(residual[m]) * norm_weight) (the arithmetic
+ * of ifx_rmsnorm_quantize_q8_1), then h and/or its Q8_1 blocks as above.
+ * Handles Q4_K, 1 <= M <= 2, N % 32 == 0 and K <= 2048; other shapes return
+ * IFX_BAD_GEOMETRY (not handled: use ifx_rmsnorm_quantize_q8_1 +
+ * ifx_qgemv_gate_up_silu).  Replaces the reference's
+ * FusedRmsNormQuantizeQ8_1 followed by FusedGateUpSiluGemvQ8_1WithEpilogue
+ * (fused_quant_gemm.h:131-150, 281-307), the FFN entry of
+ * transformer_forward.cu:2839-2870. */
+int ifx_qgemv_gate_up_silu_rmsnorm(int quant_type, const void *W_gate, const void *W_up,
+                                   const void *residual, int residual_dtype,
+                                   const uint16_t *norm_weight, float eps, void *H, int h_dtype,
+                                   void *q8_1_out, int M, int N, int K, void *stream);
+
 /* The prefill GEMM alone, for any M >= 1, fp32 accumulate: the int8 MFMA
  * GEMM below 128 rows, from 128 rows on the fp16 MFMA GEMM with in-kernel
  * dequant (see ifx_qgemm_prefill_kernel).  Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback

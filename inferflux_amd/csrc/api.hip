@@ -28,6 +28,9 @@ hipError_t launch_gemv_grouped(int qtype, int count, const void *const *W, void 
                                hipStream_t stream);
 hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const void *A, void *H,
                               bool f16h, void *Q, int M, int N, int K, hipStream_t stream);
+hipError_t launch_gemv_swiglu_rmsnorm(const void *Wg, const void *Wu, const void *x, bool x_f16,
+                                      const uint16_t *norm_w, float eps, void *H, bool f16h,
+                                      void *Q, int M, int N, int K, hipStream_t stream);
 hipError_t launch_mmvq(int qtype, int count, const void *const *W, void *const *Y,
                        const int *N, const void *bias, const void *A, bool f16, int M, int K,
                        int mode, hipStream_t stream);
@@ -386,6 +389,27 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   return status_of(ifx::launch_gemv_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
                                            h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
                                            static_cast<hipStream_t>(stream)));
+}
+
+int ifx_qgemv_gate_up_silu_rmsnorm(int quant_type, const void *W_gate, const void *W_up,
+                                   const void *residual, int residual_dtype,
+                                   const uint16_t *norm_weight, float eps, void *H, int h_dtype,
+                                   void *q8_1_out, int M, int N, int K, void *stream) {
+  if (!W_gate || !W_up || !residual || !norm_weight || (!H && !q8_1_out)) return IFX_NULL_POINTER;
+  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (residual_dtype != IFX_OUT_F32 && residual_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (!(eps >= 0.0f)) return IFX_BAD_GEOMETRY;
+  void *probe_out = H ? H : q8_1_out;
+  const int rc = check_gemm_args(quant_type, W_gate, residual, probe_out, IFX_OUT_F32, IFX_STORE,
+                                 nullptr, M, N, K);
+  if (rc != IFX_OK) return rc;
+  // the wide Q4_K kernel only: one row's slices fit half a wave
+  if (quant_type != IFX_TYPE_Q4_K || M > 2 || N % 32 != 0 || K > 2048) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_gemv_swiglu_rmsnorm(W_gate, W_up, residual,
+                                                   residual_dtype == IFX_OUT_F16, norm_weight, eps,
+                                                   H, h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
+                                                   static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,

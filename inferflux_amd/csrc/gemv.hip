@@ -921,6 +921,143 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
   }
 }
 
+// Q4_K with K <= 2048 and M <= 2: the same fusion on the wide slices of the
+// grouped GEMV.  A row's K/64 <= 32 slices take half a wave, so a wave
+// computes 4 rows (2 per half) of one tensor: waves 0-7 the 32 gate rows of
+// the block, waves 8-15 the 32 up rows (the tensor is wave-uniform).  Lanes
+// 31 and 63 put the row totals in LDS; after one barrier 8 lanes per batch
+// column form h = silu(g) * u and quantize the block.  NORM = 1 / 2: the
+// Q8_1 activations are produced in the kernel from an fp32 / fp16 residual
+// (RMSNorm then Q8_1 by the first 256 threads, the standalone producer's
+// arithmetic) into LDS, their loads issued before the weight prefetch.
+struct SwigluArgs {
+  const uint8_t *Wg, *Wu, *A;
+  const void *x;
+  const uint16_t *norm_w;
+  float eps;
+  void *H;
+  uint8_t *Q;
+  int M, N, K;
+};
+
+constexpr int kSwigluWideMaxK = 2048;
+
+template <int MC, bool F16H, int NORM>
+__global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args) {
+  constexpr int R = 2;
+  __shared__ float gu[2][MC][32];  // [gate/up][column][output]
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[NORM ? MC * (kSwigluWideMaxK / 32) * kQ8_1Bytes : 1];
+  __shared__ float npart[4 * MC];
+  const int M = args.M, N = args.N, K = args.K;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool is_up = wave >= 8;
+  const int half = lane >> 5, lt = lane & 31;
+  const int orow0 = ((wave & 7) * 2 + half) * R;  // first output of this half-wave in the block
+  const int col0 = blockIdx.y * MC;
+  const int mvalid = min(MC, M - col0);
+  const int nslice = K >> 6;
+  const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
+  const uint32_t w_row = static_cast<uint32_t>(row_bytes(kTypeQ4_K, K));
+  const rsrc_t Wr = make_rsrc(is_up ? args.Wu : args.Wg, w_row * static_cast<uint32_t>(N));
+  uint32_t voff[R], soff[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    voff[r] = static_cast<uint32_t>(blockIdx.x * 32 + orow0 + r) * w_row;
+    soff[r] = 0u;
+  }
+  float acc[R][MC];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MC; ++c) acc[r][c] = 0.0f;
+
+  Q4Wide<R> wt;
+  if constexpr (NORM != 0) {
+    constexpr bool kXF16 = NORM == 2;
+    const bool prod = threadIdx.x < 256;  // waves 0-3
+    f32x4 xr[MC][2];
+    u32x2 wr[MC][2];
+    if (prod) {
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid)
+          rmsnorm_row_load<kXF16, 2>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w, K,
+                                     threadIdx.x, xr[c], wr[c]);
+    }
+    if (lt < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, lt);
+    if (prod) {
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid) rmsnorm_row_partial<2>(xr[c], K, npart + 4 * c, threadIdx.x);
+    }
+    __syncthreads();
+    if (prod) {
+#pragma unroll
+      for (int c = 0; c < MC; ++c)
+        if (c < mvalid)
+          rmsnorm_row_apply<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
+                               threadIdx.x);
+    }
+    __syncthreads();
+    const ALds as{a_lds, a_row};
+    for (int s = lt; s < nslice; s += 32) {
+      if (s != lt) q4k_wide_load<R>(wt, Wr, voff, soff, s);
+      q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);
+    }
+  } else {
+    const AGlobal as{make_rsrc(args.A + static_cast<int64_t>(col0) * a_row, a_row * mvalid), a_row};
+    for (int s = lt; s < nslice; s += 32) {
+      q4k_wide_load<R>(wt, Wr, voff, soff, s);
+      q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < MC; ++c) {
+      const float v = halfwave_sum_to31(acc[r][c]);
+      if (lt == 31) gu[is_up][c][orow0 + r] = v;
+    }
+  __syncthreads();
+  const int c = threadIdx.x >> 3, l = threadIdx.x & 7;
+  if (c < MC && (c == 0 || c < mvalid)) {  // whole 8-lane groups (mvalid >= 1)
+    const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[0][c][4 * l]);
+    const f32x4 u4 = *reinterpret_cast<const f32x4 *>(&gu[1][c][4 * l]);
+    const f32x4 h = silu_mul4(g4, u4);
+    if (args.H) {
+      const int64_t o = static_cast<int64_t>(col0 + c) * N + blockIdx.x * 32 + 4 * l;
+      if constexpr (F16H) {
+        const u32x2 hv = {f2h_bits(h.x) | (f2h_bits(h.y) << 16), f2h_bits(h.z) | (f2h_bits(h.w) << 16)};
+        *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(args.H) + o) = hv;
+      } else {
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(args.H) + o) = h;
+      }
+    }
+    if (args.Q)
+      quantize4_store(h.x, h.y, h.z, h.w,
+                      args.Q + (static_cast<int64_t>(col0 + c) * (N >> 5) + blockIdx.x) * kQ8_1Bytes, l);
+  }
+}
+
+// One workgroup per batch column (MC = 1 at M = 2 as well): the MC = 2 kernel
+// needs 96 VGPRs, which leaves room for only one 16-wave workgroup per CU;
+// the second column's weight reads mostly hit the cache.
+template <int NORM>
+static void launch_swiglu_wide(const SwigluArgs &a, bool f16h, hipStream_t s) {
+  const dim3 grid(a.N / 32, a.M);
+  if (f16h) hipLaunchKernelGGL((k_gemv_swiglu_wide<1, true, NORM>), grid, dim3(1024), 0, s, a);
+  else hipLaunchKernelGGL((k_gemv_swiglu_wide<1, false, NORM>), grid, dim3(1024), 0, s, a);
+}
+
+static bool swiglu_wide_env() {
+  static const int v = [] {
+    const char *e = getenv("IFX_SWIGLU_WIDE");
+    return e ? atoi(e) : 1;
+  }();
+  return v != 0;
+}
+
 template <int QT, int MC>
 static void launch_swiglu_mc(const uint8_t *Wg, const uint8_t *Wu, const uint8_t *A, void *H,
                              bool f16h, uint8_t *Q, int M, int N, int K, hipStream_t s) {
@@ -944,6 +1081,11 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   const uint8_t *g = static_cast<const uint8_t *>(Wg), *u = static_cast<const uint8_t *>(Wu);
   const uint8_t *a = static_cast<const uint8_t *>(A);
   uint8_t *q = static_cast<uint8_t *>(Q);
+  if (qtype == kTypeQ4_K && K <= kSwigluWideMaxK && M <= 2 && swiglu_wide_env()) {
+    const SwigluArgs args{g, u, a, nullptr, nullptr, 0.0f, H, q, M, N, K};
+    launch_swiglu_wide<0>(args, f16h, stream);
+    return hipGetLastError();
+  }
   switch (qtype) {
   case kTypeQ4_K: launch_swiglu_t<kTypeQ4_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   case kTypeQ6_K: launch_swiglu_t<kTypeQ6_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
@@ -952,6 +1094,19 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   case kTypeQ8_K: launch_swiglu_t<kTypeQ8_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// The wide Q4_K kernel with the RMSNorm + Q8_1 producer fused in (checked by
+// the caller: Q4_K, K % 256 == 0, K <= 2048, 1 <= M <= 2, N % 32 == 0).
+hipError_t launch_gemv_swiglu_rmsnorm(const void *Wg, const void *Wu, const void *x, bool x_f16,
+                                      const uint16_t *norm_w, float eps, void *H, bool f16h,
+                                      void *Q, int M, int N, int K, hipStream_t stream) {
+  if (M < 1 || M > 2 || K > kSwigluWideMaxK || N % 32 != 0) return hipErrorInvalidValue;
+  const SwigluArgs args{static_cast<const uint8_t *>(Wg), static_cast<const uint8_t *>(Wu),
+                        nullptr, x, norm_w, eps, H, static_cast<uint8_t *>(Q), M, N, K};
+  if (x_f16) launch_swiglu_wide<2>(args, f16h, stream);
+  else launch_swiglu_wide<1>(args, f16h, stream);
   return hipGetLastError();
 }
 

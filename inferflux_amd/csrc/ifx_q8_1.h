@@ -122,10 +122,13 @@ __device__ __forceinline__ void rmsnorm_row_load(const void *x, int64_t base, co
   }
 }
 
+// rmsnorm_row_finish in two phases around a barrier that the caller
+// executes (a workgroup larger than the 256 producer threads runs the
+// barrier on every wave): rmsnorm_row_partial writes the four waves' sums of
+// squares to part[0..3], rmsnorm_row_apply reads them after the barrier.
 template <int NIT>
-__device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
-                                                   uint8_t *orow, int K, float eps, float *part,
-                                                   int tid) {
+__device__ __forceinline__ void rmsnorm_row_partial(const f32x4 (&xr)[NIT], int K, float *part,
+                                                    int tid) {
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < NIT; ++j)
@@ -133,7 +136,12 @@ __device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const
       ss += xr[j].x * xr[j].x + xr[j].y * xr[j].y + xr[j].z * xr[j].z + xr[j].w * xr[j].w;
   ss = wave_sum_to63(ss);
   if ((tid & 63) == 63) part[tid >> 6] = ss;
-  __syncthreads();
+}
+
+template <int NIT>
+__device__ __forceinline__ void rmsnorm_row_apply(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
+                                                  uint8_t *orow, int K, float eps,
+                                                  const float *part, int tid) {
   const float total = (part[0] + part[1]) + (part[2] + part[3]);
   const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
   const int l = tid & 7;
@@ -150,6 +158,24 @@ __device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const
       quantize4_store(y0, y1, y2, y3, orow + (i >> 5) * kQ8_1Bytes, l);
     }
   }
+}
+
+// 256 threads exactly.
+template <int NIT>
+__device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
+                                                   uint8_t *orow, int K, float eps, float *part,
+                                                   int tid) {
+  rmsnorm_row_partial<NIT>(xr, K, part, tid);
+  __syncthreads();
+  rmsnorm_row_apply<NIT>(xr, wr, orow, K, eps, part, tid);
+}
+
+// SiLU(g) * u of four values (the standalone producer's arithmetic).
+__device__ __forceinline__ f32x4 silu_mul4(f32x4 g, f32x4 u) {
+  f32x4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = materialize_f32(g[i] / (1.0f + expf(-g[i]))) * u[i];
+  return h;
 }
 
 // Plain Q8_1 of one row (no norm) in the same element-to-thread mapping:

@@ -89,13 +89,8 @@ __global__ __launch_bounds__(256) void k_silu_mul_quantize_q8_1(const void *__re
   if (blk >= nblocks) return;
   const f32x4 gv = load4<F16>(g, blk * 32 + l * 4);
   const f32x4 uv = load4<F16>(u, blk * 32 + l * 4);
-  float y[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float gi = gv[i];
-    y[i] = materialize_f32(gi / (1.0f + expf(-gi))) * uv[i];
-  }
-  quantize4_store(y[0], y[1], y[2], y[3], out + blk * kQ8_1Bytes, l);
+  const f32x4 y = silu_mul4(gv, uv);
+  quantize4_store(y.x, y.y, y.z, y.w, out + blk * kQ8_1Bytes, l);
 }
 
 hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t *w, void *out,

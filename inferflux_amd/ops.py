@@ -228,6 +228,36 @@ def qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, h_out=None, q8_1_out=None, wan
     return h_out, q8_1_out
 
 
+def qgemv_gate_up_silu_rmsnorm(qtype, Wg, Wu, x, norm_weight, M, N, K, eps=1e-6, h_out=None,
+                               q8_1_out=None, want_h=True, want_q8_1=True,
+                               h_dtype=torch.float32, stream=None):
+    """qgemv_gate_up_silu with the RMSNorm + Q8_1 producer of the residual
+    x [M, K] (fp32/fp16) fused in (Q4_K, M <= 2, K <= 2048); returns
+    (h or None, Q8_1 or None)."""
+    if want_h and h_out is None:
+        h_out = torch.empty((M, N), dtype=h_dtype, device=x.device)
+    if want_q8_1 and q8_1_out is None:
+        q8_1_out = torch.empty((M, N // 32 * 36), dtype=torch.uint8, device=x.device)
+    for W in (Wg, Wu):
+        if W.numel() < weight_bytes(qtype, N, K):
+            raise ValueError("W is smaller than N x K blocks")
+    if x.numel() < M * K or norm_weight.numel() < K:
+        raise ValueError("x or norm_weight is smaller than the shape")
+    if h_out is not None and (h_out.numel() < M * N or
+                              h_out.dtype not in (torch.float32, torch.float16)):
+        raise ValueError("bad h output")
+    if q8_1_out is not None and q8_1_out.numel() < M * (N // 32) * 36:
+        raise ValueError("bad Q8_1 output")
+    hd = OUT_F16 if h_out is not None and h_out.dtype == torch.float16 else OUT_F32
+    xd = OUT_F16 if x.dtype == torch.float16 else OUT_F32
+    rc = _lib.load().ifx_qgemv_gate_up_silu_rmsnorm(
+        qtype, _dev(Wg, "Wg"), _dev(Wu, "Wu"), _dev(x, "x"), xd, _dev(norm_weight, "norm_weight"),
+        eps, _dev(h_out, "h") if h_out is not None else None, hd,
+        _dev(q8_1_out, "q8_1_out") if q8_1_out is not None else None, M, N, K, _stream(stream))
+    _check(rc, "ifx_qgemv_gate_up_silu_rmsnorm")
+    return h_out, q8_1_out
+
+
 def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None, out=None):
     if out is None:
         out = torch.empty((n_rows, K), dtype=out_dtype, device=W.device)

@@ -546,7 +546,9 @@ def check_q8_1_close(a_gpu, a_ref, y_ref):
     dr, sr, qr = _q8_1_fields(a_ref)
     diff = np.abs(qg - qr)
     assert diff.max() <= 1, f"code differs by {diff.max()}"
-    assert (diff > 0).mean() <= 2e-3, f"{(diff > 0).mean():.2e} of codes differ"
+    # rare: at most 0.2 % of the codes (at least two for small tensors); the
+    # bound below checks each code against the reference value itself
+    assert (diff > 0).sum() <= max(2, 2e-3 * diff.size), f"{(diff > 0).mean():.2e} of codes differ"
     du = np.abs(dg.view(np.int16).astype(np.int32) - dr.view(np.int16).astype(np.int32))
     assert du.max() <= 1, "scale differs by more than one fp16 ulp"
     # s = f16(d * sum(q)) with the fp32 d (the block stores f16(d)): within
@@ -620,6 +622,7 @@ def test_silu_mul_quantize_exact_kat(orc, dev):
 
 # ------------------------------- fused gate/up GEMV + SiLU + Q8_1 epilogue
 @pytest.mark.parametrize("qtype,M,N,K", [(Q4_K, 1, 11008, 2048), (Q4_K, 2, 1024, 2048),
+                                         (Q4_K, 1, 64, 256), (Q4_K, 2, 96, 1280),
                                          (Q6_K, 1, 512, 1024), (Q8_0, 2, 64, 2080),
                                          (Q4_K, 1, 32, 5120), (Q5_K, 1, 1024, 2048),
                                          (Q8_K, 2, 512, 1024)])
@@ -648,6 +651,54 @@ def test_gate_up_silu_parity(orc, dev, qtype, M, N, K):
     none, q2 = ops.qgemv_gate_up_silu(qtype, up(wg, dev), up(wu, dev), up(a, dev), M, N, K,
                                       want_h=False)
     assert none is None and np.array_equal(down(q2), down(q))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 2048), (2, 1024, 2048), (1, 64, 256),
+                                   (2, 96, 1280)])
+def test_gate_up_silu_matches_two_launch_chain(orc, dev, M, N, K):
+    """The wide Q4_K kernel (K <= 2048) computes the grouped GEMV's row sums
+    in the same order and the standalone SiLU producer's arithmetic, so its
+    h and Q8_1 blocks equal those of grouped GEMV + silu_mul_quantize bit for
+    bit; the RMSNorm-fused variant equals RMSNorm producer + that kernel."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gate_up_silu chain M={M} N={N} K={K}")
+    wg = up(synth.blocks(Q4_K, N, K, seed=N + 5), dev)
+    wu = up(synth.blocks(Q4_K, N, K, seed=N + 6), dev)
+    rng = np.random.default_rng(K + M)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float16)).to(dev)
+    a = ops.rmsnorm_quantize_q8_1(x, nw)
+    g, u = ops.qgemv_grouped(Q4_K, [wg, wu], a, M, [N, N], K)
+    q_chain = down(ops.silu_mul_quantize_q8_1(g, u))
+    h, q = ops.qgemv_gate_up_silu(Q4_K, wg, wu, a, M, N, K)
+    gn, un = down(g).astype(np.float32), down(u).astype(np.float32)
+    assert np.array_equal(down(q), q_chain)
+    # device expf and the host's may differ in the last bit: h within 1e-6
+    np.testing.assert_allclose(down(h), orc.silu_mul_values(gn, un), rtol=1e-6, atol=1e-30)
+    for xx in (x, x.to(torch.float16)):
+        a2 = ops.rmsnorm_quantize_q8_1(xx, nw)
+        h2, q2 = ops.qgemv_gate_up_silu(Q4_K, wg, wu, a2, M, N, K)
+        h3, q3 = ops.qgemv_gate_up_silu_rmsnorm(Q4_K, wg, wu, xx, nw, M, N, K)
+        assert np.array_equal(down(q3), down(q2))
+        assert np.array_equal(down(h3).view(np.uint32), down(h2).view(np.uint32))
+    h16, none = ops.qgemv_gate_up_silu_rmsnorm(Q4_K, wg, wu, x, nw, M, N, K, want_q8_1=False,
+                                               h_dtype=torch.float16)
+    assert none is None
+    assert np.array_equal(down(h16), down(h).astype(np.float16))
+
+
+def test_gate_up_silu_rmsnorm_not_handled(dev):
+    """Not Q4_K, M > 2, N % 32 != 0 or K > 2048: not handled, nothing launched."""
+    import torch
+    from inferflux_amd import ops
+    w = torch.zeros(1 << 22, dtype=torch.uint8, device=dev)
+    x = torch.zeros(4 * 4096, dtype=torch.float32, device=dev)
+    nw = torch.zeros(4096, dtype=torch.float16, device=dev)
+    for qt, M, N, K in ((Q6_K, 1, 32, 256), (Q4_K, 3, 32, 256), (Q4_K, 1, 48, 256),
+                        (Q4_K, 1, 32, 2304)):
+        with pytest.raises(ops.NotHandled):
+            ops.qgemv_gate_up_silu_rmsnorm(qt, w, w, x, nw, M, N, K)
 
 
 def test_gate_up_silu_not_handled(dev):
