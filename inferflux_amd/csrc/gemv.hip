@@ -533,7 +533,7 @@ constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) || (QT == kTypeQ6_K && MC ==
 // 256-thread workgroups only.
 template <int QT, int MC, int R, int G, int P, bool F16OUT, int H, int NORM = 0>
 __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
-  static_assert(H == 1 || (G == 1 && kWide<QT, MC>), "half-wave mode: wide slices, one wave per row group");
+  static_assert(H == 1 || (G == 1 && kWide<QT, MC>), "sub-wave rows: wide slices, one wave per row group");
   static_assert(NORM == 0 || (QT == kTypeQ4_K && kWide<QT, MC> && 64 * G * P == 256),
                 "fused RMSNorm: wide Q4_K slices, 256 threads");
   constexpr int V = R * MC;  // partial sums per lane; a power of two <= 64
@@ -550,7 +550,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int gw = wave % G;   // wave within its row group
   const int grp = wave / G;  // row group within the workgroup
-  const int half = (H == 2) ? (lane >> 5) : 0;
+  const int half = (H >= 2) ? (lane / (64 / H)) : 0;  // row set of this lane
   const int lt = lane & (LPR - 1);  // lane within its row set
   const int row0 = (((bx - sg.blk_begin) * P + grp) * H + half) * R;
   const int col0 = blockIdx.y * MC;
@@ -573,8 +573,8 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   uint32_t voff[R], soff[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    voff[r] = (H == 2) ? rows[r] : 0u;
-    soff[r] = (H == 2) ? 0u : rows[r];
+    voff[r] = (H >= 2) ? rows[r] : 0u;
+    soff[r] = (H >= 2) ? 0u : rows[r];
   }
 
   float acc[R][MC];
@@ -656,7 +656,9 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int c = 0; c < MC; ++c)
-      v[r * MC + c] = (H == 2) ? halfwave_sum_to31(acc[r][c]) : wave_sum_to63(acc[r][c]);
+      v[r * MC + c] = (H == 4)   ? quarterwave_sum(acc[r][c])
+                      : (H == 2) ? halfwave_sum_to31(acc[r][c])
+                                 : wave_sum_to63(acc[r][c]);
   if constexpr (G > 1) {
     if (lane == 63) {
 #pragma unroll
@@ -712,6 +714,39 @@ static void launch_t(GemvArgs args, bool f16, hipStream_t s) {
     hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false, H>), grid, block, 0, s, args);
 }
 
+// Rows per wave section: IFX_GEMV_H in {1, 2, 4} forces full-, half- or
+// quarter-wave rows for the wide slices (tuning; read once).
+static int sub_rows_env() {
+  static const int env = [] {
+    const char *e = getenv("IFX_GEMV_H");
+    const int v = e ? atoi(e) : 0;
+    return (v == 1 || v == 2 || v == 4) ? v : 0;
+  }();
+  return env;
+}
+
+// Quarter-wave rows (16 lanes) when they leave no lane idle and the full-wave
+// launch would: e.g. K = 5120 has 80 wide slices, 5 per lane on 16 lanes
+// against 80 of 128 lanes busy on two waves.  Measured on the 14B shapes
+// (K = 5120): M = 1 QKV 6.7 -> 5.7 us, gate+up 19.3 -> 18.4 us; at M = 2
+// only launches of >= 8192 rows gain (gate+up 22.9 -> 20.9 us; QKV and O
+// lose), hence the launcher's rule.
+static bool quarter_rows(int nslice) {
+  return nslice % 16 == 0 && nslice % 64 != 0 && nslice <= 16 * 8;
+}
+
+// Lanes per row of a wide-slice launch: 64 / the result (1: full-wave rows,
+// possibly several waves per row).  The fused-RMSNorm launch uses the same
+// rule, so its row sums are formed in the same order as the plain GEMV's.
+template <int MC>
+static int wide_sub_rows(const GemvArgs &args, int nslice) {
+  if (sub_rows_env()) return sub_rows_env();
+  int n_total = 0;
+  for (int i = 0; i < args.nseg; ++i) n_total += args.seg[i].N;
+  if (nslice > 32 && quarter_rows(nslice) && (MC == 1 || n_total >= 8192)) return 4;
+  return nslice <= 32 ? 2 : 1;
+}
+
 template <int QT, int MC, int R>
 static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
   // waves per row group: enough lanes to cover the slices, at most 4; a
@@ -719,7 +754,12 @@ static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
   const int nslice = args.K / (kWide<QT, MC> ? 64 : 32);
   const int g = (nslice + 63) / 64;
   if constexpr (kWide<QT, MC>) {
-    if (nslice <= 32) {
+    const int h = wide_sub_rows<MC>(args, nslice);
+    if (h == 4) {
+      launch_t<QT, MC, R, 1, 4>(args, f16, s);
+      return;
+    }
+    if (h == 2) {
       launch_t<QT, MC, R, 1, 2>(args, f16, s);
       return;
     }
@@ -799,7 +839,9 @@ template <int MC, int R, int NORM>
 static void launch_norm_g(const GemvArgs &args, bool f16, hipStream_t s) {
   const int nslice = args.K / 64;
   const int g = (nslice + 63) / 64;
-  if (nslice <= 32) launch_norm_t<MC, R, 1, 2, NORM>(args, f16, s);
+  const int h = wide_sub_rows<MC>(args, nslice);
+  if (h == 4) launch_norm_t<MC, R, 1, 4, NORM>(args, f16, s);
+  else if (h == 2) launch_norm_t<MC, R, 1, 2, NORM>(args, f16, s);
   else if (g <= 1) launch_norm_t<MC, R, 1, 1, NORM>(args, f16, s);
   else if (g == 2) launch_norm_t<MC, R, 2, 1, NORM>(args, f16, s);
   else launch_norm_t<MC, R, 4, 1, NORM>(args, f16, s);

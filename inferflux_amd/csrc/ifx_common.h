@@ -146,6 +146,16 @@ __device__ __forceinline__ float halfwave_sum_to31(float v) {
   return v;
 }
 
+// Sums over each 16-lane row (four independent quarters): the first four
+// steps of wave_sum_to63; every lane of a row ends with its row's total.
+__device__ __forceinline__ float quarterwave_sum(float v) {
+  v += dppf<0xB1>(v);
+  v += dppf<0x4E>(v);
+  v += dppf<0x141>(v);
+  v += dppf<0x140>(v);
+  return v;
+}
+
 // Lane 8k's value in lanes 8k .. 8k+7 (row_newbcast of lanes 0 and 8 of
 // each 16-lane row into banks 0-1 and 2-3).
 __device__ __forceinline__ uint32_t bcast8(uint32_t v) {

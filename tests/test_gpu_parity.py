@@ -117,6 +117,8 @@ for qt in (Q4_K, Q6_K, Q8_0):
 CASES.append((Q8_0, 3, 50, 96))     # K not a multiple of 256
 CASES.append((Q4_K, 3, 300, 5120))  # activations-in-LDS GEMV, full-wave rows
 CASES.append((Q4_K, 4, 16400, 2048))  # activations-in-LDS GEMV, M = 4 wide launch
+CASES.append((Q4_K, 2, 8200, 5120))  # quarter-wave rows, two columns
+CASES.append((Q4_K, 1, 100, 3072))   # quarter-wave rows, 3 slices per lane
 # slot-packed MFMA GEMV (5 <= M <= 16): 8- and 16-row slots, ragged N, one
 # super-block per row, a single row
 CASES += [(Q4_K, 6, 33, 256), (Q6_K, 7, 64, 512), (Q4_K, 12, 1000, 2048),
@@ -399,6 +401,7 @@ def test_config5_prefill(orc, dev, qtype, N, K):
     (Q4_K, 16, 2048, (2048, 256, 256)),
     (Q4_K, 7, 2048, (11008, 11008)),       # slot-packed GEMV, grouped wide launch
     (Q6_K, 8, 8192, (40, 64)),             # slot-packed GEMV, grouped split
+    (Q4_K, 1, 5120, (5120, 1024, 1000)),   # quarter-wave rows, grouped, ragged
 ])
 def test_grouped_parity(orc, dev, qtype, M, K, Ns):
     import torch
