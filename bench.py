@@ -366,6 +366,20 @@ def main():
                 "kernel_us": {k: round(v, 2) for k, v in kern.items()},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN14B_LAYERS * us_layer * 1e-6), 1),
             }
+        # the Q4_K launches of the 14B layer at M = 1 and 8 (the 70 %-of-HBM
+        # target names the 3B and the 14B shapes at those M)
+        q4 = {}
+        for M in (1, 8):
+            run = decode_layer_runner(layer14, M, seed=50 + M)
+            steps = max(20, args.steps // 4)
+            for l in workloads.DECODE_LAUNCHES:
+                qt, nb = launch_bytes(layer14, l[0], M)
+                if qt != ops.Q4_K:
+                    continue
+                us = time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
+                q4[f"{l[0]}_M{M}"] = {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1),
+                                      "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        c4["q4k_launches_M1_M8"] = q4
         extras["config4_qwen14b_layer"] = c4
         del layer14
         torch.cuda.empty_cache()
