@@ -162,6 +162,25 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
                       int out_dtype, int mode, const void *bias, int M, int N, int K,
                       void *stream);
 
+/* Bytes of caller-owned workspace ifx_qgemm_prefill_ws uses at this shape
+ * (the fp16 copy of the activations, M x K halves), or 0 when the prefill
+ * GEMM at this shape does not use one: below the fp16 GEMM's range, or
+ * N < 16384, where too few weight tiles share the copy for it to pay. */
+int64_t ifx_qgemm_prefill_workspace_bytes(int quant_type, int M, int N, int K);
+
+/* ifx_qgemm_prefill with a caller-owned workspace (16-byte aligned, at least
+ * ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K) bytes; NULL or a zero
+ * requirement: exactly ifx_qgemm_prefill).  The fp16 GEMM then converts the
+ * Q8_1 activations to fp16 once, into the workspace, instead of once per
+ * weight tile; the results are bit-identical to ifx_qgemm_prefill.  The
+ * workspace is in use until the launches on `stream` complete.  A workspace
+ * smaller than required or misaligned returns IFX_BAD_GEOMETRY.  It plays
+ * the role of the reference's FP16 scratch for the dequantized weights
+ * (quantized_weight_map.cpp:176-233), for the activation operand. */
+int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                         int out_dtype, int mode, const void *bias, int M, int N, int K,
+                         void *workspace, int64_t workspace_bytes, void *stream);
+
 /* The prefill GEMM with an explicit kernel: IFX_PREFILL_INT8 is the
  * integer-exact int8 MFMA GEMM (the MMQ per-block arithmetic of
  * kernels/mmq.cuh:41-835); IFX_PREFILL_F16 dequantizes W (and the Q8_1

@@ -44,7 +44,8 @@ hipError_t launch_gemv_lds(int count, const void *const *W, void *const *Y, cons
                            const void *bias, const void *A, bool f16, int M, int K, int mode,
                            hipStream_t stream);
 bool gemm_f16_fits(int qtype, int K);
-hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *Y, const void *bias,
+int64_t gemm_f16_workspace_bytes(int M, int K);
+hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *A16, void *Y, const void *bias,
                            bool f16, int M, int N, int K, int mode, int splits_req,
                            hipStream_t stream);
 hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, const int *N,
@@ -286,7 +287,7 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
   if (!gemv_only(quant_type) && M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K))
-    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, 0, s));
+    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
   if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (use_lds(quant_type, M, K, N))
@@ -420,8 +421,37 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
   const bool f16 = out_dtype == IFX_OUT_F16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (use_f16_gemm(quant_type, M, K))
-    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, 0, s));
+    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
   return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+}
+
+// The fp16 copy pays where many weight tiles share it: measured at M = 512,
+// Q4_K 27648 x 5120 (108 tiles of 256 columns) 190 -> 162 us, Q6_K
+// 5120 x 27648 (20 tiles) 234 -> 250 us.
+constexpr int kMinWorkspaceN = 16384;
+
+int64_t ifx_qgemm_prefill_workspace_bytes(int quant_type, int M, int N, int K) {
+  if (!is_weight_type(quant_type) || gemv_only(quant_type) || M <= 0 || N <= 0 || K <= 0)
+    return 0;
+  if (!use_f16_gemm(quant_type, M, K) || !ifx::gemm_f16_fits(quant_type, K) || N < kMinWorkspaceN)
+    return 0;
+  return ifx::gemm_f16_workspace_bytes(M, K);
+}
+
+int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
+                         int mode, const void *bias, int M, int N, int K, void *workspace,
+                         int64_t workspace_bytes, void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
+  if (need == 0 || !workspace)
+    return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
+  if (workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, workspace, Y, bias,
+                                        out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
+                                        static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
@@ -442,7 +472,7 @@ int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, 
   }
   if (kernel != IFX_PREFILL_F16 || splits < 0) return IFX_BAD_GEOMETRY;
   if (!ifx::gemm_f16_fits(quant_type, K)) return IFX_BAD_GEOMETRY;
-  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, splits, s));
+  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, splits, s));
 }
 
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,

@@ -81,7 +81,8 @@ __device__ __forceinline__ h2 splat(float f) {
 template <int QT>
 struct Raw {
   uint32_t ads;     // Q8_1 {d, s}
-  u32x4 a0, a1;     // Q8_1 codes
+  u32x4 a0, a1;     // Q8_1 codes; fp16 activations (AH): the block's 64 bytes in a0..a3
+  u32x4 a2, a3;
   u32x4 w0, w1;     // Q4_K: header, 16 qs bytes; Q6_K: ql, qh; Q8_0: codes 0-15, 16-31
   uint32_t wx0, wx1;  // Q4_K: stage c & 3; Q6_K: 4 scale bytes, d; Q8_0: -, d
 };
@@ -100,11 +101,17 @@ __device__ __forceinline__ int stage_block(int c, int half) {
   }
 }
 
-template <int QT>
+template <int QT, bool AH>
 __device__ __forceinline__ void fetch(Raw<QT> &r, rsrc_t Wr, rsrc_t Ar, uint32_t w_off,
                                       uint32_t a_off, int c, int part) {
   // activation block: row (tid >> 1), half `part`
-  {
+  if constexpr (AH) {  // already converted: 32 fp16 values in commit's order
+    const uint32_t o = a_off + stage_block<QT>(c, part) * 64;
+    r.a0 = bload<u32x4>(Ar, o, 0);
+    r.a1 = bload<u32x4>(Ar, o + 16, 0);
+    r.a2 = bload<u32x4>(Ar, o + 32, 0);
+    r.a3 = bload<u32x4>(Ar, o + 48, 0);
+  } else {
     const uint32_t o = a_off + stage_block<QT>(c, part) * kQ8_1Bytes;
     r.ads = bload<uint32_t>(Ar, o, 0);
     r.a0 = bload<u32x4>(Ar, o + 4, 0);
@@ -152,16 +159,28 @@ __device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint
   p13 = as_u32(__builtin_elementwise_fma(b, d, -mn));
 }
 
+// The 32 activation values of one Q8_1 block as fp16, in the order the GEMM
+// stores them: word 2j / 2j+1 holds values (4j, 4j+2) / (4j+1, 4j+3).
+__device__ __forceinline__ void q8_1_block_to_h(uint32_t ads, u32x4 a0, u32x4 a1, uint32_t (&o)[16]) {
+  const h2 d = splat(h2f(ads & 0xFFFFu));
+  const uint32_t in[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) i8x4_to_h(in[j], d, o[2 * j], o[2 * j + 1]);
+}
+
 // Convert one stage's raw bytes and store them in LDS buffer `buf`.
-template <int QT>
+template <int QT, bool AH>
 __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int item) {
   const int row = item >> 1, part = item & 1;
-  {  // activations: 32 values of block `part` at slots 32*part ..
-    const h2 d = splat(h2f(r.ads & 0xFFFFu));
+  if constexpr (AH) {
+    u32x4 *dst = reinterpret_cast<u32x4 *>(&sm.a[buf][row * kPitch + 32 * part]);
+    dst[0] = r.a0;
+    dst[1] = r.a1;
+    dst[2] = r.a2;
+    dst[3] = r.a3;
+  } else {  // activations: 32 values of block `part` at slots 32*part ..
     uint32_t o[16];
-    const uint32_t in[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) i8x4_to_h(in[j], d, o[2 * j], o[2 * j + 1]);
+    q8_1_block_to_h(r.ads, r.a0, r.a1, o);
     u32x4 *dst = reinterpret_cast<u32x4 *>(&sm.a[buf][row * kPitch + 32 * part]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
@@ -248,7 +267,7 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
 // a third less LDS operand traffic per MFMA and twice the conversion work
 // per thread.
 // Each workgroup covers K stages [split * cps, min(nst, (split + 1) * cps)).
-template <int QT, int WV, bool F16OUT, bool ATOMIC>
+template <int QT, int WV, bool F16OUT, bool ATOMIC, bool AH>
 __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restrict__ W,
                                                          const uint8_t *__restrict__ A,
                                                          void *__restrict__ Y,
@@ -280,7 +299,8 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
   const int c_end = min(nst, c_begin + cps);
 
   const int nblk32 = K >> 5;
-  const uint32_t a_row = static_cast<uint32_t>(nblk32) * kQ8_1Bytes;
+  // AH: A holds fp16 activations (64 bytes per 32-value block)
+  const uint32_t a_row = static_cast<uint32_t>(nblk32) * (AH ? 64 : kQ8_1Bytes);
   const uint32_t w_row =
       static_cast<uint32_t>(QT == kTypeQ8_0 ? nblk32 * kQ8_0Bytes
                                             : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
@@ -307,7 +327,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
   auto fetch_stage = [&](Raw<QT> *r, int c) {
 #pragma unroll
     for (int u = 0; u < kIpt; ++u) {
-      fetch<QT>(r[u], Wr, Ar, w_off[u], a_off[u], c, part);
+      fetch<QT, AH>(r[u], Wr, Ar, w_off[u], a_off[u], c, part);
       if constexpr (QT == kTypeQ4_K) r[u].wx0 = static_cast<uint32_t>(c & 3);
       if constexpr (QT == kTypeQ6_K) {
         const int hf = c & 1;
@@ -318,7 +338,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
   };
   auto commit_stage = [&](int buf, const Raw<QT> *r) {
 #pragma unroll
-    for (int u = 0; u < kIpt; ++u) commit<QT>(sm, buf, r[u], tid + kT * u);
+    for (int u = 0; u < kIpt; ++u) commit<QT, AH>(sm, buf, r[u], tid + kT * u);
   };
 
   // Stage c+1 is converted into the idle buffer and stage c+2 is fetched in
@@ -395,13 +415,27 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
     }
 }
 
+// Q8_1 activations -> fp16 in the GEMM's staging order (64 bytes per block),
+// once per GEMM instead of once per weight tile: q8_1_block_to_h, the
+// conversion the GEMM applies itself, so both give the same bits.
+__global__ __launch_bounds__(256) void k_q8_1_to_f16(const uint8_t *__restrict__ A,
+                                                     u32x4 *__restrict__ out, int64_t nblocks) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= nblocks) return;
+  const uint8_t *src = A + t * kQ8_1Bytes;
+  uint32_t o[16];
+  q8_1_block_to_h(ldg<uint32_t>(src), ldg<u32x4>(src + 4), ldg<u32x4>(src + 20), o);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[t * 4 + j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+}
+
 namespace {
 
-template <int QT, bool F16OUT, bool ATOMIC, int WV = IFX_F16_WAVES>
+template <int QT, bool F16OUT, bool ATOMIC, bool AH, int WV = IFX_F16_WAVES>
 hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, int M, int N,
                     int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
                     hipStream_t s) {
-  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC>);
+  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>);
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -410,14 +444,30 @@ hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bia
     attr_set = true;
   }
   const dim3 grid(static_cast<unsigned>(m_tiles * n_tiles * splits));
-  hipLaunchKernelGGL((k_gemm_f16<QT, WV, F16OUT, ATOMIC>), grid, dim3(64 * WV), sizeof(Smem), s, W,
-                     A, Y, bias, M, N, K, mode, m_tiles, splits, cps);
+  hipLaunchKernelGGL((k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>), grid, dim3(64 * WV), sizeof(Smem), s,
+                     W, A, Y, bias, M, N, K, mode, m_tiles, splits, cps);
   return hipGetLastError();
 }
 
+template <int QT, bool F16OUT, bool ATOMIC>
+hipError_t launch_a(const uint8_t *W, const uint8_t *A, void *A16, void *Y, const void *bias,
+                    int M, int N, int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
+                    hipStream_t s) {
+  if (!A16)
+    return launch_k<QT, F16OUT, ATOMIC, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles,
+                                               splits, cps, s);
+  const int64_t nblocks = static_cast<int64_t>(M) * (K >> 5);
+  hipLaunchKernelGGL(k_q8_1_to_f16, dim3(static_cast<unsigned>((nblocks + 255) / 256)), dim3(256),
+                     0, s, A, static_cast<u32x4 *>(A16), nblocks);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_k<QT, F16OUT, ATOMIC, true>(W, static_cast<const uint8_t *>(A16), Y, bias, M, N,
+                                            K, mode, m_tiles, n_tiles, splits, cps, s);
+}
+
 template <int QT>
-hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, bool f16,
-                     int M, int N, int K, int mode, int splits_req, hipStream_t s) {
+hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, const void *bias,
+                     bool f16, int M, int N, int K, int mode, int splits_req, hipStream_t s) {
   const int m_tiles = (M + kBM - 1) / kBM, n_tiles = (N + kBN - 1) / kBN;
   const int nst = K / kBK;
   // Split K only for fp32 outputs, when the tile grid fills less than 3/4
@@ -442,12 +492,12 @@ hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *Y, const void *bi
       f.n[0] = static_cast<int64_t>(M) * N;
       if (launch_fill_zero(f, 1, s) != hipSuccess) return hipGetLastError();
     }
-    return launch_k<QT, false, true>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits, cps,
-                                     s);
+    return launch_a<QT, false, true>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits,
+                                     cps, s);
   }
   if (f16)
-    return launch_k<QT, true, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
-  return launch_k<QT, false, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
+    return launch_a<QT, true, false>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
+  return launch_a<QT, false, false>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
 }
 
 }  // namespace
@@ -458,17 +508,28 @@ bool gemm_f16_fits(int qtype, int K) {
   return false;
 }
 
-// splits_req: 0 = chosen from the tile grid, else forced (tests).
-hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *Y, const void *bias,
-                           bool f16, int M, int N, int K, int mode, int splits_req,
-                           hipStream_t stream) {
+// Bytes of the fp16 activation copy the GEMM can use (M x K halves), or 0
+// when it would not fit the kernel's 32-bit buffer offsets.
+int64_t gemm_f16_workspace_bytes(int M, int K) {
+  const int64_t b = static_cast<int64_t>(M) * K * 2;
+  return b < (int64_t{1} << 32) ? b : 0;
+}
+
+// splits_req: 0 = chosen from the tile grid, else forced (tests).  A16:
+// caller-owned workspace of gemm_f16_workspace_bytes(M, K) bytes (16-byte
+// aligned) for the fp16 activations, converted once before the GEMM; NULL:
+// each workgroup converts its Q8_1 activation tiles itself.  Same results.
+hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *A16, void *Y,
+                           const void *bias, bool f16, int M, int N, int K, int mode,
+                           int splits_req, hipStream_t stream) {
   const uint8_t *w = static_cast<const uint8_t *>(W);
   const uint8_t *a = static_cast<const uint8_t *>(A);
   if (!gemm_f16_fits(qtype, K)) return hipErrorInvalidValue;
+  if (A16 && gemm_f16_workspace_bytes(M, K) == 0) A16 = nullptr;
   switch (qtype) {
-  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(w, a, Y, bias, f16, M, N, K, mode, splits_req, stream);
-  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(w, a, Y, bias, f16, M, N, K, mode, splits_req, stream);
-  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(w, a, Y, bias, f16, M, N, K, mode, splits_req, stream);
+  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
+  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
+  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
   default: return hipErrorInvalidValue;
   }
 }

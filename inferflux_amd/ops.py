@@ -128,6 +128,30 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     return out
 
 
+def prefill_workspace_bytes(qtype, M, N, K):
+    """Bytes of workspace qgemm_prefill_ws uses at this shape (0: none)."""
+    return int(_lib.load().ifx_qgemm_prefill_workspace_bytes(qtype, M, N, K))
+
+
+def qgemm_prefill_ws(qtype, W, A, M, N, K, workspace, out=None, out_dtype=torch.float32,
+                     mode=STORE, bias=None, stream=None):
+    """The prefill GEMM with a caller-owned workspace (a device tensor of at
+    least prefill_workspace_bytes bytes): the fp16 activations are converted
+    once into it; bit-identical to qgemv(..., prefill=True)."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, N, K) or A.numel() < M * (K // 32) * 36 or out.numel() < M * N:
+        raise ValueError("W, A or out is smaller than the shape")
+    nbytes = workspace.numel() * workspace.element_size()
+    bptr = _dev(bias, "bias") if bias is not None else None
+    rc = _lib.load().ifx_qgemm_prefill_ws(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"), od,
+                                          mode, bptr, M, N, K, _dev(workspace, "workspace"), nbytes,
+                                          _stream(stream))
+    _check(rc, "ifx_qgemm_prefill_ws")
+    return out
+
+
 PREFILL_INT8, PREFILL_F16, DECODE_DQ_F16 = 1, 2, 3
 
 

@@ -319,6 +319,38 @@ def test_gemv_dq_parity(orc, dev, qtype, M, N, K, splits):
             ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, splits, out_dtype=torch.float16)
 
 
+@pytest.mark.parametrize("qtype,M,N,K", [(Q4_K, 128, 16400, 512), (Q4_K, 256, 16384, 256),
+                                         (Q6_K, 129, 16384, 256), (Q8_0, 200, 16500, 192),
+                                         (Q6_K, 512, 320, 4096)])
+def test_gemm_f16_workspace(orc, dev, qtype, M, N, K):
+    """The activations converted once into a caller workspace give the same
+    bits as the per-tile conversion (fp16 output: no split-K atomics), and
+    fp32 outputs pass the oracle bar; a short or misaligned workspace is
+    refused.  Below N = 16384 no workspace is used and the call is the plain
+    prefill GEMM."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemm_f16 workspace type={qtype} M={M} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=M + N)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=K + 1, outlier_frac=0.01))
+    need = ops.prefill_workspace_bytes(qtype, M, N, K)
+    assert need == (M * K * 2 if N >= 16384 else 0)
+    ws = torch.empty(max(need, 16) // 2 + 8, dtype=torch.float16, device=dev)
+    W, A = up(w, dev), up(a, dev)
+    y16 = ops.qgemv(qtype, W, A, M, N, K, out_dtype=torch.float16, prefill=True)
+    y16w = ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws, out_dtype=torch.float16)
+    assert np.array_equal(down(y16w).view(np.uint16), down(y16).view(np.uint16))
+    y = ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws)
+    check_rows(down(y), orc.gemv_exact(qtype, w, a, M, N, K))
+    if need:
+        with pytest.raises(ops.NotHandled):
+            ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws[: need // 2 - 1])
+        with pytest.raises(ops.NotHandled):
+            ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws[1:])
+    # below the fp16 GEMM's range there is no workspace
+    assert ops.prefill_workspace_bytes(qtype, 64, N, K) == 0
+
+
 def test_gemm_f16_rejects_ragged_k(dev):
     import torch
     from inferflux_amd import ops
