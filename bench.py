@@ -530,7 +530,8 @@ def profile_run(args, dev):
 def profile_kernels_run(args, dev):
     """Eager launches for rocprofv3 counter runs of the batch kernels:
     `steps` launches each of the config-5 prefill GEMMs on the fp16 kernel
-    and (a quarter as many) on the int8 kernel, and of the config-4 14B
+    (and, where the shape uses one, with the activation workspace) and (a
+    quarter as many) on the int8 kernel, and of the config-4 14B
     grouped gate+up and down launches at M = 32 (weights rotating over
     >= 512 MB of replicas), then 20 copies of exactly 64 MiB for counter
     calibration.  Prints one JSON line of event timings."""
@@ -561,6 +562,12 @@ def profile_kernels_run(args, dev):
                                ("int8", ops.PREFILL_INT8, max(1, args.steps // 4))):
             out[f"prefill_{name}_{kname}_us"] = timed(
                 lambda i, kern=kern: ops.qgemm_prefill_kernel(qt, w, A, M, N, K, kern, out=Y), n)
+        need = ops.prefill_workspace_bytes(qt, M, N, K)
+        if need:  # the fp16 kernel with the activations converted once
+            wsp = torch.empty(need, dtype=torch.uint8, device=dev)
+            out[f"prefill_{name}_f16_workspace_us"] = timed(
+                lambda i: ops.qgemm_prefill_ws(qt, w, A, M, N, K, wsp, out=Y), args.steps)
+            del wsp
         del w
     M = 32
     layer = {n: (qt, N, K) for n, qt, N, K in workloads.QWEN14B_LAYER}
