@@ -129,6 +129,31 @@ def main():
         del g
         return a.elapsed_time(b) * 1e3 / steps  # us per call
 
+    def spread(fn, steps, reps=15):
+        """median / p10 / p90 of us per call over `reps` replays of one graph
+        of `steps` calls, each replay timed on its own (events on torch's
+        current stream, the stream the kernels run on)."""
+        fn(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(reps):
+            a, b = ev(), ev()
+            a.record()
+            g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            samples.append(a.elapsed_time(b) * 1e3 / steps)
+        del g
+        p10, med, p90 = np.percentile(samples, [10, 50, 90])
+        return {"median_us": round(float(med), 2), "p10_us": round(float(p10), 2),
+                "p90_us": round(float(p90), 2), "replays": reps, "calls_per_replay": steps}
+
     def decode_layer_runner(layer, M, seed, fused=False):
         """One decode layer at batch M as a chain over an fp32 residual
         stream: RMSNorm+Q8_1 -> grouped QKV -> Q8_1 of the attention output
@@ -271,6 +296,7 @@ def main():
             step_is = min(variants, key=variants.get)
             ms_per_step = variants[step_is] / 1e3
             headline = q4_bytes / q4_us / 1e3
+            step_spread = spread(dict(zip(variants, (run, runf, runs)))[step_is], steps)
     extras["qwen3b_layer"] = per_m
 
     # --------------------------------------- dominant kernel: roofline
@@ -285,6 +311,8 @@ def main():
     dom_us = time_loop(lambda i: ops.qgemv_grouped(qt, [gate[i % R3], up[i % R3]], A1, M, [N, N],
                                                    K, outs=Yg),
                        max(args.steps, 200), args.warmup)
+    dom_spread = spread(lambda i: ops.qgemv_grouped(qt, [gate[i % R3], up[i % R3]], A1, M, [N, N],
+                                                    K, outs=Yg), max(args.steps, 200))
     dom_bytes = gemv_bytes(ops, qt, M, [N, N], K)
     achieved = dom_bytes / dom_us / 1e3
     result["roofline"] = {
@@ -457,6 +485,7 @@ def main():
                    "M": 1, "hidden": 2048, "ffn": 11008, "weight_replicas": R3,
                    "launches": [l[0] for l in workloads.DECODE_LAUNCHES],
                    "step": step_is,
+                   "spread": {"step": step_spread, "dominant_kernel": dom_spread},
                    "value_is": "HBM GB/s of the layer's Q4_K GEMV launches (QKV, O, gate+up)",
                    "frac_of_hbm_peak": round(headline / HBM_PEAK_GBS, 4)},
         "roofline": result["roofline"],
