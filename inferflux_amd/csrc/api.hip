@@ -380,7 +380,8 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   // the fused kernel serves the decode batch M <= 2 and whole Q8_1 blocks
   // of outputs; other shapes take the grouped GEMV + SiLU producer
-  if (M < 1 || M > 2 || N % 32 != 0) return IFX_BAD_GEOMETRY;
+  const int max_m = (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
+  if (M < 1 || M > max_m || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)
   void *probe_out = H ? H : q8_1_out;
@@ -406,7 +407,8 @@ int ifx_qgemv_gate_up_silu_rmsnorm(int quant_type, const void *W_gate, const voi
                                  nullptr, M, N, K);
   if (rc != IFX_OK) return rc;
   // the wide Q4_K kernel only: one row's slices fit half a wave
-  if (quant_type != IFX_TYPE_Q4_K || M > 2 || N % 32 != 0 || K > 2048) return IFX_BAD_GEOMETRY;
+  if (quant_type != IFX_TYPE_Q4_K || M > IFX_SWIGLU_MAX_M || N % 32 != 0 || K > 2048)
+    return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_gemv_swiglu_rmsnorm(W_gate, W_up, residual,
                                                    residual_dtype == IFX_OUT_F16, norm_weight, eps,
                                                    H, h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,

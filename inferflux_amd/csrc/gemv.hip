@@ -1123,7 +1123,7 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   const uint8_t *g = static_cast<const uint8_t *>(Wg), *u = static_cast<const uint8_t *>(Wu);
   const uint8_t *a = static_cast<const uint8_t *>(A);
   uint8_t *q = static_cast<uint8_t *>(Q);
-  if (qtype == kTypeQ4_K && K <= kSwigluWideMaxK && M <= 2 && swiglu_wide_env()) {
+  if (qtype == kTypeQ4_K && K <= kSwigluWideMaxK && M <= IFX_SWIGLU_MAX_M && swiglu_wide_env()) {
     const SwigluArgs args{g, u, a, nullptr, nullptr, 0.0f, H, q, M, N, K};
     launch_swiglu_wide<0>(args, f16h, stream);
     return hipGetLastError();
@@ -1144,7 +1144,7 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
 hipError_t launch_gemv_swiglu_rmsnorm(const void *Wg, const void *Wu, const void *x, bool x_f16,
                                       const uint16_t *norm_w, float eps, void *H, bool f16h,
                                       void *Q, int M, int N, int K, hipStream_t stream) {
-  if (M < 1 || M > 2 || K > kSwigluWideMaxK || N % 32 != 0) return hipErrorInvalidValue;
+  if (M < 1 || M > IFX_SWIGLU_MAX_M || K > kSwigluWideMaxK || N % 32 != 0) return hipErrorInvalidValue;
   const SwigluArgs args{static_cast<const uint8_t *>(Wg), static_cast<const uint8_t *>(Wu),
                         nullptr, x, norm_w, eps, H, static_cast<uint8_t *>(Q), M, N, K};
   if (x_f16) launch_swiglu_wide<2>(args, f16h, stream);

@@ -15,6 +15,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Largest batch of the fused gate/up/SiLU kernel on wide Q4_K slices (one
+// workgroup per batch column).  Measured at 11008 x 2048: from M = 3 on it
+// loses to grouped GEMV + SiLU producer (M = 3 / 4 / 8: 12.6 / 14.5 / 23.0 us
+// against 10.6 / 11.5 / 11.5 us): every column re-reads the weights.
+#ifndef IFX_SWIGLU_MAX_M
+#define IFX_SWIGLU_MAX_M 2
+#endif
+
 namespace ifx {
 
 constexpr int kTypeQ8_0 = 8;
