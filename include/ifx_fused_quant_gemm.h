@@ -61,7 +61,7 @@ enum class KernelFamily : int {
   kGemv = 1,
   kSkinnyMfma = 2,
   kTiledMfma = 3,
-  kF16DequantMfma = 4,  // fp16 MFMA with in-kernel dequant (prefill, M >= 128)
+  kF16DequantMfma = 4,  // fp16 MFMA with in-kernel dequant (prefill; M >= 33 Q6_K, 96 Q4_K, 128 Q8_0)
   kF16DequantGemv = 5   // fp16 dequant MFMA GEMV (decode batches 17 <= M <= 32)
 };
 

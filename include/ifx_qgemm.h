@@ -153,9 +153,10 @@ int ifx_qgemv_gate_up_silu_rmsnorm(int quant_type, const void *W_gate, const voi
                                    const uint16_t *norm_weight, float eps, void *H, int h_dtype,
                                    void *q8_1_out, int M, int N, int K, void *stream);
 
-/* The prefill GEMM alone, for any M >= 1, fp32 accumulate: the int8 MFMA
- * GEMM below 128 rows, from 128 rows on the fp16 MFMA GEMM with in-kernel
- * dequant (see ifx_qgemm_prefill_kernel).  Replaces the reference's dequantize-to-FP16 + cublasGemmEx fallback
+/* The prefill GEMM alone, for any M >= 1, fp32 accumulate: the fp16 MFMA
+ * GEMM with in-kernel dequant from 33 (Q6_K), 96 (Q4_K) or 128 (Q8_0) rows
+ * on, the int8 MFMA GEMM below (see ifx_qgemm_prefill_kernel).  Replaces
+ * the reference's dequantize-to-FP16 + cublasGemmEx fallback
  * (quantized_weight_map.cpp:176-233, cublas_gemm.h:47, called at
  * transformer_forward.cu:1479). */
 int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y,
@@ -211,7 +212,7 @@ int ifx_supports(int quant_type, int M, int N, int K);
 
 /* Kernel family ifx_qgemv runs (quant_type, M, N, K) on: 0 = not supported,
  * 1 = v_dot4 GEMV, 2 = skinny int8 MFMA (decode batches), 3 = tiled int8
- * MFMA, 4 = fp16 MFMA with in-kernel dequant (prefill, M >= 128), 5 = fp16
+ * MFMA, 4 = fp16 MFMA with in-kernel dequant (prefill; M >= 33 Q6_K, 96 Q4_K, 128 Q8_0), 5 = fp16
  * dequant MFMA GEMV (decode batches 17 <= M <= 32).  No
  * reference counterpart (the reference logs the choice,
  * fused_quant_gemm.cu:2104-2117). */

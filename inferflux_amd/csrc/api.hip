@@ -69,22 +69,28 @@ namespace {
 //   M <= 2       v_dot4 GEMV        (gemv.hip)
 //   3 <= M <= 32 skinny int8 MFMA   (mmq_skinny.hip), K % 256 == 0
 //   M > 32       tiled int8 MFMA    (gemm_mfma.hip)
-//   M >= 128     fp16 MFMA with in-kernel dequant (gemm_f16.hip), the
-//                reference's FP16 prefill arithmetic
+//   M >= 33 (Q6_K), 96 (Q4_K), 128 (Q8_0): fp16 MFMA with in-kernel dequant
+//                (gemm_f16.hip), the reference's FP16 prefill arithmetic
 constexpr int kMaxGemvMDefault = 2;
 constexpr int kMaxSkinnyM = 32;
-constexpr int kMinF16GemmM = 128;
+// Prefill kernel for M > 32: the fp16 GEMM from min_f16_gemm_m(qtype) rows
+// on, else the int8 MFMA GEMM.  Measured at the 32B shapes (graph-replayed,
+// us for fp16 / int8): Q6_K 5120 x 27648 M = 48: 111 / 438, M = 128: 118 /
+// 438 (the int8 kernel's per-block rescale of 16-value Q6_K groups); Q4_K
+// 27648 x 5120 M = 48: 104 / 63, M = 64: 98 / 64, M = 96: 99 / 105, M = 128:
+// 102 / 104.  Q8_0 is unmeasured and keeps 128 (a 256-row tile is mostly
+// padding below that).  IFX_PREFILL=int8|f16 forces one (tuning; read once).
+int min_f16_gemm_m(int qtype) {
+  return qtype == IFX_TYPE_Q6_K ? kMaxSkinnyM + 1 : qtype == IFX_TYPE_Q4_K ? 96 : 128;
+}
 
-// Prefill kernel for M > 32: the fp16 GEMM from kMinF16GemmM rows on (a
-// 256-row tile is mostly padding below that).  IFX_PREFILL=int8|f16 forces
-// one (tuning; read once).
 bool use_f16_gemm(int qtype, int M, int K) {
   static const int v = [] {
     const char *e = getenv("IFX_PREFILL");
     return e ? (e[0] == 'i' ? 1 : e[0] == 'f' ? 2 : 0) : 0;
   }();
   if (!ifx::gemm_f16_fits(qtype, K) || v == 1) return false;
-  return v == 2 || M >= kMinF16GemmM;
+  return v == 2 || M >= min_f16_gemm_m(qtype);
 }
 // Q5_K and Q8_K run on the v_dot4 GEMV only, for M <= 64: the reference's
 // Q8_K dispatch stops at 64 (fused_quant_gemm.cu:1740-1747) and it has no

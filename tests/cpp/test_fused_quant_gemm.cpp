@@ -191,6 +191,8 @@ void TestPolicy() {
   EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 16, 5120, 13824) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 512, 27648, 5120) == KernelFamily::kF16DequantMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 64, 27648, 5120) == KernelFamily::kTiledMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q4_K, 96, 27648, 5120) == KernelFamily::kF16DequantMfma);
+  EXPECT(FusedQuantGemm::SelectKernel(Q6_K, 48, 5120, 27648) == KernelFamily::kF16DequantMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 512, 64, 2080) == KernelFamily::kGemv);  // K % 64 != 0
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 8, 64, 2080) == KernelFamily::kSkinnyMfma);
   EXPECT(FusedQuantGemm::SelectKernel(Q8_0, 40, 64, 2080) == KernelFamily::kGemv);

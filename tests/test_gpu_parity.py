@@ -347,8 +347,8 @@ def test_gemm_f16_workspace(orc, dev, qtype, M, N, K):
             ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws[: need // 2 - 1])
         with pytest.raises(ops.NotHandled):
             ops.qgemm_prefill_ws(qtype, W, A, M, N, K, ws[1:])
-    # below the fp16 GEMM's range there is no workspace
-    assert ops.prefill_workspace_bytes(qtype, 64, N, K) == 0
+    # below the prefill range there is no workspace
+    assert ops.prefill_workspace_bytes(qtype, 32, N, K) == 0
 
 
 def test_gemm_f16_rejects_ragged_k(dev):
