@@ -436,13 +436,10 @@ hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bia
                     int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
                     hipStream_t s) {
   const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>);
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(sizeof(Smem)));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  // set once per instantiation (a function-local static: thread-safe)
+  static const hipError_t attr = hipFuncSetAttribute(
+      fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(Smem)));
+  if (attr != hipSuccess) return attr;
   const dim3 grid(static_cast<unsigned>(m_tiles * n_tiles * splits));
   hipLaunchKernelGGL((k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>), grid, dim3(64 * WV), sizeof(Smem), s,
                      W, A, Y, bias, M, N, K, mode, m_tiles, splits, cps);

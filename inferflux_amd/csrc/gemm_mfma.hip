@@ -429,15 +429,15 @@ static hipError_t launch_qts(const uint8_t *W, const uint8_t *A, void *Y, const 
   const dim3 grid((N + kB - 1) / kB, (M + kB - 1) / kB);
   const size_t shm = sizeof(Smem<QT, S>);
   // The staged tiles can exceed the 64 KiB default; gfx950 has 160 KiB of LDS.
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[f16]) {
-    const void *fn = f16 ? reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, true>)
-                         : reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, false>);
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(shm));
-    if (e != hipSuccess) return e;
-    attr_set[f16] = true;
-  }
+  // set once per kernel (function-local statics: thread-safe)
+  static const hipError_t attr_f32 = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, false>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
+  static const hipError_t attr_f16 = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
+  const hipError_t attr = f16 ? attr_f16 : attr_f32;
+  if (attr != hipSuccess) return attr;
   if (f16)
     hipLaunchKernelGGL((k_gemm_mfma<QT, S, true>), grid, dim3(256), shm, s, W, A, Y, bias, M, N, K, mode);
   else
