@@ -416,17 +416,23 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
 }
 
 // Q8_1 activations -> fp16 in the GEMM's staging order (64 bytes per block),
-// once per GEMM instead of once per weight tile: q8_1_block_to_h, the
-// conversion the GEMM applies itself, so both give the same bits.
+// once per GEMM instead of once per weight tile, with the conversion the
+// GEMM applies itself (i8x4_to_h on the block's fp16 d), so both give the
+// same bits.  Thread t writes 16 bytes, words 4q..4q+3 of block t/4
+// (q = t%4), i.e. codes 8q..8q+7: consecutive threads store consecutive
+// 16-byte chunks.
 __global__ __launch_bounds__(256) void k_q8_1_to_f16(const uint8_t *__restrict__ A,
-                                                     u32x4 *__restrict__ out, int64_t nblocks) {
+                                                     u32x4 *__restrict__ out, int64_t nchunks) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= nblocks) return;
-  const uint8_t *src = A + t * kQ8_1Bytes;
-  uint32_t o[16];
-  q8_1_block_to_h(ldg<uint32_t>(src), ldg<u32x4>(src + 4), ldg<u32x4>(src + 20), o);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) out[t * 4 + j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+  if (t >= nchunks) return;
+  const uint8_t *src = A + (t >> 2) * kQ8_1Bytes;
+  const int q = static_cast<int>(t & 3);
+  const h2 d = splat(h2f(ldg<uint32_t>(src) & 0xFFFFu));
+  const u32x2 c = ldg<u32x2>(src + 4 + 8 * q);
+  uint32_t o[4];
+  i8x4_to_h(c.x, d, o[0], o[1]);
+  i8x4_to_h(c.y, d, o[2], o[3]);
+  out[t] = u32x4{o[0], o[1], o[2], o[3]};
 }
 
 namespace {
@@ -453,9 +459,9 @@ hipError_t launch_a(const uint8_t *W, const uint8_t *A, void *A16, void *Y, cons
   if (!A16)
     return launch_k<QT, F16OUT, ATOMIC, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles,
                                                splits, cps, s);
-  const int64_t nblocks = static_cast<int64_t>(M) * (K >> 5);
-  hipLaunchKernelGGL(k_q8_1_to_f16, dim3(static_cast<unsigned>((nblocks + 255) / 256)), dim3(256),
-                     0, s, A, static_cast<u32x4 *>(A16), nblocks);
+  const int64_t nchunks = static_cast<int64_t>(M) * (K >> 5) * 4;
+  hipLaunchKernelGGL(k_q8_1_to_f16, dim3(static_cast<unsigned>((nchunks + 255) / 256)), dim3(256),
+                     0, s, A, static_cast<u32x4 *>(A16), nchunks);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_k<QT, F16OUT, ATOMIC, true>(W, static_cast<const uint8_t *>(A16), Y, bias, M, N,
