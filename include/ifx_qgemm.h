@@ -218,6 +218,19 @@ int ifx_supports(int quant_type, int M, int N, int K);
  * fused_quant_gemm.cu:2104-2117). */
 int ifx_kernel_family(int quant_type, int M, int N, int K);
 
+/* Launch log of the calling thread.  ifx_launch_log_begin opens it: every
+ * kernel that the entry points called afterwards on this thread launch is
+ * recorded by instance name ("k_gemv<12,1,2,1,4,0,2>": kernel name and
+ * template arguments as integers, ';'-separated, in launch order).  With
+ * dry_run != 0 nothing is launched (no HIP call is made, no pointer is
+ * dereferenced; entry points return IFX_OK after validation), so the
+ * dispatch of any shape can be inspected on a host without a GPU.
+ * ifx_launch_log_end closes the log and returns its text, valid until the
+ * next begin on this thread ("" when no log is open).  Replaces the reference's one-time dispatch log
+ * (fused_quant_gemm.cu:2104-2117), which names the chosen kernel path. */
+void ifx_launch_log_begin(int dry_run);
+const char *ifx_launch_log_end(void);
+
 /* Bytes per block / values per block of a quant type (0 if unknown). */
 int ifx_block_bytes(int quant_type);
 int ifx_block_elems(int quant_type);

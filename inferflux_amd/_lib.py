@@ -30,6 +30,8 @@ SIGNATURES = {
     "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
+    "ifx_launch_log_begin": ([_i32], None),
+    "ifx_launch_log_end": ([], ctypes.c_char_p),
     "ifx_supports": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_block_bytes": ([_i32], _i32),
     "ifx_block_elems": ([_i32], _i32),

@@ -12,6 +12,8 @@
 
 #include <stdlib.h>
 
+#include <string>
+
 namespace ifx {
 hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
                                 hipStream_t stream);
@@ -60,6 +62,38 @@ bool gemv_slot_fits(int qtype, int M, int K);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
                             int mode, hipStream_t stream);
+}  // namespace ifx
+
+// ---------------------------------------------------------------- launch log
+namespace ifx {
+namespace {
+struct LaunchLog {
+  bool open = false, dry = false;
+  std::string text;
+};
+thread_local LaunchLog g_log;
+}  // namespace
+
+bool note_launch(const char *kernel, std::initializer_list<int> targs) {
+  if (g_log.open) {
+    if (!g_log.text.empty()) g_log.text += ';';
+    g_log.text += kernel;
+    if (targs.size()) {
+      g_log.text += '<';
+      bool first = true;
+      for (int v : targs) {
+        if (!first) g_log.text += ',';
+        g_log.text += std::to_string(v);
+        first = false;
+      }
+      g_log.text += '>';
+    }
+  }
+  return !g_log.dry;
+}
+bool dry_run() { return g_log.dry; }
+hipError_t last_error() { return g_log.dry ? hipSuccess : hipGetLastError(); }
+hipError_t peek_error() { return g_log.dry ? hipSuccess : hipPeekAtLastError(); }
 }  // namespace ifx
 
 namespace {
@@ -250,6 +284,19 @@ int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   if (!use_slot(quant_type, M, K, N, false) && use_dq(quant_type, M, K, false)) return 5;
   return M <= kMaxSkinnyM ? 2 : 3;
+}
+
+void ifx_launch_log_begin(int dry_run) {
+  ifx::g_log.open = true;
+  ifx::g_log.dry = dry_run != 0;
+  ifx::g_log.text.clear();
+}
+
+const char *ifx_launch_log_end(void) {
+  if (!ifx::g_log.open) return "";
+  ifx::g_log.open = false;
+  ifx::g_log.dry = false;
+  return ifx::g_log.text.c_str();
 }
 
 int ifx_q8_1_quantize_f32(const float *x, void *q8_1, int M, int K, void *stream) {

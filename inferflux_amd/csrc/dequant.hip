@@ -122,9 +122,9 @@ static void launch_dq(const uint8_t *W, uint32_t w_bytes, void *out, bool f16, i
                       hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((ngroups + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL((k_dequant<QT, true>), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
+    IFX_LAUNCH(k_dequant, (QT, true), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
   else
-    hipLaunchKernelGGL((k_dequant<QT, false>), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
+    IFX_LAUNCH(k_dequant, (QT, false), grid, dim3(256), 0, s, W, w_bytes, out, ngroups);
 }
 
 // n_elems must be a multiple of the block size of qtype and the tensor
@@ -148,7 +148,7 @@ hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int6
   case kTypeQ8_K: launch_dq<kTypeQ8_K>(w, wb, out, f16, ngroups, stream); break;
   default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

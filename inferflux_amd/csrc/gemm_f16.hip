@@ -443,13 +443,15 @@ hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bia
                     hipStream_t s) {
   const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>);
   // set once per instantiation (a function-local static: thread-safe)
-  static const hipError_t attr = hipFuncSetAttribute(
-      fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(Smem)));
-  if (attr != hipSuccess) return attr;
+  if (!dry_run()) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(Smem)));
+    if (attr != hipSuccess) return attr;
+  }
   const dim3 grid(static_cast<unsigned>(m_tiles * n_tiles * splits));
-  hipLaunchKernelGGL((k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>), grid, dim3(64 * WV), sizeof(Smem), s,
+  IFX_LAUNCH(k_gemm_f16, (QT, WV, F16OUT, ATOMIC, AH), grid, dim3(64 * WV), sizeof(Smem), s,
                      W, A, Y, bias, M, N, K, mode, m_tiles, splits, cps);
-  return hipGetLastError();
+  return last_error();
 }
 
 template <int QT, bool F16OUT, bool ATOMIC>
@@ -460,9 +462,9 @@ hipError_t launch_a(const uint8_t *W, const uint8_t *A, void *A16, void *Y, cons
     return launch_k<QT, F16OUT, ATOMIC, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles,
                                                splits, cps, s);
   const int64_t nchunks = static_cast<int64_t>(M) * (K >> 5) * 4;
-  hipLaunchKernelGGL(k_q8_1_to_f16, dim3(static_cast<unsigned>((nchunks + 255) / 256)), dim3(256),
+  IFX_LAUNCH0(k_q8_1_to_f16, dim3(static_cast<unsigned>((nchunks + 255) / 256)), dim3(256),
                      0, s, A, static_cast<u32x4 *>(A16), nchunks);
-  const hipError_t e = hipGetLastError();
+  const hipError_t e = last_error();
   if (e != hipSuccess) return e;
   return launch_k<QT, F16OUT, ATOMIC, true>(W, static_cast<const uint8_t *>(A16), Y, bias, M, N,
                                             K, mode, m_tiles, n_tiles, splits, cps, s);
@@ -493,7 +495,7 @@ hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, con
       FillArgs f{};
       f.y[0] = static_cast<float *>(Y);
       f.n[0] = static_cast<int64_t>(M) * N;
-      if (launch_fill_zero(f, 1, s) != hipSuccess) return hipGetLastError();
+      if (launch_fill_zero(f, 1, s) != hipSuccess) return last_error();
     }
     return launch_a<QT, false, true>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits,
                                      cps, s);

@@ -430,19 +430,21 @@ static hipError_t launch_qts(const uint8_t *W, const uint8_t *A, void *Y, const 
   const size_t shm = sizeof(Smem<QT, S>);
   // The staged tiles can exceed the 64 KiB default; gfx950 has 160 KiB of LDS.
   // set once per kernel (function-local statics: thread-safe)
-  static const hipError_t attr_f32 = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
-  static const hipError_t attr_f16 = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, true>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
-  const hipError_t attr = f16 ? attr_f16 : attr_f32;
-  if (attr != hipSuccess) return attr;
+  if (!dry_run()) {
+    static const hipError_t attr_f32 = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, false>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
+    static const hipError_t attr_f16 = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemm_mfma<QT, S, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
+    const hipError_t attr = f16 ? attr_f16 : attr_f32;
+    if (attr != hipSuccess) return attr;
+  }
   if (f16)
-    hipLaunchKernelGGL((k_gemm_mfma<QT, S, true>), grid, dim3(256), shm, s, W, A, Y, bias, M, N, K, mode);
+    IFX_LAUNCH(k_gemm_mfma, (QT, S, true), grid, dim3(256), shm, s, W, A, Y, bias, M, N, K, mode);
   else
-    hipLaunchKernelGGL((k_gemm_mfma<QT, S, false>), grid, dim3(256), shm, s, W, A, Y, bias, M, N, K, mode);
-  return hipGetLastError();
+    IFX_LAUNCH(k_gemm_mfma, (QT, S, false), grid, dim3(256), shm, s, W, A, Y, bias, M, N, K, mode);
+  return last_error();
 }
 
 // 128 x 128 workgroup tiles when they give at least two workgroups per CU,

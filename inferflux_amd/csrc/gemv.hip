@@ -709,9 +709,9 @@ static void launch_t(GemvArgs args, bool f16, hipStream_t s) {
   const dim3 grid(blocks, (args.M + MC - 1) / MC);
   const dim3 block(64 * G * P);
   if (f16)
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, true, H>), grid, block, 0, s, args);
+    IFX_LAUNCH(k_gemv, (QT, MC, R, G, P, true, H), grid, block, 0, s, args);
   else
-    hipLaunchKernelGGL((k_gemv<QT, MC, R, G, P, false, H>), grid, block, 0, s, args);
+    IFX_LAUNCH(k_gemv, (QT, MC, R, G, P, false, H), grid, block, 0, s, args);
 }
 
 // Rows per wave section: IFX_GEMV_H in {1, 2, 4} forces full-, half- or
@@ -828,10 +828,10 @@ static void launch_norm_t(GemvArgs args, bool f16, hipStream_t s) {
   const dim3 grid(blocks, (args.M + MC - 1) / MC);
   const size_t shm = static_cast<size_t>(MC) * (args.K >> 5) * kQ8_1Bytes;
   if (f16)
-    hipLaunchKernelGGL((k_gemv<kTypeQ4_K, MC, R, G, P, true, H, NORM>), grid, dim3(256), shm, s,
+    IFX_LAUNCH(k_gemv, (kTypeQ4_K, MC, R, G, P, true, H, NORM), grid, dim3(256), shm, s,
                        args);
   else
-    hipLaunchKernelGGL((k_gemv<kTypeQ4_K, MC, R, G, P, false, H, NORM>), grid, dim3(256), shm, s,
+    IFX_LAUNCH(k_gemv, (kTypeQ4_K, MC, R, G, P, false, H, NORM), grid, dim3(256), shm, s,
                        args);
 }
 
@@ -875,7 +875,7 @@ static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStre
   case kTypeQ8_K: launch_type<kTypeQ8_K>(args, f16, stream); break;
   default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 // ---------------------------------------------------------------------------
@@ -1088,8 +1088,8 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args
 template <int NORM>
 static void launch_swiglu_wide(const SwigluArgs &a, bool f16h, hipStream_t s) {
   const dim3 grid(a.N / 32, a.M);
-  if (f16h) hipLaunchKernelGGL((k_gemv_swiglu_wide<1, true, NORM>), grid, dim3(1024), 0, s, a);
-  else hipLaunchKernelGGL((k_gemv_swiglu_wide<1, false, NORM>), grid, dim3(1024), 0, s, a);
+  if (f16h) IFX_LAUNCH(k_gemv_swiglu_wide, (1, true, NORM), grid, dim3(1024), 0, s, a);
+  else IFX_LAUNCH(k_gemv_swiglu_wide, (1, false, NORM), grid, dim3(1024), 0, s, a);
 }
 
 static bool swiglu_wide_env() {
@@ -1105,9 +1105,9 @@ static void launch_swiglu_mc(const uint8_t *Wg, const uint8_t *Wu, const uint8_t
                              bool f16h, uint8_t *Q, int M, int N, int K, hipStream_t s) {
   const dim3 grid(N / 32, (M + MC - 1) / MC);
   if (f16h)
-    hipLaunchKernelGGL((k_gemv_swiglu<QT, MC, true>), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
+    IFX_LAUNCH(k_gemv_swiglu, (QT, MC, true), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
   else
-    hipLaunchKernelGGL((k_gemv_swiglu<QT, MC, false>), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
+    IFX_LAUNCH(k_gemv_swiglu, (QT, MC, false), grid, dim3(1024), 0, s, Wg, Wu, A, H, Q, M, N, K);
 }
 
 template <int QT>
@@ -1126,7 +1126,7 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   if (qtype == kTypeQ4_K && K <= kSwigluWideMaxK && M <= IFX_SWIGLU_MAX_M && swiglu_wide_env()) {
     const SwigluArgs args{g, u, a, nullptr, nullptr, 0.0f, H, q, M, N, K};
     launch_swiglu_wide<0>(args, f16h, stream);
-    return hipGetLastError();
+    return last_error();
   }
   switch (qtype) {
   case kTypeQ4_K: launch_swiglu_t<kTypeQ4_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
@@ -1136,7 +1136,7 @@ hipError_t launch_gemv_swiglu(int qtype, const void *Wg, const void *Wu, const v
   case kTypeQ8_K: launch_swiglu_t<kTypeQ8_K>(g, u, a, H, f16h, q, M, N, K, stream); break;
   default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 // The wide Q4_K kernel with the RMSNorm + Q8_1 producer fused in (checked by
@@ -1149,7 +1149,7 @@ hipError_t launch_gemv_swiglu_rmsnorm(const void *Wg, const void *Wu, const void
                         nullptr, x, norm_w, eps, H, static_cast<uint8_t *>(Q), M, N, K};
   if (x_f16) launch_swiglu_wide<2>(args, f16h, stream);
   else launch_swiglu_wide<1>(args, f16h, stream);
-  return hipGetLastError();
+  return last_error();
 }
 
 // Geometry is validated by the caller: K % 256 == 0 for Q4_K/Q6_K,
@@ -1218,7 +1218,7 @@ hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, 
     default: launch_norm_r<2, 4>(args, f16, stream); break;
     }
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

@@ -397,9 +397,9 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
   const dim3 grid(groups, ks), block(64 * kWaves);
   if (f16) {
-    hipLaunchKernelGGL((k_gemv_dq<QT, true, false>), grid, block, shm, s, args);
+    IFX_LAUNCH(k_gemv_dq, (QT, true, false), grid, block, shm, s, args);
   } else if (ks == 1) {
-    hipLaunchKernelGGL((k_gemv_dq<QT, false, false>), grid, block, shm, s, args);
+    IFX_LAUNCH(k_gemv_dq, (QT, false, false), grid, block, shm, s, args);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -407,11 +407,11 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
         f.y[i] = static_cast<float *>(args.seg[i].Y);
         f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
       }
-      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return hipGetLastError();
+      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return last_error();
     }
-    hipLaunchKernelGGL((k_gemv_dq<QT, false, true>), grid, block, shm, s, args);
+    IFX_LAUNCH(k_gemv_dq, (QT, false, true), grid, block, shm, s, args);
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace

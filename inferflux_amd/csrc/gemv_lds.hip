@@ -213,7 +213,7 @@ void launch_lds_p(LdsArgs args, hipStream_t s) {
     blocks += (args.seg[i].N + rows_per_wg - 1) / rows_per_wg;
   }
   const int lds = args.M * ((args.K >> 6) * kLdsSlicePitch + (args.K >> 5) * 4);
-  hipLaunchKernelGGL((k_gemv_lds<MC, R, H, P, F16>), dim3(blocks), dim3(64 * P), lds, s, args);
+  IFX_LAUNCH(k_gemv_lds, (MC, R, H, P, F16), dim3(blocks), dim3(64 * P), lds, s, args);
 }
 
 // Waves per workgroup: 8 (one activation copy per 32 rows at H = 2) unless
@@ -261,7 +261,7 @@ hipError_t launch_gemv_lds(int count, const void *const *W, void *const *Y, cons
     if (f16) launch_lds_m<8, true>(args, stream);
     else launch_lds_m<8, false>(args, stream);
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

@@ -408,7 +408,7 @@ void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
 template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC>
 void slot_launch(const SlotArgs &args, int blocks, int ks, hipStream_t s) {
   constexpr int lds = slot_lds_bytes<QT, MP, KW>();
-  hipLaunchKernelGGL((k_gemv_slot<QT, MP, KW, F16OUT, ATOMIC>), dim3(blocks, ks), dim3(64 * KW), lds,
+  IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC), dim3(blocks, ks), dim3(64 * KW), lds,
                      s, args);
 }
 
@@ -477,7 +477,7 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
   args.mode = mode;
   if (qtype == kTypeQ4_K) slot_q<kTypeQ4_K>(args, blocks, f16, stream);
   else slot_q<kTypeQ6_K>(args, blocks, f16, stream);
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

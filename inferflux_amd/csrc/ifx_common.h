@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 // Largest batch of the fused gate/up/SiLU kernel on wide Q4_K slices (one
 // workgroup per batch column).  Measured at 11008 x 2048: from M = 3 on it
 // loses to grouped GEMV + SiLU producer (M = 3 / 4 / 8: 12.6 / 14.5 / 23.0 us
@@ -24,6 +26,28 @@
 #endif
 
 namespace ifx {
+
+// Launch log: every kernel launch goes through IFX_LAUNCH, which records the
+// instance name ("k_gemv<12,1,2,1,4,0,2>": the kernel's template arguments as
+// integers) while a log is open on the calling thread, and skips the launch
+// itself in dry-run mode (ifx_launch_log_begin, include/ifx_qgemm.h), so the
+// dispatch can be inspected on a host without a GPU.
+bool note_launch(const char *kernel, std::initializer_list<int> targs);
+bool dry_run();
+// hipGetLastError / hipPeekAtLastError, or hipSuccess in dry-run mode.
+hipError_t last_error();
+hipError_t peek_error();
+
+#define IFX_UNPAREN(...) __VA_ARGS__
+#define IFX_LAUNCH(K, TARGS, ...)                                        \
+  do {                                                                   \
+    if (::ifx::note_launch(#K, {IFX_UNPAREN TARGS}))                     \
+      hipLaunchKernelGGL((K<IFX_UNPAREN TARGS>), __VA_ARGS__);           \
+  } while (0)
+#define IFX_LAUNCH0(K, ...)                                              \
+  do {                                                                   \
+    if (::ifx::note_launch(#K, {})) hipLaunchKernelGGL(K, __VA_ARGS__);  \
+  } while (0)
 
 constexpr int kTypeQ8_0 = 8;
 constexpr int kTypeQ8_1 = 9;

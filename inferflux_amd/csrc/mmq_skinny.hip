@@ -204,9 +204,9 @@ hipError_t launch_fill_zero(const FillArgs &f, int nseg, hipStream_t s) {
   int64_t nmax = 0;
   for (int i = 0; i < nseg; ++i) nmax = max(nmax, f.n[i]);
   if (nmax == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_fill_zero, dim3(static_cast<unsigned>((nmax + 1023) / 1024), nseg),
+  IFX_LAUNCH0(k_fill_zero, dim3(static_cast<unsigned>((nmax + 1023) / 1024), nseg),
                      dim3(256), 0, s, f);
-  return hipPeekAtLastError();  // left set for the caller's hipGetLastError
+  return peek_error();  // left set for the caller's hipGetLastError
 }
 
 // grid: x = row groups of 64 (all projections), y = super-block splits.
@@ -439,9 +439,9 @@ hipError_t launch_mt(SkArgs args, bool f16, hipStream_t s) {
   ks = (nsb + args.sb_per - 1) / args.sb_per;
   const dim3 grid(groups, ks);
   if (f16) {
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, true, false>), grid, dim3(64 * kWaves), shm, s, args);
+    IFX_LAUNCH(k_mmq_skinny, (QT, MT, true, false), grid, dim3(64 * kWaves), shm, s, args);
   } else if (ks == 1) {
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, false>), grid, dim3(64 * kWaves), shm, s, args);
+    IFX_LAUNCH(k_mmq_skinny, (QT, MT, false, false), grid, dim3(64 * kWaves), shm, s, args);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -449,11 +449,11 @@ hipError_t launch_mt(SkArgs args, bool f16, hipStream_t s) {
         f.y[i] = static_cast<float *>(args.seg[i].Y);
         f.n[i] = static_cast<int64_t>(args.M) * args.seg[i].N;
       }
-      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return hipGetLastError();
+      if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return last_error();
     }
-    hipLaunchKernelGGL((k_mmq_skinny<QT, MT, false, true>), grid, dim3(64 * kWaves), shm, s, args);
+    IFX_LAUNCH(k_mmq_skinny, (QT, MT, false, true), grid, dim3(64 * kWaves), shm, s, args);
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace

@@ -477,13 +477,15 @@ template <int QT, int MT, int KW, bool F16OUT>
 void launch_one(const MmvqArgs &args, int blocks, hipStream_t s) {
   constexpr int lds = mmvq_lds_bytes<QT, MT, KW>();
   if constexpr (lds > 65536) {
-    // once per instantiation: allow the dynamic LDS above 64 KB
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&k_mmvq<QT, MT, KW, F16OUT>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    (void)attr;
+    if (!dry_run()) {
+      // once per instantiation: allow the dynamic LDS above 64 KB
+      static const hipError_t attr = hipFuncSetAttribute(
+          reinterpret_cast<const void *>(&k_mmvq<QT, MT, KW, F16OUT>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      (void)attr;
+    }
   }
-  hipLaunchKernelGGL((k_mmvq<QT, MT, KW, F16OUT>), dim3(blocks), dim3(64 * KW), lds, s, args);
+  IFX_LAUNCH(k_mmvq, (QT, MT, KW, F16OUT), dim3(blocks), dim3(64 * KW), lds, s, args);
 }
 
 template <int QT, int MT, int KW>
@@ -536,7 +538,7 @@ hipError_t launch_mmvq(int qtype, int count, const void *const *W, void *const *
   case kTypeQ8_0: launch_q<kTypeQ8_0>(args, f16, stream); break;
   default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

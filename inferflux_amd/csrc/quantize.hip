@@ -97,12 +97,12 @@ hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t 
                                         int M, int K, float eps, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   if (f16)
-    hipLaunchKernelGGL(k_rmsnorm_quantize_q8_1<true>, dim3(M), dim3(256), 0, stream, x, w,
+    IFX_LAUNCH(k_rmsnorm_quantize_q8_1, (true), dim3(M), dim3(256), 0, stream, x, w,
                        static_cast<uint8_t *>(out), K, eps);
   else
-    hipLaunchKernelGGL(k_rmsnorm_quantize_q8_1<false>, dim3(M), dim3(256), 0, stream, x, w,
+    IFX_LAUNCH(k_rmsnorm_quantize_q8_1, (false), dim3(M), dim3(256), 0, stream, x, w,
                        static_cast<uint8_t *>(out), K, eps);
-  return hipGetLastError();
+  return last_error();
 }
 
 hipError_t launch_silu_mul_quantize_q8_1(const void *g, const void *u, bool f16, void *out,
@@ -111,12 +111,12 @@ hipError_t launch_silu_mul_quantize_q8_1(const void *g, const void *u, bool f16,
   if (nblocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((nblocks * 8 + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL(k_silu_mul_quantize_q8_1<true>, grid, dim3(256), 0, stream, g, u,
+    IFX_LAUNCH(k_silu_mul_quantize_q8_1, (true), grid, dim3(256), 0, stream, g, u,
                        static_cast<uint8_t *>(out), nblocks);
   else
-    hipLaunchKernelGGL(k_silu_mul_quantize_q8_1<false>, grid, dim3(256), 0, stream, g, u,
+    IFX_LAUNCH(k_silu_mul_quantize_q8_1, (false), grid, dim3(256), 0, stream, g, u,
                        static_cast<uint8_t *>(out), nblocks);
-  return hipGetLastError();
+  return last_error();
 }
 
 hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, int64_t K,
@@ -126,12 +126,12 @@ hipError_t launch_quantize_q8_1(const void *x, bool f16, void *out, int64_t M, i
   const int64_t threads = nblocks * 8;
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (f16)
-    hipLaunchKernelGGL(k_quantize_q8_1_f16, grid, dim3(256), 0, stream,
+    IFX_LAUNCH0(k_quantize_q8_1_f16, grid, dim3(256), 0, stream,
                        static_cast<const uint16_t *>(x), static_cast<uint8_t *>(out), nblocks);
   else
-    hipLaunchKernelGGL(k_quantize_q8_1_f32, grid, dim3(256), 0, stream,
+    IFX_LAUNCH0(k_quantize_q8_1_f32, grid, dim3(256), 0, stream,
                        static_cast<const float *>(x), static_cast<uint8_t *>(out), nblocks);
-  return hipGetLastError();
+  return last_error();
 }
 
 }  // namespace ifx

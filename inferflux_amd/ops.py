@@ -301,3 +301,25 @@ def supports(qtype, M, N, K):
 def kernel_family(qtype, M, N, K):
     """Kernel family ifx_qgemv runs the shape on (include/ifx_qgemm.h)."""
     return int(_lib.load().ifx_kernel_family(qtype, M, N, K))
+
+
+class launch_log:
+    """Records the kernel instances the entry points called inside the
+    `with` block launch on this thread (ifx_launch_log_begin/_end,
+    include/ifx_qgemm.h).  dry=True launches nothing: no HIP call is made, so
+    the dispatch of any shape can be read on a host without a GPU (use fake
+    non-null pointers then).  After the block, `.kernels` is the list of
+    instance names, e.g. ["k_gemv<12,1,2,1,4,0,2>"]."""
+
+    def __init__(self, dry=False):
+        self.dry = dry
+        self.kernels = []
+
+    def __enter__(self):
+        _lib.load().ifx_launch_log_begin(1 if self.dry else 0)
+        return self
+
+    def __exit__(self, *exc):
+        text = _lib.load().ifx_launch_log_end().decode()
+        self.kernels = text.split(";") if text else []
+        return False

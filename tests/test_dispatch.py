@@ -1,0 +1,72 @@
+"""Dispatch routing on the CPU: every launch the benchmark times goes to the
+kernel instance tests/launch_table.py names.  The C ABI runs in dry-run mode
+(ifx_launch_log_begin(1)): it validates, picks and records the kernel, and
+makes no HIP call, so fake non-null pointers stand in for device memory."""
+import ctypes
+
+import pytest
+
+from tests.launch_table import IDS, LAUNCHES
+
+_P = ctypes.c_void_p
+
+
+def _fake(i):
+    return _P(0x100000 * (i + 1))
+
+
+def dry_dispatch(entry, qt, M, Ns, K):
+    """Calls the entry point of `entry` in dry-run mode; returns (status,
+    kernel instance names)."""
+    from inferflux_amd import _lib, ops
+    L = _lib.load()
+    n = len(Ns)
+    W = (_P * n)(*[_fake(i) for i in range(n)])
+    Y = (_P * n)(*[_fake(4 + i) for i in range(n)])
+    NN = (ctypes.c_int * n)(*Ns)
+    A, X, NW, B = _fake(8), _fake(9), _fake(10), _fake(11)
+    with ops.launch_log(dry=True) as lg:
+        if entry in ("gemv", "gemv_accum"):
+            rc = L.ifx_qgemv(qt, W[0], A, Y[0], ops.OUT_F32,
+                             ops.ACCUM if entry == "gemv_accum" else ops.STORE, None, M, Ns[0], K,
+                             None)
+        elif entry == "grouped":
+            rc = L.ifx_qgemv_grouped(qt, n, W, Y, NN, A, ops.OUT_F32, ops.STORE, M, K, None)
+        elif entry in ("grouped_rmsnorm", "quantize_accum"):
+            norm = NW if entry == "grouped_rmsnorm" else None
+            mode = ops.STORE if entry == "grouped_rmsnorm" else ops.ACCUM
+            rc = L.ifx_qgemv_grouped_rmsnorm(qt, n, W, Y, NN, X, ops.OUT_F32, norm, 1e-6,
+                                             ops.OUT_F32, mode, M, K, None)
+        elif entry == "gate_up_silu_rmsnorm":
+            rc = L.ifx_qgemv_gate_up_silu_rmsnorm(qt, W[0], _fake(1), X, ops.OUT_F32, NW, 1e-6,
+                                                  None, ops.OUT_F32, B, M, Ns[0], K, None)
+        elif entry == "prefill":
+            rc = L.ifx_qgemm_prefill(qt, W[0], A, Y[0], ops.OUT_F32, ops.STORE, None, M, Ns[0], K,
+                                     None)
+        elif entry == "prefill_int8":
+            rc = L.ifx_qgemm_prefill_kernel(qt, W[0], A, Y[0], ops.OUT_F32, ops.STORE, None, M,
+                                            Ns[0], K, ops.PREFILL_INT8, 0, None)
+        else:
+            raise ValueError(entry)
+    return rc, lg.kernels
+
+
+@pytest.mark.parametrize("lid,entry,qt,M,Ns,K,want", LAUNCHES, ids=IDS)
+def test_bench_launch_routing(lid, entry, qt, M, Ns, K, want):
+    rc, kernels = dry_dispatch(entry, qt, M, Ns, K)
+    assert rc == 0
+    assert kernels == want
+
+
+def test_dry_run_launches_nothing_and_log_closes():
+    """Validation still runs in dry-run mode (a bad geometry launches and
+    records nothing), and a closed log records nothing further."""
+    from inferflux_amd import _lib, ops
+    L = _lib.load()
+    with ops.launch_log(dry=True) as lg:
+        rc = L.ifx_qgemv(ops.Q4_K, _fake(0), _fake(1), _fake(2), ops.OUT_F32, ops.STORE, None,
+                         1, 64, 300, None)  # K % 256 != 0
+    assert rc == 2 and lg.kernels == []  # IFX_BAD_GEOMETRY
+    rc, kernels = dry_dispatch("gemv", ops.Q4_K, 1, (64,), 256)
+    assert rc == 0 and len(kernels) == 1
+    assert L.ifx_launch_log_end().decode() == ""

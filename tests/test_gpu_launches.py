@@ -1,0 +1,107 @@
+"""Every launch the benchmark times, run on the GPU at its production shape
+(tests/launch_table.py): the launch log must show the kernel instance the
+table names, and the outputs must pass the oracle bar (1e-3 * ||y_row||_2
+against the fp64 oracle) on sampled weight rows.  The fused-producer
+launches are also compared bit for bit with the producer + GEMV chain they
+replace."""
+import numpy as np
+import pytest
+
+from tests.launch_table import IDS, LAUNCHES
+from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, up
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _rows(N, seed, n=256):
+    return np.unique(np.concatenate([[0, N - 1], np.random.default_rng(seed).choice(N, n)]))
+
+
+@pytest.mark.parametrize("lid,entry,qt,M,Ns,K,want", LAUNCHES, ids=IDS)
+def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"launch {lid}: {entry} type={qt} M={M} N={Ns} K={K} -> {want}")
+    seed = sum(Ns) + K + M
+    ws = [synth.blocks(qt, n, K, seed=seed + i) for i, n in enumerate(Ns)]
+    W = [up(w, dev) for w in ws]
+    rng = np.random.default_rng(seed)
+    outl = 0.01 if entry.startswith("prefill") else 0.0
+    x = synth.activations(M, K, seed=seed + 7, outlier_frac=outl)
+    base = rng.standard_normal((M, max(Ns))).astype(np.float32)
+
+    if entry in ("grouped_rmsnorm", "gate_up_silu_rmsnorm"):
+        nw = rng.uniform(0.5, 1.5, K).astype(np.float16)
+        X, NW = up(x, dev), up(nw, dev)
+        A = ops.rmsnorm_quantize_q8_1(X, NW, eps=1e-6)  # the standalone producer
+        a = down(A)
+        check_q8_1_close(a, orc.rmsnorm_quantize_q8_1(x, nw, 1e-6), orc.rmsnorm_values(x, nw, 1e-6))
+    else:
+        a = orc.quantize_q8_1(x)
+        A = up(a, dev)
+        X = up(x, dev)
+
+    with ops.launch_log() as lg:
+        if entry == "gemv":
+            outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K)]
+        elif entry in ("gemv_accum", "quantize_accum"):
+            y0 = up(base[:, :Ns[0]], dev)
+            if entry == "gemv_accum":
+                ops.qgemv(qt, W[0], A, M, Ns[0], K, out=y0, mode=ops.ACCUM)
+            else:
+                ops.qgemv_grouped_rmsnorm(qt, W, X, None, M, list(Ns), K, outs=[y0],
+                                          mode=ops.ACCUM)
+            outs = [y0]
+        elif entry == "grouped":
+            outs = ops.qgemv_grouped(qt, W, A, M, list(Ns), K)
+        elif entry == "grouped_rmsnorm":
+            outs = ops.qgemv_grouped_rmsnorm(qt, W, X, NW, M, list(Ns), K, eps=1e-6)
+        elif entry == "gate_up_silu_rmsnorm":
+            wu = synth.blocks(qt, Ns[0], K, seed=seed + 11)
+            h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], up(wu, dev), X, NW, M, Ns[0], K,
+                                                  eps=1e-6)
+        elif entry == "prefill":
+            outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, prefill=True)]
+        elif entry == "prefill_int8":
+            outs = [ops.qgemm_prefill_kernel(qt, W[0], A, M, Ns[0], K, ops.PREFILL_INT8)]
+        else:
+            raise ValueError(entry)
+        torch.cuda.synchronize()
+    assert lg.kernels == want
+
+    if entry == "gate_up_silu_rmsnorm":
+        N = Ns[0]
+        blocks = np.random.default_rng(seed).choice(N // 32, 16, replace=False)
+        idx = (blocks[:, None] * 32 + np.arange(32)[None, :]).ravel()
+        g = orc.gemv_exact(qt, ws[0][idx], a, M, len(idx), K)
+        u = orc.gemv_exact(qt, wu[idx], a, M, len(idx), K)
+        h_ref = g / (1.0 + np.exp(-g)) * u
+        check_rows(down(h)[:, idx], h_ref)
+        qb = down(q).reshape(M, N // 32, 36)[:, blocks].reshape(M, -1)
+        check_q8_1_close(qb, orc.quantize_q8_1(h_ref.astype(np.float32)), h_ref)
+        # the chain it replaces: grouped GEMV + SiLU producer, bit for bit
+        g2, u2 = ops.qgemv_grouped(qt, [W[0], up(wu, dev)], A, M, [N, N], K)
+        assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
+        return
+
+    for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):
+        idx = _rows(n, seed + i)
+        ye = orc.gemv_exact(qt, w[idx], a, M, len(idx), K)
+        if entry in ("gemv_accum", "quantize_accum"):
+            ye = ye + base[:, idx]
+        yd = down(y)
+        assert np.isfinite(yd).all()
+        check_rows(yd[:, idx], ye)
+    if entry == "grouped_rmsnorm":
+        # bit for bit the standalone producer + grouped GEMV (same geometry)
+        ref = ops.qgemv_grouped(qt, W, A, M, list(Ns), K)
+        for y, yr in zip(outs, ref):
+            assert np.array_equal(down(y), down(yr))

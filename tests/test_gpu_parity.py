@@ -119,6 +119,7 @@ CASES.append((Q4_K, 3, 300, 5120))  # activations-in-LDS GEMV, full-wave rows
 CASES.append((Q4_K, 4, 16400, 2048))  # activations-in-LDS GEMV, M = 4 wide launch
 CASES.append((Q4_K, 2, 8200, 5120))  # quarter-wave rows, two columns
 CASES.append((Q4_K, 1, 100, 3072))   # quarter-wave rows, 3 slices per lane
+CASES += [(Q6_K, 1, 301, 11008), (Q4_K, 1, 77, 11008)]  # wide slices, 3 waves per row group
 # slot-packed MFMA GEMV (5 <= M <= 16): 8- and 16-row slots, ragged N, one
 # super-block per row, a single row
 CASES += [(Q4_K, 6, 33, 256), (Q6_K, 7, 64, 512), (Q4_K, 12, 1000, 2048),
@@ -391,9 +392,36 @@ def _sampled(orc, dev, qtype, M, N, K, seed, outl=0.0, rows=256):
 
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0])
 def test_gemm_large_tiles(orc, dev, qtype):
-    """A grid of >= 512 128x128 tiles takes the large-tile GEMM (the small
-    parity cases above all run 64x64 tiles); ragged M and N edges."""
-    _sampled(orc, dev, qtype, 1000, 8190, 512, seed=21, outl=0.01, rows=128)
+    """The int8 MFMA GEMM on a grid of >= 512 tiles of 128 x 128 (M = 1000,
+    N = 8190: 8 x 64 tiles), which takes its large-tile instance
+    k_gemm_mfma<QT, 2> (the small parity cases above run 64 x 64 tiles);
+    ragged M and N edges; store, accumulate, bias and fp16 outputs."""
+    import torch
+    from inferflux_amd import ops, synth
+    M, N, K = 1000, 8190, 512
+    note(f"gemm int8 large tiles type={qtype} M={M} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=21)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=22, outlier_frac=0.01))
+    W, A = up(w, dev), up(a, dev)
+    idx = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(21).choice(N, 128)]))
+    ye = orc.gemv_exact(qtype, w[idx], a, M, len(idx), K)
+    rng = np.random.default_rng(23)
+    base = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    kern = ops.PREFILL_INT8
+    with ops.launch_log() as lg:
+        y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern,
+                                     out=torch.full((M, N), 7.0, device=dev))
+    assert lg.kernels == [f"k_gemm_mfma<{qtype},2,0>"]
+    check_rows(down(y)[:, idx], ye)
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, out=up(base, dev), mode=ops.ACCUM)
+    check_rows(down(y)[:, idx], ye + base[:, idx])
+    y = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, mode=ops.BIAS, bias=up(bias, dev))
+    check_rows(down(y)[:, idx], ye + bias[None, idx])
+    with ops.launch_log() as lg:
+        y16 = ops.qgemm_prefill_kernel(qtype, W, A, M, N, K, kern, out_dtype=torch.float16)
+    assert lg.kernels == [f"k_gemm_mfma<{qtype},2,1>"]
+    check_rows(down(y16)[:, idx].astype(np.float64), ye, tol=2e-3)
 
 
 @pytest.mark.parametrize("M", [1, 8])
@@ -702,7 +730,9 @@ def test_gate_up_silu_matches_two_launch_chain(orc, dev, M, N, K):
     wu = up(synth.blocks(Q4_K, N, K, seed=N + 6), dev)
     rng = np.random.default_rng(K + M)
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev)
-    nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float16)).to(dev)
+    # norm weights small enough that h = silu(g) * u stays inside the fp16
+    # range, so the fp16 comparison below compares finite values
+    nw = torch.from_numpy(rng.uniform(0.05, 0.15, K).astype(np.float16)).to(dev)
     a = ops.rmsnorm_quantize_q8_1(x, nw)
     g, u = ops.qgemv_grouped(Q4_K, [wg, wu], a, M, [N, N], K)
     q_chain = down(ops.silu_mul_quantize_q8_1(g, u))
@@ -720,6 +750,7 @@ def test_gate_up_silu_matches_two_launch_chain(orc, dev, M, N, K):
     h16, none = ops.qgemv_gate_up_silu_rmsnorm(Q4_K, wg, wu, x, nw, M, N, K, want_q8_1=False,
                                                h_dtype=torch.float16)
     assert none is None
+    assert np.isfinite(down(h16)).all()
     assert np.array_equal(down(h16), down(h).astype(np.float16))
 
 
