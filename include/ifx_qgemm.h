@@ -43,7 +43,9 @@ enum ifx_status {
   IFX_UNSUPPORTED_TYPE = 1, /* quant type has no kernel              */
   IFX_BAD_GEOMETRY = 2,     /* M, N or K out of range / not a multiple */
   IFX_NULL_POINTER = 3,     /* a required pointer is NULL            */
-  IFX_DISABLED = 4          /* policy disabled the fused path (C++ wrapper) */
+  IFX_DISABLED = 4,         /* policy disabled the fused path (C++ wrapper) */
+  IFX_SCRATCH_LIMIT = 5     /* the shape needs more than the library's static
+                               scratch (ifx_qgemm_prefill_noalloc)      */
 };
 
 enum ifx_out_dtype { IFX_OUT_F32 = 0, IFX_OUT_F16 = 1 };
@@ -181,6 +183,27 @@ int64_t ifx_qgemm_prefill_workspace_bytes(int quant_type, int M, int N, int K);
 int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void *Y,
                          int out_dtype, int mode, const void *bias, int M, int N, int K,
                          void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Size of the library's static device scratch (per GPU, held until the
+ * process ends) that ifx_qgemm_prefill_noalloc uses as its workspace. */
+#define IFX_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/* ifx_qgemm_prefill_ws with the library's static scratch as the workspace:
+ * allocates nothing (no hipMalloc, no allocating library call), so callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it) get the workspace path.  No counterpart in the
+ * reference.  Bit-identical to ifx_qgemm_prefill_ws with a caller workspace.
+ * A shape whose workspace (ifx_qgemm_prefill_workspace_bytes) exceeds
+ * IFX_NOALLOC_SCRATCH_BYTES returns IFX_SCRATCH_LIMIT and launches nothing;
+ * a shape that needs no workspace runs exactly ifx_qgemm_prefill.  Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (concurrent streams, or threads) race and must be serialized by the
+ * caller.  The scratch needs no clearing (each call writes all of the part
+ * it reads first).  The first call on a device resolves the scratch's
+ * address there (hipGetSymbolAddress). */
+int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                              int out_dtype, int mode, const void *bias, int M, int N, int K,
+                              void *stream);
 
 /* The prefill GEMM with an explicit kernel: IFX_PREFILL_INT8 is the
  * integer-exact int8 MFMA GEMM (the MMQ per-block arithmetic of

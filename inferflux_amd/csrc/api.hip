@@ -58,6 +58,7 @@ bool gemv_dq_fits_f16(int M, int K);
 hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
                           int mode, int splits_req, hipStream_t stream);
+hipError_t scratch_address(void **out);
 bool gemv_slot_fits(int qtype, int M, int K);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
@@ -262,6 +263,7 @@ const char *ifx_status_string(int status) {
   case IFX_BAD_GEOMETRY: return "bad geometry or argument";
   case IFX_NULL_POINTER: return "null pointer";
   case IFX_DISABLED: return "fused path disabled by policy";
+  case IFX_SCRATCH_LIMIT: return "shape exceeds the static scratch of the no-alloc entry";
   default: return status < 0 ? hipGetErrorString(static_cast<hipError_t>(-status)) : "unknown";
   }
 }
@@ -505,6 +507,26 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
   if (workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
     return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, workspace, Y, bias,
+                                        out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                              int out_dtype, int mode, const void *bias, int M, int N, int K,
+                              void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
+  if (need == 0)
+    return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
+  if (need > IFX_NOALLOC_SCRATCH_BYTES) return IFX_SCRATCH_LIMIT;
+  void *ws = reinterpret_cast<void *>(uintptr_t{256});  // dry run: never dereferenced
+  if (!ifx::dry_run()) {
+    const hipError_t e = ifx::scratch_address(&ws);
+    if (e != hipSuccess) return status_of(e);
+  }
+  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, ws, Y, bias,
                                         out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
                                         static_cast<hipStream_t>(stream)));
 }

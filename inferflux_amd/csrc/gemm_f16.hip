@@ -44,7 +44,10 @@
 // MFMA lane layouts (32x32x16 f16): lane l supplies row (l % 32) of A and
 // column (l % 32) of B, with 8 K values for K half l / 32; it receives
 // column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4), i = 0..15.
+#include "../../include/ifx_qgemm.h"
 #include "ifx_common.h"
+
+#include <mutex>
 
 namespace ifx {
 
@@ -537,6 +540,40 @@ hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *A16, v
   case kTypeQ8_0: return launch_qt<kTypeQ8_0>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
   default: return hipErrorInvalidValue;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Static workspace of the no-alloc prefill entry (ifx_qgemm_prefill_noalloc):
+// the fp16 activation copy lives in this array instead of caller memory.
+// Each GPU holds its own copy, at its own address, until the process ends.
+// On the host `scratch` names a host-side stand-in, never a device address:
+// host code uses only the address hipGetSymbolAddress returns for the
+// current device.
+static __device__ __align__(256) uint8_t scratch[IFX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // per device, resolved on first use
+}  // namespace
+
+// Device address of `scratch` on the current device, resolved once per
+// device with that device current.
+hipError_t scratch_address(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 }  // namespace ifx

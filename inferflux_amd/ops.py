@@ -152,6 +152,27 @@ def qgemm_prefill_ws(qtype, W, A, M, N, K, workspace, out=None, out_dtype=torch.
     return out
 
 
+def qgemm_prefill_noalloc(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE,
+                          bias=None, stream=None):
+    """qgemm_prefill_ws with the library's static device scratch as the
+    workspace (ifx_qgemm_prefill_noalloc): the call allocates nothing (pass
+    `out` to keep this wrapper from allocating too).  Calls that overlap on
+    one GPU race on the scratch."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, N, K) or A.numel() < M * (K // 32) * 36 or out.numel() < M * N:
+        raise ValueError("W, A or out is smaller than the shape")
+    bptr = _dev(bias, "bias") if bias is not None else None
+    rc = _lib.load().ifx_qgemm_prefill_noalloc(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"),
+                                               od, mode, bptr, M, N, K, _stream(stream))
+    _check(rc, "ifx_qgemm_prefill_noalloc")
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # IFX_NOALLOC_SCRATCH_BYTES
+
+
 PREFILL_INT8, PREFILL_F16, DECODE_DQ_F16 = 1, 2, 3
 
 
