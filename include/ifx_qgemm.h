@@ -184,6 +184,44 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
                          int out_dtype, int mode, const void *bias, int M, int N, int K,
                          void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Bytes of workspace ifx_decode_ffn needs: a 2048-byte control block, then
+ * 8 copies of h = silu(gate) * up in fp32 (M x ffn values, each copy padded
+ * to a multiple of 256 bytes). */
+int64_t ifx_decode_ffn_workspace_bytes(int M, int ffn);
+
+/* The post-attention half of a decode layer at M = 1 in two launches:
+ *   residual += W_o . Q8_1(attn)                      (O, accumulate)
+ *   a = Q8_1(RMSNorm(residual) * ffn_norm_weight)
+ *   h = silu(W_gate . a) * (W_up . a), as Q8_1 blocks in the workspace
+ *   residual += W_down . h                            (down, accumulate)
+ * Replaces the launch sequence of transformer_forward.cu:726-817
+ * (GemvQ8_1AccumF32 for O, FusedRmsNormQuantizeQ8_1,
+ * FusedGateUpSiluGemvQ8_1WithEpilogue, GemvQ8_1AccumF32 for down), and
+ * leaves the residual bit for bit equal to that chain's (here:
+ * ifx_qgemv_grouped_rmsnorm with norm_weight NULL in IFX_ACCUM mode,
+ * ifx_qgemv_gate_up_silu_rmsnorm, ifx_qgemv in IFX_ACCUM mode).
+ * Types: W_o, W_gate, W_up Q4_K, W_down Q6_K (the Q4_K_M mix); attn [q_dim]
+ * fp32 or fp16 (attn_dtype IFX_OUT_F32 / IFX_OUT_F16); residual [hidden]
+ * fp32; norm weight [hidden] fp16.  Covered shapes: M = 1, q_dim and hidden
+ * multiples of 256 up to 2048, ffn a multiple of 256 up to 16384, and the
+ * down rows of a workgroup within 12 waves (Qwen2.5-3B: 2048 / 11008 on 256
+ * CUs); other shapes return IFX_BAD_GEOMETRY (use the chain).
+ * The first launch is O (the GEMV with the fused quantizer); the second
+ * does everything after it, one workgroup per compute unit, all resident
+ * together, with one grid barrier in the workspace (256-byte aligned, at least
+ * ifx_decode_ffn_workspace_bytes).  Its control block (bytes 0..2047) must
+ * be zero before the first call; the kernel leaves it ready for the next
+ * call.  Bytes 16..23 may hold an int64 wait limit in 100 MHz ticks (0: one
+ * second).  A barrier that waits longer records a failure: the uint32 at
+ * byte 8 becomes nonzero, the results are not valid, and the control block
+ * must be zeroed again before the next call.  Calls sharing a workspace
+ * must not overlap. */
+int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype, int q_dim,
+                   float *residual, const uint16_t *ffn_norm_weight, float eps, int gate_up_type,
+                   const void *W_gate, const void *W_up, int ffn, int down_type,
+                   const void *W_down, int M, int hidden, void *workspace,
+                   int64_t workspace_bytes, void *stream);
+
 /* Size of the library's static device scratch (per GPU, held until the
  * process ends) that ifx_qgemm_prefill_noalloc uses as its workspace. */
 #define IFX_NOALLOC_SCRATCH_BYTES (16 << 20)

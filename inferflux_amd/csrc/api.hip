@@ -59,6 +59,11 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
                           int mode, int splits_req, hipStream_t stream);
 hipError_t scratch_address(void **out);
+bool decode_ffn_fits(int hidden, int ffn);
+hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, float *resid,
+                             const uint16_t *norm_w, float eps, const void *Wg, const void *Wu,
+                             const void *Wd, void *workspace, int q_dim, int hidden, int ffn,
+                             hipStream_t s);
 bool gemv_slot_fits(int qtype, int M, int K);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
@@ -529,6 +534,42 @@ int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1,
   return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, ws, Y, bias,
                                         out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
                                         static_cast<hipStream_t>(stream)));
+}
+
+int64_t ifx_decode_ffn_workspace_bytes(int M, int ffn) {
+  if (M <= 0 || ffn <= 0 || ffn % 32) return 0;
+  return 2048 + 8 * ((static_cast<int64_t>(M) * ffn * 4 + 255) / 256) * 256;
+}
+
+int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype, int q_dim,
+                   float *residual, const uint16_t *ffn_norm_weight, float eps, int gate_up_type,
+                   const void *W_gate, const void *W_up, int ffn, int down_type,
+                   const void *W_down, int M, int hidden, void *workspace,
+                   int64_t workspace_bytes, void *stream) {
+  if (!W_o || !attn || !residual || !ffn_norm_weight || !W_gate || !W_up || !W_down || !workspace)
+    return IFX_NULL_POINTER;
+  if (o_type != IFX_TYPE_Q4_K || gate_up_type != IFX_TYPE_Q4_K || down_type != IFX_TYPE_Q6_K)
+    return IFX_UNSUPPORTED_TYPE;
+  if (attn_dtype != IFX_OUT_F32 && attn_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (!(eps >= 0.0f) || M != 1) return IFX_BAD_GEOMETRY;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return IFX_BAD_GEOMETRY;
+  if (workspace_bytes < ifx_decode_ffn_workspace_bytes(M, ffn)) return IFX_BAD_GEOMETRY;
+  // the 32-bit range checks of the three GEMVs
+  int rc = check_gemm_args(o_type, W_o, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M, hidden,
+                           q_dim);
+  if (rc == IFX_OK)
+    rc = check_gemm_args(gate_up_type, W_gate, attn, residual, IFX_OUT_F32, IFX_STORE, nullptr, M,
+                         ffn, hidden);
+  if (rc == IFX_OK)
+    rc = check_gemm_args(down_type, W_down, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M,
+                         hidden, ffn);
+  if (rc != IFX_OK) return rc;
+  // the O launch: the fused-quantizer GEMV's activation tile fits its LDS
+  if (q_dim % 256 || q_dim / 32 * ifx::kQ8_1Bytes > 65536) return IFX_BAD_GEOMETRY;
+  if (!ifx::decode_ffn_fits(hidden, ffn)) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_decode_ffn(W_o, attn, attn_dtype == IFX_OUT_F16, residual,
+                                          ffn_norm_weight, eps, W_gate, W_up, W_down, workspace,
+                                          q_dim, hidden, ffn, static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,

@@ -15,7 +15,16 @@
 
 namespace ifx {
 
+// Stores of a word that other workgroups of the same launch read:
+// device-coherent (a relaxed device-scope atomic store), so no cache
+// write-back is needed before a grid barrier.
+__device__ __forceinline__ void store_dev(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 #pragma clang fp contract(off)
+// DEV: write the block with device-coherent stores (store_dev).
+template <bool DEV = false>
 __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, float x3,
                                                 uint8_t *blk, int l) {
   // max and the integer sum over the 8 lanes of the block: DPP moves
@@ -44,11 +53,13 @@ __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, fl
                           ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
                           ((static_cast<uint32_t>(q2) & 0xFFu) << 16) |
                           ((static_cast<uint32_t>(q3) & 0xFFu) << 24);
-  *reinterpret_cast<uint32_t *>(blk + 4 + 4 * l) = packed;
+  if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(blk + 4 + 4 * l), packed);
+  else *reinterpret_cast<uint32_t *>(blk + 4 + 4 * l) = packed;
   if (l == 0) {
     const float s = materialize_f32(d * static_cast<float>(sum));  // fp32 first, then fp16
     const uint32_t ds = f2h_bits(d) | (f2h_bits(s) << 16);
-    *reinterpret_cast<uint32_t *>(blk) = ds;
+    if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(blk), ds);
+    else *reinterpret_cast<uint32_t *>(blk) = ds;
   }
 }
 
@@ -108,15 +119,25 @@ __device__ __forceinline__ void rmsnorm_quantize_row(const void *x, int64_t base
 // thread's elements 4t + 1024j (j < NIT) of x and of the norm weight into
 // registers, rmsnorm_row_finish computes exactly what rmsnorm_quantize_row
 // computes from them.  Requires K <= 1024 * NIT.
-template <bool F16, int NIT>
+// DEV: x is fp32 written earlier in the same launch by other workgroups:
+// device-coherent loads (relaxed device-scope atomic loads).
+template <bool F16, int NIT, bool DEV = false>
 __device__ __forceinline__ void rmsnorm_row_load(const void *x, int64_t base, const uint16_t *w,
                                                  int K, int tid, f32x4 (&xr)[NIT],
                                                  u32x2 (&wr)[NIT]) {
+  static_assert(!(DEV && F16), "device-coherent loads of fp32 rows only");
 #pragma unroll
   for (int j = 0; j < NIT; ++j) {
     const int i = 4 * tid + 1024 * j;
     if (i < K) {
-      xr[j] = load4<F16>(x, base + i);
+      if constexpr (DEV) {
+        const float *xf = static_cast<const float *>(x) + base + i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xr[j][e] = __hip_atomic_load(xf + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        xr[j] = load4<F16>(x, base + i);
+      }
       if (w) wr[j] = ldg<u32x2>(w + i);  // w == nullptr: plain quantize, no norm weight
     }
   }
@@ -170,11 +191,14 @@ __device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const
   rmsnorm_row_apply<NIT>(xr, wr, orow, K, eps, part, tid);
 }
 
-// SiLU(g) * u of four values (the standalone producer's arithmetic).
+// SiLU(g) * u (the standalone producer's arithmetic), of one and of four values.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  return materialize_f32(g / (1.0f + expf(-g))) * u;
+}
 __device__ __forceinline__ f32x4 silu_mul4(f32x4 g, f32x4 u) {
   f32x4 h;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) h[i] = materialize_f32(g[i] / (1.0f + expf(-g[i]))) * u[i];
+  for (int i = 0; i < 4; ++i) h[i] = silu_mul1(g[i], u[i]);
   return h;
 }
 
