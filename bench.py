@@ -1,31 +1,37 @@
 """Benchmark of the quantized GEMV/GEMM path on one MI355X.
 
-Workload: one Qwen2.5-3B Q4_K_M decode layer through
-the quantized path, launched as the reference's forward pass launches it
-(inferflux_amd/workloads.py DECODE_LAUNCHES), as a chain over an fp32
-residual stream: fused RMSNorm+Q8_1 -> one grouped Q/K/V GEMV -> Q8_1 of
-the attention output -> O accumulated into the residual -> fused
-RMSNorm+Q8_1 -> one grouped gate/up GEMV -> fused SiLU*up+Q8_1 -> the Q6_K
-down projection accumulated into the residual.  A step is one such layer at M = 1 (the unified decode
-batch of the headline).  Weights rotate through replicas totalling >= 512
-MB so every step streams from HBM, not the 256 MB Infinity Cache.
+Workload: one Qwen2.5-3B Q4_K_M decode layer at M = 1
+(the unified decode batch of the headline) through the quantized path, as a
+chain over an fp32 residual stream: RMSNorm + Q8_1 -> grouped Q/K/V GEMV ->
+Q8_1 of the attention output -> O accumulated into the residual -> RMSNorm
++ Q8_1 -> grouped gate/up GEMV -> SiLU * up + Q8_1 -> the Q6_K down
+projection accumulated into the residual.  The layer is timed in four launch
+forms (as the reference launches it, inferflux_amd/workloads.py
+DECODE_LAUNCHES; with the Q8_1 producers fused into the GEMVs; with SiLU * up
+in the gate/up epilogue as well; with one grid-synchronised FFN launch), and
+a step is one layer in the fastest form (config.step names it).  Weights
+rotate through replicas totalling >= 512 MB so every step streams from HBM,
+not the 256 MB Infinity Cache.
 
-Headline `value`: HBM GB/s of the layer's Q4_K GEMVs at M = 1 (algorithmic
-bytes: weights + Q8_1 activations + fp32 outputs, each counted once, over
-the summed kernel time).  The JSON line also carries the roofline of the
-dominant kernel (the grouped gate/up Q4_K GEMV, 2 x 11008 x 2048), us per
-layer at M = 1/4/8, an HBM read probe at the same transfer size, the other
-configs (config 1 at M = 1/8, LM head, 14B layer at M = 16/32, 32B prefill
-GEMMs) and a CPU baseline timed on this host.
+Headline `value`: HBM GB/s of the timed step, i.e. the layer's algorithmic
+bytes (weights, activations and outputs, each counted once) over
+ms_per_step.  `roofline` is the step's longest launch timed alone, with the
+HBM traffic per launch read from the committed rocprofv3 counter summary of
+that kernel (profiles/).  The line also carries us per layer at M = 1/4/8,
+an HBM read probe at the dominant launch's byte count, the other configs
+(config 1 at M = 1/8, LM head, 14B layer at M = 16/32, 32B prefill GEMMs),
+per-phase wall times and a CPU baseline timed on this host.
 
-`python bench.py --profile` runs only the dominant kernel and the counter
-calibration kernels, for rocprofv3.
+`python bench.py --profile FORM:LAUNCH` runs one launch of a layer form and
+the counter calibration kernels, for rocprofv3.
 """
 import argparse
 import json
 import os
 import sys
 import time
+
+T_START = time.perf_counter()
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -34,11 +40,6 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 F16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA
 ROTATE_BYTES = 512 << 20
-# HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
-# (FETCH_SIZE, WRITE_SIZE), each scaled by what the counter reads for a copy
-# of exactly 64 MiB; the summary and commands are in
-# profiles/k_gemv_q4k_gate_up_2x11008x2048_m1.md.
-DOMINANT_TRAFFIC_BYTES = 25513160
 
 
 def parse():
@@ -49,9 +50,10 @@ def parse():
     p.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--profile", action="store_true",
-                   help="profiling run: only the dominant GEMV (eager launches), the HBM "
-                        "read probe and a copy of known size for counter calibration")
+    p.add_argument("--profile", default=None, metavar="FORM:LAUNCH",
+                   help="profiling run: eager launches of one launch of a 3B layer form "
+                        "(e.g. ffn_block:ffn, fused_norm_swiglu:gate_up), the HBM read probe "
+                        "at its byte count and a copy of known size for counter calibration")
     p.add_argument("--profile-kernels", action="store_true",
                    help="profiling run of the batch kernels: the 32B prefill GEMMs (fp16 and "
                         "int8 kernels, M = 512) and the 14B gate+up / down decode launches at "
@@ -79,9 +81,6 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.profile:
-        profile_run(args, dev)
-        return
     if args.profile_kernels:
         profile_kernels_run(args, dev)
         return
@@ -165,7 +164,12 @@ def main():
         (ifx_qgemv_grouped_rmsnorm; Q4_K, M <= 2): 1 producer + 4 GEMVs.
         fused == "swiglu": in addition gate/up computes SiLU(gate)*up and
         writes its Q8_1 blocks for down itself
-        (ifx_qgemv_gate_up_silu_rmsnorm): 4 launches, no producer."""
+        (ifx_qgemv_gate_up_silu_rmsnorm): 4 launches, no producer.
+        fused == "ffn": QKV with the fused RMSNorm, then ifx_decode_ffn: O
+        with the fused quantizer and one grid-synchronised launch for
+        RMSNorm, gate/up + SiLU and down (M = 1): 3 launches.
+        run(i, which) runs one launch kind alone ("qkv", "o", "gate_up",
+        "down", "producers"; "ffn": the FFN kernel of the "ffn" form alone)."""
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
         rng = np.random.default_rng(seed)
         resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
@@ -181,6 +185,9 @@ def main():
         Y["o"] = Y["down"] = resid  # O and down accumulate into the residual
         R = len(layer["q"][3])
         launches = {l[0]: l for l in workloads.DECODE_LAUNCHES}
+        ws = None
+        if fused == "ffn":
+            ws = torch.zeros(ops.decode_ffn_workspace_bytes(M, ffn), dtype=torch.uint8, device=dev)
 
         def gemv(lname, r):
             _, projs, src, accum = launches[lname]
@@ -202,8 +209,23 @@ def main():
                                       outs=[Y[p] for p in projs],
                                       mode=ops.ACCUM if accum else ops.STORE)
 
+        def ffn_block(r, with_o=True):
+            ops.decode_ffn(layer["o"][3][r] if with_o else None, attn, resid, norm_w["ffn"],
+                           layer["gate"][3][r], layer["up"][3][r], layer["down"][3][r], hidden,
+                           q_dim, ffn, ws)
+
         def run(i, which=None):
             r = i % R
+            if fused == "ffn":
+                if which is None or which == "qkv":
+                    gemv_norm("qkv", r, resid, norm_w["attn"])
+                if which is None:
+                    ffn_block(r)
+                elif which == "o":
+                    gemv_norm("o", r, attn, None)
+                elif which == "ffn":
+                    ffn_block(r, with_o=False)
+                return
             prod = which is None or which == "producers"
             if prod and not fused:
                 ops.rmsnorm_quantize_q8_1(resid, norm_w["attn"], out=A["attn_in"])
@@ -236,14 +258,52 @@ def main():
         qt, _, K, _ = layer[projs[0]]
         return qt, gemv_bytes(ops, qt, M, [layer[p][1] for p in projs], K)
 
+    def form_kernel_bytes(layer, M, form):
+        """Algorithmic bytes of each launch of a layer form (weights, inputs
+        and outputs each counted once; fp32 residual, fp16 norm weights)."""
+        hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
+        wb = {n: ops.weight_bytes(v[0], v[1], v[2]) for n, v in layer.items()}
+        a = lambda K: M * (K // 32) * 36  # Q8_1 activations
+        qkv_n = sum(layer[p][1] for p in ("q", "k", "v"))
+        if form == "reference":
+            return {l[0]: launch_bytes(layer, l[0], M)[1] for l in workloads.DECODE_LAUNCHES}
+        out = {"qkv": wb["q"] + wb["k"] + wb["v"] + M * hidden * 4 + hidden * 2 + M * qkv_n * 4,
+               "o": wb["o"] + M * q_dim * 4 + M * hidden * 4}
+        if form == "ffn":
+            out["ffn"] = wb["gate"] + wb["up"] + wb["down"] + 2 * M * hidden * 4 + hidden * 2
+        else:
+            out["gate_up"] = (wb["gate"] + wb["up"] + M * hidden * 4 + hidden * 2 +
+                              (a(ffn) if form == "swiglu" else 2 * M * ffn * 4))
+            out["down"] = wb["down"] + a(ffn) + M * hidden * 4
+        return out
+
+    if args.profile:
+        # eager launches of one launch of a 3B layer form, for rocprofv3
+        form, kind = args.profile.split(":")
+        fused = {"reference": False, "fused_norm": True, "fused_norm_swiglu": "swiglu",
+                 "ffn_block": "ffn"}[form]
+        projs3b = workloads.QWEN3B_LAYER
+        R3 = n_replicas(layer_bytes(projs3b))
+        layer3b = make_layer(projs3b, seed=1, replicas=R3)
+        run = decode_layer_runner(layer3b, 1, seed=11, fused=fused)
+        profile_run(args, dev, lambda i: run(i, kind), f"{form}:{kind}",
+                    form_kernel_bytes(layer3b, 1, {False: "reference", True: "norm",
+                                                   "swiglu": "swiglu", "ffn": "ffn"}[fused])[kind])
+        return
+
     result = {}
     extras = {}
+    phase = {"setup_s": round(time.perf_counter() - T_START, 2)}
+    t_gpu = time.perf_counter()
 
     # ------------------------------------------------ headline: 3B layer
     projs3b = workloads.QWEN3B_LAYER
     R3 = n_replicas(layer_bytes(projs3b))
     layer3b = make_layer(projs3b, seed=1, replicas=R3)
+    layer_alg_bytes = {M: sum(launch_bytes(layer3b, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
+                       for M in (1, 4, 8)}
     per_m = {}
+    forms = {}  # M = 1 layer forms: name -> (runner, us per layer, kernel us, kernel bytes)
     for M in (1, 4, 8):
         run = decode_layer_runner(layer3b, M, seed=10 + M)
         steps = args.steps if M == 1 else max(20, args.steps // 2)
@@ -257,75 +317,76 @@ def main():
         q4 = [l[0] for l in workloads.DECODE_LAUNCHES if launch_bytes(layer3b, l[0], M)[0] == ops.Q4_K]
         q4_bytes = sum(launch_bytes(layer3b, n, M)[1] for n in q4)
         q4_us = sum(kern[n] for n in q4)
-        all_bytes = sum(launch_bytes(layer3b, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
         gemv_us = sum(kern[l[0]] for l in workloads.DECODE_LAUNCHES)
         per_m[M] = {
             "us_per_layer": round(us_layer, 2),
+            "layer_GBs": round(layer_alg_bytes[M] / us_layer / 1e3, 1),
             "us_sum_kernels": round(sum(kern.values()), 2),
             "q4k_gemv_GBs": round(q4_bytes / q4_us / 1e3, 1),
-            "layer_gemv_GBs": round(all_bytes / gemv_us / 1e3, 1),
+            "layer_gemv_GBs": round(layer_alg_bytes[M] / gemv_us / 1e3, 1),
             "kernel_us": {k: round(v, 2) for k, v in kern.items()},
             "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_layer * 1e-6), 1),
         }
-        if M <= 2:
-            # the same layer with the RMSNorm producers fused into QKV and gate/up
-            runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=True)
-            us_fused = time_loop(runf, steps, args.warmup)
-            per_m[M]["fused_norm"] = {
-                "us_per_layer": round(us_fused, 2),
-                "kernel_us": {n: round(time_loop(lambda i, n=n: runf(i, n), steps, args.warmup), 2)
-                              for n in ("qkv", "o", "gate_up", "producers")},
-                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_fused * 1e-6), 1),
-            }
-            # and with SiLU*up + Q8_1 fused into gate/up as well
-            runs = decode_layer_runner(layer3b, M, seed=10 + M, fused="swiglu")
-            us_swiglu = time_loop(runs, steps, args.warmup)
-            per_m[M]["fused_norm_swiglu"] = {
-                "us_per_layer": round(us_swiglu, 2),
-                "kernel_us": {n: round(time_loop(lambda i, n=n: runs(i, n), steps, args.warmup), 2)
-                              for n in ("qkv", "o", "gate_up", "down")},
-                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_swiglu * 1e-6), 1),
-            }
         if M == 1:
-            variants = {
-                "layer as the reference launches it": us_layer,
-                "layer with the Q8_1 producers of QKV, O and gate/up fused into them": us_fused,
-                "layer with the Q8_1 producers fused and SiLU*up + Q8_1 in the gate/up epilogue":
-                    us_swiglu,
-            }
-            step_is = min(variants, key=variants.get)
-            ms_per_step = variants[step_is] / 1e3
-            headline = q4_bytes / q4_us / 1e3
-            step_spread = spread(dict(zip(variants, (run, runf, runs)))[step_is], steps)
+            fb = form_kernel_bytes(layer3b, M, "reference")
+            forms["reference"] = (run, us_layer, {k: kern[k] for k in fb}, fb)
+            for form, fused, kinds in (("fused_norm", True, ("qkv", "o", "gate_up", "down")),
+                                       ("fused_norm_swiglu", "swiglu", ("qkv", "o", "gate_up", "down")),
+                                       ("ffn_block", "ffn", ("qkv", "o", "ffn"))):
+                runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=fused)
+                us_f = time_loop(runf, steps, args.warmup)
+                kus = {n: time_loop(lambda i, n=n: runf(i, n), steps, args.warmup) for n in kinds}
+                fb = form_kernel_bytes(layer3b, M, {"fused_norm": "norm", "fused_norm_swiglu": "swiglu",
+                                                    "ffn_block": "ffn"}[form])
+                fb = {k: fb[k] for k in kinds}
+                forms[form] = (runf, us_f, kus, fb)
+                per_m[M][form] = {
+                    "us_per_layer": round(us_f, 2),
+                    "layer_GBs": round(layer_alg_bytes[M] / us_f / 1e3, 1),
+                    "kernel_us": {k: round(v, 2) for k, v in kus.items()},
+                    "kernel_GBs": {k: round(fb[k] / kus[k] / 1e3, 1) for k in kinds},
+                    "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_f * 1e-6), 1),
+                }
     extras["qwen3b_layer"] = per_m
+    FORM_TEXT = {
+        "reference": "layer as the reference launches it (4 Q8_1 producers + 4 GEMVs)",
+        "fused_norm": "Q8_1 producers of QKV, O and gate/up fused into them (5 launches)",
+        "fused_norm_swiglu": "producers fused and SiLU*up + Q8_1 in the gate/up epilogue (4 launches)",
+        "ffn_block": "QKV with the fused RMSNorm, O, and one grid-synchronised FFN launch (3 launches)",
+    }
+    step_form = min(forms, key=lambda f: forms[f][1])
+    step_run, step_us, step_kus, step_kbytes = forms[step_form]
+    ms_per_step = step_us / 1e3
+    # headline: HBM GB/s of the timed step (the layer's algorithmic bytes over
+    # the step time), the same layer form that ms_per_step times
+    headline = layer_alg_bytes[1] / step_us / 1e3
+    step_spread = spread(step_run, max(20, args.steps // 10))
 
     # --------------------------------------- dominant kernel: roofline
-    # the grouped gate/up Q4_K GEMV (2 x 11008 x 2048), M = 1: events
-    # around graph-replayed launches on the stream the kernel runs on
-    M = 1
-    qt, N, K, _ = layer3b["gate"]
-    x = torch.from_numpy(synth.activations(M, K, seed=0)).to(dev)
-    A1 = ops.quantize_q8_1(x)
-    Yg = [torch.empty((M, N), dtype=torch.float32, device=dev) for _ in range(2)]
-    gate, up = layer3b["gate"][3], layer3b["up"][3]
-    dom_us = time_loop(lambda i: ops.qgemv_grouped(qt, [gate[i % R3], up[i % R3]], A1, M, [N, N],
-                                                   K, outs=Yg),
-                       max(args.steps, 200), args.warmup)
-    dom_spread = spread(lambda i: ops.qgemv_grouped(qt, [gate[i % R3], up[i % R3]], A1, M, [N, N],
-                                                    K, outs=Yg), max(args.steps, 200))
-    dom_bytes = gemv_bytes(ops, qt, M, [N, N], K)
+    # the timed step's longest launch, timed alone (events around graph-
+    # replayed launches on torch's current stream, the stream it runs on)
+    dom = max(step_kus, key=step_kus.get)
+    dom_us = time_loop(lambda i: step_run(i, dom), max(args.steps, 200), args.warmup)
+    dom_spread = spread(lambda i: step_run(i, dom), max(args.steps, 200))
+    dom_bytes = step_kbytes[dom]
+    with ops.launch_log() as lg:
+        step_run(0, dom)
+        torch.cuda.synchronize()
+    dom_kernels = lg.kernels
     achieved = dom_bytes / dom_us / 1e3
+    traffic, traffic_src = profile_traffic(dom_kernels[-1])
     result["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
-        "kernel": "k_gemv<Q4_K,MC=1,R=2,H=2> (wide slices, half-wave rows) grouped gate+up, N=2x11008 K=2048 M=1",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+        "kernel": ";".join(dom_kernels), "launch": dom,
         "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3),
+        "traffic_source": traffic_src,
     }
     # what a plain streaming read of the same number of bytes achieves
     # (the size-dependent ceiling: launch ramp and drain are fixed costs)
     probe = probe_lib()
     sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
-    wbytes = gate[0].numel() * 2
+    wbytes = (dom_bytes // 256) * 256
     big = torch.empty(max(ROTATE_BYTES * 2, 8 * wbytes), dtype=torch.uint8, device=dev)
     nrot = big.numel() // wbytes
 
@@ -337,7 +398,7 @@ def main():
     p_us = time_loop(probe_step, 200, 10)
     result["roofline"]["read_probe_same_bytes_GBs"] = round(wbytes / p_us / 1e3, 1)
     del big
-    del layer3b
+    del layer3b, forms, step_run
     torch.cuda.empty_cache()
 
     if not args.quick:
@@ -463,10 +524,13 @@ def main():
             torch.cuda.empty_cache()
         extras["config5_prefill_M512"] = c5
 
+    phase["gpu_s"] = round(time.perf_counter() - t_gpu, 2)
     # --------------------------------------------------- CPU baseline
     cpu = None
+    t_cpu = time.perf_counter()
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
+    phase["cpu_baseline_s"] = round(time.perf_counter() - t_cpu, 2)
 
     line = {
         "metric": "Q4_K dequant-GEMV HBM GB/s (% of peak) at M=1,8; us per decode layer",
@@ -483,16 +547,38 @@ def main():
         "data": "synthetic (seeded GGUF blocks, N(0,1) activations)",
         "config": {"workload": "qwen2.5-3b Q4_K_M decode layer, M=1 (BASELINE config 2)",
                    "M": 1, "hidden": 2048, "ffn": 11008, "weight_replicas": R3,
-                   "launches": [l[0] for l in workloads.DECODE_LAUNCHES],
-                   "step": step_is,
+                   "step": step_form, "step_is": FORM_TEXT[step_form],
+                   "step_launch_us": {k: round(v, 2) for k, v in step_kus.items()},
                    "spread": {"step": step_spread, "dominant_kernel": dom_spread},
-                   "value_is": "HBM GB/s of the layer's Q4_K GEMV launches (QKV, O, gate+up)",
-                   "frac_of_hbm_peak": round(headline / HBM_PEAK_GBS, 4)},
+                   "value_is": "HBM GB/s of the timed step: the layer's algorithmic bytes "
+                               "(Q4_K + Q6_K weights, Q8_1/fp32 activations, fp32 outputs, "
+                               "each once) over us per layer",
+                   "layer_bytes": layer_alg_bytes[1],
+                   "frac_of_hbm_peak": round(headline / HBM_PEAK_GBS, 4),
+                   "wall_s": phase},
         "roofline": result["roofline"],
         "cpu_baseline": cpu,
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
+
+
+def profile_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (profiles/*.md holding the lines "kernel: <instance>" and
+    "traffic_bytes_per_launch: <n>", from FETCH_SIZE and WRITE_SIZE runs
+    scaled by a copy of known size), or (None, reason)."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        kern = traffic = None
+        for line in open(path):
+            if line.startswith("kernel: "):
+                kern = line.split(":", 1)[1].strip()
+            elif line.startswith("traffic_bytes_per_launch: "):
+                traffic = int(line.split(":", 1)[1].strip())
+        if kern == kernel and traffic is not None:
+            return traffic, os.path.relpath(path, ROOT)
+    return None, "no counter summary for " + kernel + " under profiles/"
 
 
 def probe_lib():
@@ -507,36 +593,40 @@ def probe_lib():
     return lib
 
 
-def profile_run(args, dev):
-    """Eager launches for rocprofv3: `steps` launches of the dominant GEMV
-    (the grouped gate/up Q4_K GEMV, 2 x 11008 x 2048, M = 1, rotating weight
-    replicas), 20 copies of exactly 64 MiB (k_probe_copy: FETCH_SIZE and
-    WRITE_SIZE per dispatch of a known 64 MiB read and 64 MiB write
-    calibrate the counters), and 20 streaming reads of the dominant
-    launch's weight bytes (k_probe_read: the HBM read rate at this size).
+def profile_run(args, dev, launch, name, nbytes):
+    """Launches for rocprofv3: `warmup` eager launches, then `steps` launches
+    of one launch of the 3B layer (weight replicas rotating) captured in a
+    HIP graph and replayed twice, as the benchmark times them; 20 copies of exactly 64 MiB (k_probe_copy:
+    FETCH_SIZE and WRITE_SIZE per dispatch of a known 64 MiB read and 64 MiB
+    write calibrate the counters), and 20 streaming reads of the launch's
+    algorithmic byte count (k_probe_read: the HBM read rate at this size).
     Prints one JSON line of event timings."""
     import torch
 
-    from inferflux_amd import ops, synth
+    from inferflux_amd import ops
 
     stream = torch.cuda.current_stream()
-    qt, N, K = ops.Q4_K, 11008, 2048
-    g = torch.from_numpy(synth.blocks(qt, N, K, seed=0)).to(dev)
-    u = torch.from_numpy(synth.blocks(qt, N, K, seed=1)).to(dev)
-    R = max(2, -(-ROTATE_BYTES // (2 * g.numel())))
-    reps = [(g, u)] + [(g.clone(), u.clone()) for _ in range(R - 1)]
-    A = ops.quantize_q8_1(torch.from_numpy(synth.activations(1, K, seed=0)).to(dev))
-    Y = [torch.empty((1, N), dtype=torch.float32, device=dev) for _ in range(2)]
     for i in range(args.warmup):
-        ops.qgemv_grouped(qt, list(reps[i % R]), A, 1, [N, N], K, outs=Y)
+        launch(i)
+    torch.cuda.synchronize()
+    with ops.launch_log() as lg:
+        launch(0)
+        torch.cuda.synchronize()
+    # the launches captured in a graph and replayed, as the benchmark times them
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(args.steps):
+            launch(i)
+    stream = torch.cuda.current_stream()
+    g.replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(stream)
-    for i in range(args.steps):
-        ops.qgemv_grouped(qt, list(reps[i % R]), A, 1, [N, N], K, outs=Y)
+    g.replay()
     b.record(stream)
     torch.cuda.synchronize()
-    gemv_us = a.elapsed_time(b) * 1e3 / args.steps
+    us = a.elapsed_time(b) * 1e3 / args.steps
+    del g
 
     lib = probe_lib()
     sp = stream.cuda_stream
@@ -545,15 +635,14 @@ def profile_run(args, dev):
     sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
     for _ in range(20):
         assert lib.ifx_probe_copy(dst.data_ptr(), big.data_ptr(), big.numel(), 8192, sp) == 0
-    nbytes = g.numel()
+    rb = (nbytes // 256) * 256
+    src = torch.empty(rb, dtype=torch.uint8, device=dev)
     for i in range(20):
-        assert lib.ifx_probe_read(reps[i % R][0].data_ptr(), nbytes, sink.data_ptr(), 1 << 20,
-                                  sp) == 0
+        assert lib.ifx_probe_read(src.data_ptr(), rb, sink.data_ptr(), 1 << 20, sp) == 0
     torch.cuda.synchronize()
-    print(json.dumps({"profile": "dominant gemv",
-                      "kernel": "k_gemv Q4_K grouped gate+up N=2x11008 K=2048 M=1",
-                      "launches": args.steps, "event_us_per_launch": round(gemv_us, 3),
-                      "copy_bytes": big.numel(), "read_probe_bytes": nbytes}), flush=True)
+    print(json.dumps({"profile": name, "kernels": lg.kernels, "launches": args.steps,
+                      "event_us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
+                      "copy_bytes": big.numel(), "read_probe_bytes": rb}), flush=True)
 
 
 def profile_kernels_run(args, dev):

@@ -200,6 +200,8 @@ int64_t ifx_decode_ffn_workspace_bytes(int M, int ffn);
  * leaves the residual bit for bit equal to that chain's (here:
  * ifx_qgemv_grouped_rmsnorm with norm_weight NULL in IFX_ACCUM mode,
  * ifx_qgemv_gate_up_silu_rmsnorm, ifx_qgemv in IFX_ACCUM mode).
+ * W_o NULL skips the O launch (attn is then not read): for callers whose
+ * residual already holds the attention block's output.
  * Types: W_o, W_gate, W_up Q4_K, W_down Q6_K (the Q4_K_M mix); attn [q_dim]
  * fp32 or fp16 (attn_dtype IFX_OUT_F32 / IFX_OUT_F16); residual [hidden]
  * fp32; norm weight [hidden] fp16.  Covered shapes: M = 1, q_dim and hidden

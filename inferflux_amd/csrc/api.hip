@@ -546,26 +546,32 @@ int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype
                    const void *W_gate, const void *W_up, int ffn, int down_type,
                    const void *W_down, int M, int hidden, void *workspace,
                    int64_t workspace_bytes, void *stream) {
-  if (!W_o || !attn || !residual || !ffn_norm_weight || !W_gate || !W_up || !W_down || !workspace)
+  if ((W_o && !attn) || !residual || !ffn_norm_weight || !W_gate || !W_up || !W_down ||
+      !workspace)
     return IFX_NULL_POINTER;
-  if (o_type != IFX_TYPE_Q4_K || gate_up_type != IFX_TYPE_Q4_K || down_type != IFX_TYPE_Q6_K)
+  if ((W_o && o_type != IFX_TYPE_Q4_K) || gate_up_type != IFX_TYPE_Q4_K ||
+      down_type != IFX_TYPE_Q6_K)
     return IFX_UNSUPPORTED_TYPE;
-  if (attn_dtype != IFX_OUT_F32 && attn_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
+  if (W_o && attn_dtype != IFX_OUT_F32 && attn_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   if (!(eps >= 0.0f) || M != 1) return IFX_BAD_GEOMETRY;
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return IFX_BAD_GEOMETRY;
   if (workspace_bytes < ifx_decode_ffn_workspace_bytes(M, ffn)) return IFX_BAD_GEOMETRY;
-  // the 32-bit range checks of the three GEMVs
-  int rc = check_gemm_args(o_type, W_o, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M, hidden,
-                           q_dim);
+  // the 32-bit range checks of the GEMVs
+  int rc = IFX_OK;
+  if (W_o) {
+    rc = check_gemm_args(o_type, W_o, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M, hidden,
+                         q_dim);
+    // the O launch: the fused-quantizer GEMV's activation tile fits its LDS
+    if (rc == IFX_OK && (q_dim % 256 || q_dim / 32 * ifx::kQ8_1Bytes > 65536))
+      rc = IFX_BAD_GEOMETRY;
+  }
   if (rc == IFX_OK)
-    rc = check_gemm_args(gate_up_type, W_gate, attn, residual, IFX_OUT_F32, IFX_STORE, nullptr, M,
-                         ffn, hidden);
+    rc = check_gemm_args(gate_up_type, W_gate, W_gate, residual, IFX_OUT_F32, IFX_STORE, nullptr,
+                         M, ffn, hidden);
   if (rc == IFX_OK)
-    rc = check_gemm_args(down_type, W_down, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M,
+    rc = check_gemm_args(down_type, W_down, W_down, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M,
                          hidden, ffn);
   if (rc != IFX_OK) return rc;
-  // the O launch: the fused-quantizer GEMV's activation tile fits its LDS
-  if (q_dim % 256 || q_dim / 32 * ifx::kQ8_1Bytes > 65536) return IFX_BAD_GEOMETRY;
   if (!ifx::decode_ffn_fits(hidden, ffn)) return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_decode_ffn(W_o, attn, attn_dtype == IFX_OUT_F16, residual,
                                           ffn_norm_weight, eps, W_gate, W_up, W_down, workspace,

@@ -349,17 +349,19 @@ hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, 
                                const void *x, bool x_f16, const uint16_t *norm_w, float eps,
                                bool f16, int M, int K, int mode, hipStream_t stream);
 
-// O accumulated into the residual (the GEMV with the fused quantizer), then
-// the FFN kernel.
+// O accumulated into the residual (the GEMV with the fused quantizer; none
+// when Wo is NULL), then the FFN kernel.
 hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, float *resid,
                              const uint16_t *norm_w, float eps, const void *Wg, const void *Wu,
                              const void *Wd, void *workspace, int q_dim, int hidden, int ffn,
                              hipStream_t s) {
   if (!decode_ffn_fits(hidden, ffn)) return hipErrorInvalidValue;
-  void *y = resid;
-  hipError_t e = launch_gemv_rmsnorm(1, &Wo, &y, &hidden, attn, attn_f16, nullptr, 0.0f, false, 1,
-                                     q_dim, 1 /* accumulate */, s);
-  if (e != hipSuccess) return e;
+  if (Wo) {  // NULL: the residual already holds the attention block's output
+    void *y = resid;
+    const hipError_t e = launch_gemv_rmsnorm(1, &Wo, &y, &hidden, attn, attn_f16, nullptr, 0.0f,
+                                             false, 1, q_dim, 1 /* accumulate */, s);
+    if (e != hipSuccess) return e;
+  }
   FfnArgs a;
   a.Wg = static_cast<const uint8_t *>(Wg);
   a.Wu = static_cast<const uint8_t *>(Wu);

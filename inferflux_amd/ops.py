@@ -309,26 +309,31 @@ def decode_ffn_workspace_bytes(M, ffn):
 
 def decode_ffn(W_o, attn, resid, norm_weight, W_gate, W_up, W_down, hidden, q_dim, ffn,
                workspace, eps=1e-6, stream=None):
-    """The post-attention half of a decode layer at M = 1 in one launch
+    """The post-attention half of a decode layer at M = 1 in two launches
     (ifx_decode_ffn): resid += O . Q8_1(attn); h = silu(gate . a) * (up . a)
     with a = Q8_1(RMSNorm(resid)); resid += down . Q8_1(h).  O, gate, up
     Q4_K, down Q6_K; resid [1, hidden] fp32 updated in place; workspace a
     device tensor of at least decode_ffn_workspace_bytes(1, ffn) bytes whose
-    first 2048 bytes (the control block) are zero before the first call."""
+    first 2048 bytes (the control block) are zero before the first call.
+    W_o None: the O launch is skipped (the residual already holds the
+    attention block's output; attn is not read)."""
     M = 1
-    if resid.dtype != torch.float32 or resid.numel() < hidden or attn.numel() < q_dim:
+    if resid.dtype != torch.float32 or resid.numel() < hidden or (
+            W_o is not None and attn.numel() < q_dim):
         raise ValueError("resid must be fp32 [hidden]; attn [q_dim]")
     if norm_weight.dtype != torch.float16 or norm_weight.numel() < hidden:
         raise ValueError("norm_weight must be fp16 [hidden]")
     for W, n, k in ((W_o, hidden, q_dim), (W_gate, ffn, hidden), (W_up, ffn, hidden)):
-        if W.numel() < weight_bytes(Q4_K, n, k):
+        if W is not None and W.numel() < weight_bytes(Q4_K, n, k):
             raise ValueError("a Q4_K weight is smaller than its shape")
     if W_down.numel() < weight_bytes(Q6_K, hidden, ffn):
         raise ValueError("W_down is smaller than its shape")
-    ad = OUT_F16 if attn.dtype == torch.float16 else OUT_F32
+    ad = OUT_F16 if W_o is not None and attn.dtype == torch.float16 else OUT_F32
     nbytes = workspace.numel() * workspace.element_size()
+    wo = _dev(W_o, "W_o") if W_o is not None else None
+    ap = _dev(attn, "attn") if W_o is not None else None
     rc = _lib.load().ifx_decode_ffn(
-        Q4_K, _dev(W_o, "W_o"), _dev(attn, "attn"), ad, q_dim, _dev(resid, "resid"),
+        Q4_K, wo, ap, ad, q_dim, _dev(resid, "resid"),
         _dev(norm_weight, "norm_weight"), eps, Q4_K, _dev(W_gate, "W_gate"), _dev(W_up, "W_up"),
         ffn, Q6_K, _dev(W_down, "W_down"), M, hidden, _dev(workspace, "workspace"), nbytes,
         _stream(stream))

@@ -87,5 +87,9 @@ def test_decode_ffn_routing():
                                   None)
         return rc, lg.kernels
     assert call(2048, 11008) == (0, ["k_gemv<12,1,1,1,4,0,2,3>", "k_decode_ffn"])
+    with ops.launch_log(dry=True) as lg:  # W_o NULL: the FFN kernel alone
+        rc = L.ifx_decode_ffn(ops.Q4_K, None, None, ops.OUT_F32, 2048, f[2], f[3], 1e-6,
+                              ops.Q4_K, f[4], f[5], 11008, ops.Q6_K, f[6], 1, 2048, f[7], ws, None)
+    assert rc == 0 and lg.kernels == ["k_decode_ffn"]
     assert call(5120, 13824)[0] == 2  # hidden beyond half-wave rows: not handled
     assert call(2048, 11008, M=2)[0] == 2

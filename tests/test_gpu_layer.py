@@ -192,3 +192,22 @@ def test_decode_ffn_not_handled(dev):
             rc = L.ifx_decode_ffn(ot, p, p, 0, q, p, p, 1e-6, gt, p, p, f, dt, p, M, hd, p, wsb,
                                   torch.cuda.current_stream().cuda_stream)
         assert rc > 0 and lg.kernels == []
+
+
+def test_decode_ffn_without_o(layer, dev):
+    """W_o None: only the FFN kernel runs, on a residual that already holds
+    the attention block's output; equal to the two launches after O."""
+    from inferflux_amd import ops
+    h, d = layer
+    note("decode_ffn without O")
+    rc = d["resid"].clone()
+    _, hq = ops.qgemv_gate_up_silu_rmsnorm(Q4_K, d["wg"], d["wu"], rc, d["nw"], 1, FFN, HIDDEN,
+                                           eps=1e-6)
+    ops.qgemv(Q6_K, d["wd"], hq, 1, HIDDEN, FFN, out=rc, mode=ops.ACCUM)
+    rf = d["resid"].clone()
+    ws = new_ws(ops, dev)
+    with ops.launch_log() as lg:
+        ops.decode_ffn(None, None, rf, d["nw"], d["wg"], d["wu"], d["wd"], HIDDEN, QDIM, FFN, ws,
+                       eps=1e-6)
+    assert lg.kernels == ["k_decode_ffn"]
+    assert np.array_equal(down(rf).view(np.uint32), down(rc).view(np.uint32))
