@@ -86,9 +86,14 @@ int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void
  * Replaces FusedQuantGemm::GemvQ8_1 / GemvQ8_1Accum / GemvQ8_1AccumF32 /
  * GemvQ8_1WithBias (fused_quant_gemm.h:171-173, 190-193, 202-205; .cu
  * 2085-2260) and the dispatch DispatchQ8_1Gemv{Q4K,Q6K,Q8_0}
- * (fused_quant_gemm.cu:1705-1738).  M <= 8 runs the weight-streaming GEMV,
- * larger M the int8-MFMA GEMM (the reference returns false for M > 64 and
- * falls back to FP16 cuBLAS; here every M is handled).
+ * (fused_quant_gemm.cu:1705-1738).  The kernel is chosen by M, shape and
+ * type (ifx_launch_log_begin names it): M <= 2 the weight-streaming v_dot4
+ * GEMV; 3 <= M <= 16 the integer-dot batch kernels (activations in LDS,
+ * slot-packed int8 MFMA, LDS-staged int8 MFMA); 17 <= M <= 32 the fp16-
+ * dequant MFMA GEMV; larger M the int8 MFMA GEMM, and from M = 33 (Q6_K),
+ * 96 (Q4_K) or 128 (Q8_0) on the fp16 MFMA GEMM with in-kernel dequant (the
+ * reference's prefill arithmetic).  The reference returns false for M > 64
+ * and falls back to FP16 cuBLAS; here every M is handled.
  * out_dtype: ifx_out_dtype.  mode: ifx_out_mode.  bias may be NULL unless
  * mode == IFX_BIAS. */
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,

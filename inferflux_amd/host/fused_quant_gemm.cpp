@@ -4,6 +4,7 @@
 // bool "launched" results, QuantizedWeightInfo views, the
 // INFERFLUX_DISABLE_FUSED_GEMV policy switch -- and leaves every launch to
 // the C ABI, which validates arguments and reports HIP errors.
+#include <algorithm>
 #include "../../include/ifx_fused_quant_gemm.h"
 
 #include <cstdlib>
@@ -198,10 +199,12 @@ bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
 
 // The reference scales a per-GPU-generation base by 16/bpw and clamps to
 // [4, 64] (fused_quant_gemm.cu:62-184, 830-880): above it, dequantize +
-// FP16 cuBLAS wins on its tensor cores.  On gfx950 the quantized path has
-// an int8 MFMA GEMM at every M >= 33 that reads the raw blocks (3.6x fewer
-// bytes than an FP16 copy for Q4_K) and runs at twice the FP16 MFMA rate,
-// so the fallback never wins: the threshold is the path's M limit.
+// FP16 cuBLAS wins on its tensor cores.  On gfx950 the quantized path itself
+// switches to an fp16 MFMA GEMM that dequantizes inside the kernel (from
+// M = 33 for Q6_K, 96 for Q4_K, 128 for Q8_0; below that the integer-dot
+// kernels), which reads the raw blocks instead of an FP16 copy and measured
+// 1.4-1.7x faster than dequantize + the vendor FP16 GEMM at the 32B prefill
+// shapes, so the fallback never wins: the threshold is the path's M limit.
 int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
   if (!SupportsQ8_1Activations(quant_type)) return 0;
   if (quant_type == static_cast<int>(TensorType::Q5_K) ||
@@ -210,10 +213,25 @@ int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
   return kMaxFusedM;
 }
 
+// The geometry narrows it where a kernel has a hard limit (the reference
+// adjusts its threshold for packed activations, grouped outputs and K,
+// fused_quant_gemm.cu:830-923):
+//  * includes_rmsnorm: the RMSNorm + Q8_1 producer fused into the GEMV
+//    (ifx_qgemv_grouped_rmsnorm) is Q4_K only, M <= 2, with the batch's Q8_1
+//    rows in 64 KiB of LDS; larger batches take the producer + GEMV;
+//  * K: the Q8_1 activations [M][K/32] are addressed with 32-bit offsets.
 int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,
                                               const FusedDispatchGeometry &geometry) {
-  if (geometry.M <= 0) return 0;
-  return GetAdaptiveThreshold(quant_type);
+  int64_t t = GetAdaptiveThreshold(quant_type);
+  if (t == 0) return 0;
+  const int64_t a_row = geometry.K > 0 ? static_cast<int64_t>(geometry.K / 32) * 36 : 0;
+  if (geometry.includes_rmsnorm) {
+    if (quant_type != static_cast<int>(TensorType::Q4_K)) return 0;
+    t = std::min<int64_t>(t, 2);
+    if (a_row > 0) t = std::min<int64_t>(t, 65536 / a_row);
+  }
+  if (a_row > 0) t = std::min<int64_t>(t, ((int64_t{1} << 32) - 1) / a_row);
+  return static_cast<int>(t);
 }
 
 bool FusedQuantGemm::ShouldUseFusedPath(int quant_type, int M) {
