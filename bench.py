@@ -153,7 +153,7 @@ def main():
         return {"median_us": round(float(med), 2), "p10_us": round(float(p10), 2),
                 "p90_us": round(float(p90), 2), "replays": reps, "calls_per_replay": steps}
 
-    def decode_layer_runner(layer, M, seed, fused=False):
+    def decode_layer_runner(layer, M, seed, fused=False, split_down=False):
         """One decode layer at batch M as a chain over an fp32 residual
         stream: RMSNorm+Q8_1 -> grouped QKV -> Q8_1 of the attention output
         (synthetic: attention itself is not on this path) -> O accumulated
@@ -168,6 +168,8 @@ def main():
         fused == "ffn": QKV with the fused RMSNorm, then ifx_decode_ffn: O
         with the fused quantizer and one grid-synchronised launch for
         RMSNorm, gate/up + SiLU and down (M = 1): 3 launches.
+        split_down: the down projection reads a row-split copy of its Q6_K
+        weights (ifx_repack, M <= 2).
         run(i, which) runs one launch kind alone ("qkv", "o", "gate_up",
         "down", "producers"; "ffn": the FFN kernel of the "ffn" form alone)."""
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
@@ -185,6 +187,10 @@ def main():
         Y["o"] = Y["down"] = resid  # O and down accumulate into the residual
         R = len(layer["q"][3])
         launches = {l[0]: l for l in workloads.DECODE_LAUNCHES}
+        down_w = layer["down"]
+        if split_down:
+            qt, N, K, reps = layer["down"]
+            down_w = (ops.Q6_K_R, N, K, [ops.repack(qt, w, N, K)[1] for w in reps])
         ws = None
         if fused == "ffn":
             ws = torch.zeros(ops.decode_ffn_workspace_bytes(M, ffn), dtype=torch.uint8, device=dev)
@@ -194,7 +200,8 @@ def main():
             qt, _, K, _ = layer[projs[0]]
             mode = ops.ACCUM if accum else ops.STORE
             if len(projs) == 1:
-                p = layer[projs[0]]
+                p = down_w if projs[0] == "down" else layer[projs[0]]
+                qt = p[0]
                 ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode)
             else:
                 ops.qgemv_grouped(qt, [layer[p][3][r] for p in projs], A[src], M,
@@ -281,11 +288,12 @@ def main():
         # eager launches of one launch of a 3B layer form, for rocprofv3
         form, kind = args.profile.split(":")
         fused = {"reference": False, "fused_norm": True, "fused_norm_swiglu": "swiglu",
-                 "ffn_block": "ffn"}[form]
+                 "fused_norm_swiglu_split_down": "swiglu", "ffn_block": "ffn"}[form]
         projs3b = workloads.QWEN3B_LAYER
         R3 = n_replicas(layer_bytes(projs3b))
         layer3b = make_layer(projs3b, seed=1, replicas=R3)
-        run = decode_layer_runner(layer3b, 1, seed=11, fused=fused)
+        run = decode_layer_runner(layer3b, 1, seed=11, fused=fused,
+                                  split_down=form.endswith("split_down"))
         profile_run(args, dev, lambda i: run(i, kind), f"{form}:{kind}",
                     form_kernel_bytes(layer3b, 1, {False: "reference", True: "norm",
                                                    "swiglu": "swiglu", "ffn": "ffn"}[fused])[kind])
@@ -332,11 +340,15 @@ def main():
             forms["reference"] = (run, us_layer, {k: kern[k] for k in fb}, fb)
             for form, fused, kinds in (("fused_norm", True, ("qkv", "o", "gate_up", "down")),
                                        ("fused_norm_swiglu", "swiglu", ("qkv", "o", "gate_up", "down")),
+                                       ("fused_norm_swiglu_split_down", "swiglu",
+                                        ("qkv", "o", "gate_up", "down")),
                                        ("ffn_block", "ffn", ("qkv", "o", "ffn"))):
-                runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=fused)
+                runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=fused,
+                                           split_down=form.endswith("split_down"))
                 us_f = time_loop(runf, steps, args.warmup)
                 kus = {n: time_loop(lambda i, n=n: runf(i, n), steps, args.warmup) for n in kinds}
                 fb = form_kernel_bytes(layer3b, M, {"fused_norm": "norm", "fused_norm_swiglu": "swiglu",
+                                                    "fused_norm_swiglu_split_down": "swiglu",
                                                     "ffn_block": "ffn"}[form])
                 fb = {k: fb[k] for k in kinds}
                 forms[form] = (runf, us_f, kus, fb)
@@ -352,6 +364,8 @@ def main():
         "reference": "layer as the reference launches it (4 Q8_1 producers + 4 GEMVs)",
         "fused_norm": "Q8_1 producers of QKV, O and gate/up fused into them (5 launches)",
         "fused_norm_swiglu": "producers fused and SiLU*up + Q8_1 in the gate/up epilogue (4 launches)",
+        "fused_norm_swiglu_split_down": "as fused_norm_swiglu, with the down projection on a "
+                                        "row-split copy of its Q6_K weights (ifx_repack)",
         "ffn_block": "QKV with the fused RMSNorm, O, and one grid-synchronised FFN launch (3 launches)",
     }
     step_form = min(forms, key=lambda f: forms[f][1])
@@ -433,6 +447,19 @@ def main():
                 gb = gemv_bytes(ops, qt, M, [N], K) / us / 1e3
                 c3[f"{key}_M{M}"] = {"us": round(us, 2), "GBs": round(gb, 1),
                                      "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
+            # the same weights as a row-split copy (ifx_repack), M = 1 and 2;
+            # GB/s over the raw layout's algorithmic bytes
+            rreps = [ops.repack(qt, w_, N, K)[1] for w_ in reps]
+            rt = ops.Q8_0_R if qt == ops.Q8_0 else ops.Q6_K_R
+            for M in (1, 2):
+                A = ops.quantize_q8_1(torch.from_numpy(synth.activations(M, K, seed=3)).to(dev))
+                Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+                us = time_loop(lambda i: ops.qgemv(rt, rreps[i % 2], A, M, N, K, out=Y),
+                               max(20, args.steps // 4), 5)
+                gb = gemv_bytes(ops, qt, M, [N], K) / us / 1e3
+                c3[f"{key}_row_split_M{M}"] = {"us": round(us, 2), "GBs": round(gb, 1),
+                                               "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
+            del rreps
             del reps, w
             torch.cuda.empty_cache()
         extras["config3_lm_head_151936x2048"] = c3

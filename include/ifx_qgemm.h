@@ -35,7 +35,12 @@ enum ifx_quant_type {
   IFX_TYPE_Q4_K = 12,
   IFX_TYPE_Q5_K = 13, /* GEMV kernel family only, M <= 64 (no reference kernel) */
   IFX_TYPE_Q6_K = 14,
-  IFX_TYPE_Q8_K = 15  /* GEMV kernel family only, M <= 64 (the reference's limit) */
+  IFX_TYPE_Q8_K = 15, /* GEMV kernel family only, M <= 64 (the reference's limit) */
+  /* The row-split layouts ifx_repack writes (this library's own, no GGUF
+   * id): each row's block fields in separate 16-byte-aligned sections.
+   * ifx_qgemv / ifx_qgemv_grouped at M <= 2 only. */
+  IFX_TYPE_Q8_0_R = 108, /* [qs: K bytes][d: K/32 fp16][pad to 16] per row */
+  IFX_TYPE_Q6_K_R = 114  /* [ql: K/2][qh: K/4][scales: K/16][d: K/256 fp16][pad to 16] */
 };
 
 enum ifx_status {
@@ -266,6 +271,23 @@ enum ifx_prefill_kernel { IFX_PREFILL_INT8 = 1, IFX_PREFILL_F16 = 2, IFX_DECODE_
 int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
                              int out_dtype, int mode, const void *bias, int M, int N, int K,
                              int kernel, int splits, void *stream);
+
+/* Bytes of the row-split copy of n_rows x K Q8_0 or Q6_K weights (0 for
+ * another type or a bad K). */
+int64_t ifx_repacked_bytes(int quant_type, int64_t n_rows, int K);
+
+/* Load-time repack of raw GGUF Q8_0 / Q6_K rows into the row-split layout
+ * IFX_TYPE_Q8_0_R / IFX_TYPE_Q6_K_R (W_out: ifx_repacked_bytes, caller
+ * owned, 16-byte aligned).  Their 34- and 210-byte blocks leave rows and
+ * fields unaligned; split, every field is read with aligned 16-byte loads
+ * that use all their bytes (measured on the 151936 x 2048 Q8_0 LM head: 5.8
+ * against 4.7 TB/s for a pure read of either layout).  The row sums are the
+ * raw layout's, bit for bit, wherever the GEMV geometry is the same.  The
+ * copy serves the M <= 2 GEMV; larger batches need the raw weights.  Plays
+ * the role of the reference's load-time re-tiled down-projection copy
+ * (BuildDownProjMmqLayout / transform_downproj_mmq_layout,
+ * fused_quant_gemm.h:213-234, fused_quant_gemm.cu:573-596, 1966-2032). */
+int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K, void *stream);
 
 /* Whole-tensor dequantization of n_rows x K weights to fp32 or fp16.
  * Replaces dequantize_q4_k / dequantize_q6_k / dequantize_q8_0

@@ -32,6 +32,8 @@ SIGNATURES = {
                         _i32, _vp, _i32, _i32, _vp, _i64, _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
+    "ifx_repacked_bytes": ([_i32, _i64, _i32], _i64),
+    "ifx_repack": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_launch_log_begin": ([_i32], None),

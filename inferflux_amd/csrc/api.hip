@@ -59,6 +59,8 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
                           int mode, int splits_req, hipStream_t stream);
 hipError_t scratch_address(void **out);
+hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, int K,
+                         hipStream_t stream);
 bool decode_ffn_fits(int hidden, int ffn);
 hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, float *resid,
                              const uint16_t *norm_w, float eps, const void *Wg, const void *Wu,
@@ -214,8 +216,18 @@ int status_of(hipError_t e) { return e == hipSuccess ? IFX_OK : -static_cast<int
 
 bool gemv_only(int t) { return t == IFX_TYPE_Q5_K || t == IFX_TYPE_Q8_K; }
 
+// the row-split layouts of ifx_repack: the v_dot4 GEMV at M <= 2 only
+bool row_split(int t) { return t == IFX_TYPE_Q8_0_R || t == IFX_TYPE_Q6_K_R; }
+constexpr int kMaxRowSplitM = 2;
+
 bool is_weight_type(int t) {
-  return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0 || gemv_only(t);
+  return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0 || gemv_only(t) ||
+         row_split(t);
+}
+
+// Bytes of an N x K weight tensor (0 for an unknown type).
+uint64_t weight_bytes(int t, int N, int K) {
+  return ifx_block_elems(t) ? static_cast<uint64_t>(N) * ifx::row_bytes(t, K) : 0;
 }
 
 int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int out_dtype,
@@ -228,10 +240,10 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   if (M <= 0 || N <= 0 || K <= 0) return IFX_BAD_GEOMETRY;
   if (K % ifx_block_elems(quant_type) != 0) return IFX_BAD_GEOMETRY;
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return IFX_BAD_GEOMETRY;
+  if (row_split(quant_type) && M > kMaxRowSplitM) return IFX_BAD_GEOMETRY;
   // Kernels address W and A with 32-bit byte offsets (buffer loads).
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
-  const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
-                           ifx_block_bytes(quant_type);
+  const uint64_t w_bytes = weight_bytes(quant_type, N, K);
   const uint64_t a_bytes = static_cast<uint64_t>(M) * (K / 32) * 36;
   if (w_bytes >= (1ull << 32) || a_bytes >= (1ull << 32)) return IFX_BAD_GEOMETRY;
   return IFX_OK;
@@ -249,14 +261,17 @@ int ifx_block_bytes(int quant_type) {
   case IFX_TYPE_Q8_K: return ifx::kQ8KBytes;
   case IFX_TYPE_Q8_0: return ifx::kQ8_0Bytes;
   case IFX_TYPE_Q8_1: return ifx::kQ8_1Bytes;
+  case IFX_TYPE_Q8_0_R: return ifx::kQ8_0Bytes;
+  case IFX_TYPE_Q6_K_R: return ifx::kQ6KBytes;
   default: return 0;
   }
 }
 
 int ifx_block_elems(int quant_type) {
   switch (quant_type) {
-  case IFX_TYPE_Q4_K: case IFX_TYPE_Q5_K: case IFX_TYPE_Q6_K: case IFX_TYPE_Q8_K: return 256;
-  case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: return 32;
+  case IFX_TYPE_Q4_K: case IFX_TYPE_Q5_K: case IFX_TYPE_Q6_K: case IFX_TYPE_Q8_K:
+  case IFX_TYPE_Q6_K_R: return 256;
+  case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: case IFX_TYPE_Q8_0_R: return 32;
   default: return 0;
   }
 }
@@ -277,16 +292,16 @@ int ifx_supports(int quant_type, int M, int N, int K) {
   if (!is_weight_type(quant_type)) return 0;
   if (M <= 0 || N <= 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return 0;
+  if (row_split(quant_type) && M > kMaxRowSplitM) return 0;
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
-  const uint64_t w_bytes = static_cast<uint64_t>(N) * (K / ifx_block_elems(quant_type)) *
-                           ifx_block_bytes(quant_type);
+  const uint64_t w_bytes = weight_bytes(quant_type, N, K);
   if (w_bytes >= (1ull << 32) || static_cast<uint64_t>(M) * (K / 32) * 36 >= (1ull << 32)) return 0;
   return 1;
 }
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
-  if (gemv_only(quant_type) || use_lds(quant_type, M, K, N)) return 1;
+  if (gemv_only(quant_type) || row_split(quant_type) || use_lds(quant_type, M, K, N)) return 1;
   if (M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K)) return 4;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
   if (!use_slot(quant_type, M, K, N, false) && use_dq(quant_type, M, K, false)) return 5;
@@ -348,7 +363,8 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   const bool f16 = out_dtype == IFX_OUT_F16;
   if (!gemv_only(quant_type) && M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K))
     return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
-  if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
+  if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
+      (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
   if (use_lds(quant_type, M, K, N))
     return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
@@ -378,7 +394,8 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  if (gemv_only(quant_type) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
+  if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
+      (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
         ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
   int n_total = 0;
@@ -436,7 +453,7 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
                            const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
                            int N, int K, void *stream) {
   if (!W_gate || !W_up || !A_q8_1 || (!H && !q8_1_out)) return IFX_NULL_POINTER;
-  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   // the fused kernel serves the decode batch M <= 2 and whole Q8_1 blocks
   // of outputs; other shapes take the grouped GEMV + SiLU producer
@@ -479,7 +496,7 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
                       int mode, const void *bias, int M, int N, int K, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
+  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
   const bool f16 = out_dtype == IFX_OUT_F16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (use_f16_gemm(quant_type, M, K))
@@ -493,7 +510,8 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
 constexpr int kMinWorkspaceN = 16384;
 
 int64_t ifx_qgemm_prefill_workspace_bytes(int quant_type, int M, int N, int K) {
-  if (!is_weight_type(quant_type) || gemv_only(quant_type) || M <= 0 || N <= 0 || K <= 0)
+  if (!is_weight_type(quant_type) || gemv_only(quant_type) || row_split(quant_type) || M <= 0 ||
+      N <= 0 || K <= 0)
     return 0;
   if (!use_f16_gemm(quant_type, M, K) || !ifx::gemm_f16_fits(quant_type, K) || N < kMinWorkspaceN)
     return 0;
@@ -505,7 +523,7 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
                          int64_t workspace_bytes, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
   if (need == 0 || !workspace)
     return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
@@ -521,7 +539,7 @@ int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1,
                               void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
   if (need == 0)
     return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
@@ -583,7 +601,7 @@ int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, 
                              int kernel, int splits, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const bool f16 = out_dtype == IFX_OUT_F16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (kernel == IFX_PREFILL_INT8)
@@ -599,10 +617,28 @@ int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, 
   return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, splits, s));
 }
 
+int64_t ifx_repacked_bytes(int quant_type, int64_t n_rows, int K) {
+  const int rt = quant_type == IFX_TYPE_Q8_0 ? IFX_TYPE_Q8_0_R
+                 : quant_type == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_R : 0;
+  if (!rt || n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
+  return n_rows * static_cast<int64_t>(ifx::row_bytes(rt, K));
+}
+
+int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K, void *stream) {
+  if (!W || !W_out) return IFX_NULL_POINTER;
+  if (quant_type != IFX_TYPE_Q8_0 && quant_type != IFX_TYPE_Q6_K) return IFX_UNSUPPORTED_TYPE;
+  if (n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return IFX_BAD_GEOMETRY;
+  if (ifx_repacked_bytes(quant_type, n_rows, K) >= (int64_t{1} << 32) ||
+      n_rows * (K / ifx_block_elems(quant_type)) * static_cast<int64_t>(ifx_block_bytes(quant_type)) >=
+          (int64_t{1} << 32))
+    return IFX_BAD_GEOMETRY;  // the GEMV addresses rows with 32-bit offsets
+  return status_of(ifx::launch_repack(quant_type, W, W_out, n_rows, K, static_cast<hipStream_t>(stream)));
+}
+
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,
                    void *stream) {
   if (!W || !out) return IFX_NULL_POINTER;
-  if (!is_weight_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (out_dtype != IFX_OUT_F32 && out_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   if (n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return IFX_BAD_GEOMETRY;
   if (n_rows * static_cast<int64_t>((K / ifx_block_elems(quant_type)) * ifx_block_bytes(quant_type)) >= (int64_t{1} << 32))

@@ -151,4 +151,56 @@ hipError_t launch_dequantize(int qtype, const void *W, void *out, bool f16, int6
   return last_error();
 }
 
+// ---------------------------------------------------------------------------
+// Row-split repack (ifx_repack): the fields of each GGUF block of a row move
+// to separate 16-byte-aligned sections of the row (layouts in ifx_common.h).
+// One thread per (row, block); a load-time operation, so plain byte moves.
+// Each row's padding bytes are written as zeros by the row's last block.
+// ---------------------------------------------------------------------------
+template <int QT>
+__global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ W,
+                                                uint8_t *__restrict__ out, int64_t n_rows, int K) {
+  constexpr int kElems = QT == kTypeQ8_0 ? 32 : 256;
+  constexpr int kBytes = QT == kTypeQ8_0 ? kQ8_0Bytes : kQ6KBytes;
+  const int nb = K / kElems;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= n_rows * nb) return;
+  const int64_t row = t / nb;
+  const int b = static_cast<int>(t % nb);
+  const uint8_t *src = W + t * kBytes;
+  const int rs = row_bytes(QT == kTypeQ8_0 ? kTypeQ8_0R : kTypeQ6_KR, K);
+  uint8_t *dst = out + row * rs;
+  int end;  // end of the row's data sections
+  if constexpr (QT == kTypeQ8_0) {
+    for (int i = 0; i < 32; ++i) dst[32 * b + i] = src[2 + i];
+    dst[K + 2 * b] = src[0];
+    dst[K + 2 * b + 1] = src[1];
+    end = K + 2 * nb;
+  } else {
+    const int qh0 = K / 2, sc0 = qh0 + K / 4, d0 = sc0 + K / 16;
+    for (int i = 0; i < 128; ++i) dst[128 * b + i] = src[i];
+    for (int i = 0; i < 64; ++i) dst[qh0 + 64 * b + i] = src[128 + i];
+    for (int i = 0; i < 16; ++i) dst[sc0 + 16 * b + i] = src[192 + i];
+    dst[d0 + 2 * b] = src[208];
+    dst[d0 + 2 * b + 1] = src[209];
+    end = d0 + 2 * nb;
+  }
+  if (b == nb - 1)
+    for (int i = end; i < rs; ++i) dst[i] = 0;
+}
+
+hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, int K,
+                         hipStream_t stream) {
+  const int nb = K / (qtype == kTypeQ8_0 ? 32 : 256);
+  const int64_t n = n_rows * nb;
+  if (n == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  const uint8_t *w = static_cast<const uint8_t *>(W);
+  uint8_t *o = static_cast<uint8_t *>(out);
+  if (qtype == kTypeQ8_0) IFX_LAUNCH(k_repack, (kTypeQ8_0), grid, dim3(256), 0, stream, w, o, n_rows, K);
+  else if (qtype == kTypeQ6_K) IFX_LAUNCH(k_repack, (kTypeQ6_K), grid, dim3(256), 0, stream, w, o, n_rows, K);
+  else return hipErrorInvalidValue;
+  return last_error();
+}
+
 }  // namespace ifx

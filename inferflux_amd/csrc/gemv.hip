@@ -46,13 +46,16 @@ namespace ifx {
 // K8 = true: Q8_K (mmvq.cuh:1019-1070): slice s is codes 32(s&7).. of
 // super-block s>>3 (292 bytes: fp32 d, i8 qs[256], i16 bsums[16]); the
 // fp32 d is shared by the eight slices of a super-block.
-template <int MC, int R, bool K8 = false>
+// RS = true: the row-split Q8_0_R layout (ifx_common.h): codes at 32 s,
+// d at K + 2 s.
+template <int MC, int R, bool K8 = false, bool RS = false>
 __device__ __forceinline__ void q8_0_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
-                                           uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
+                                           uint32_t a_row, int mvalid, int s, float (&acc)[R][MC],
+                                           int K = 0) {
   i32x4 w0[R], w1[R];
   uint32_t dbits[R];
-  const uint32_t wo = K8 ? (s >> 3) * kQ8KBytes : s * kQ8_0Bytes;
-  const uint32_t qo = K8 ? wo + 4 + 32 * (s & 7) : wo + 2;
+  const uint32_t wo = RS ? K + 2 * s : K8 ? (s >> 3) * kQ8KBytes : s * kQ8_0Bytes;
+  const uint32_t qo = RS ? 32 * s : K8 ? wo + 4 + 32 * (s & 7) : wo + 2;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if constexpr (K8) dbits[r] = wload<uint32_t>(Wr[r], wo, rows[r]);
@@ -126,7 +129,8 @@ struct GemvArgs {
 // mode, wide slices, K <= 2048 so that one row needs at most 32 lanes):
 // lanes 0-31 and 32-63 own different sets of R rows.
 template <int QT, int MC>
-constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) || (QT == kTypeQ6_K && MC == 1);
+constexpr bool kWide = (QT == kTypeQ4_K && MC <= 2) ||
+                       ((QT == kTypeQ6_K || QT == kTypeQ6_KR) && MC == 1);
 
 // NORM = 1 / 2: the activations are produced in the kernel from an fp32 /
 // fp16 residual (RMSNorm then Q8_1, the standalone producer's exact
@@ -241,15 +245,19 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
     if constexpr (kWide<QT, MC> && QT == kTypeQ4_K)
       q4k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
     else if constexpr (kWide<QT, MC>)
-      q6k_wide<MC, R>(Wr, Ar, voff, soff, a_row, mvalid, s, acc);
+      q6k_wide<MC, R, QT == kTypeQ6_KR>(Wr, Ar, voff, soff, a_row, mvalid, s, acc, K);
     else if constexpr (QT == kTypeQ4_K)
       q4k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ5_K)
       q4k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
       q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ6_KR)
+      q6k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc, K);
     else if constexpr (QT == kTypeQ8_K)
       q8_0_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ8_0R)
+      q8_0_slice<MC, R, false, true>(Wrs, Ar, rows, a_row, mvalid, s, acc, K);
     else
       q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }
@@ -397,7 +405,7 @@ static int rows_env() {
 template <int QT, int MC>
 static int rows_per_wave(int N, int K) {
   if (rows_env()) return rows_env();
-  if constexpr (kWide<QT, MC> && QT == kTypeQ6_K) return 2;
+  if constexpr (kWide<QT, MC> && (QT == kTypeQ6_K || QT == kTypeQ6_KR)) return 2;
   if constexpr (kWide<QT, MC>) {
     const bool half = K / 64 <= 32;  // half-wave launch: a wave covers 2R rows
     if (N < 8192) return half ? 1 : MC;
@@ -471,6 +479,13 @@ static void launch_type(const GemvArgs &args, bool f16, hipStream_t s) {
   else launch_g<QT, 8, 4>(args, f16, s);
 }
 
+// The row-split layouts run at M <= 2 only (checked by the caller).
+template <int QT>
+static void launch_m12(const GemvArgs &args, bool f16, hipStream_t s) {
+  if (args.M == 1) launch_r<QT, 1>(args, f16, s);
+  else launch_r<QT, 2>(args, f16, s);
+}
+
 static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStream_t stream) {
   switch (qtype) {
   case kTypeQ4_K: launch_type<kTypeQ4_K>(args, f16, stream); break;
@@ -478,6 +493,8 @@ static hipError_t launch_args(int qtype, const GemvArgs &args, bool f16, hipStre
   case kTypeQ8_0: launch_type<kTypeQ8_0>(args, f16, stream); break;
   case kTypeQ5_K: launch_type<kTypeQ5_K>(args, f16, stream); break;
   case kTypeQ8_K: launch_type<kTypeQ8_K>(args, f16, stream); break;
+  case kTypeQ8_0R: launch_m12<kTypeQ8_0R>(args, f16, stream); break;
+  case kTypeQ6_KR: launch_m12<kTypeQ6_KR>(args, f16, stream); break;
   default: return hipErrorInvalidValue;
   }
   return last_error();
@@ -531,8 +548,12 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
       q4k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
     else if constexpr (QT == kTypeQ6_K)
       q6k_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ6_KR)
+      q6k_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc, K);
     else if constexpr (QT == kTypeQ8_K)
       q8_0_slice<MC, R, true>(Wrs, Ar, rows, a_row, mvalid, s, acc);
+    else if constexpr (QT == kTypeQ8_0R)
+      q8_0_slice<MC, R, false, true>(Wrs, Ar, rows, a_row, mvalid, s, acc, K);
     else
       q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }

@@ -63,6 +63,26 @@ constexpr int kQ6KBytes = 210;
 constexpr int kQ8_0Bytes = 34;
 constexpr int kQ8_1Bytes = 36;
 
+// Row-split layouts of this library (ifx_repack): each row's fields in
+// separate 16-byte-aligned sections instead of interleaved GGUF blocks, so
+// the M <= 2 GEMV reads them with aligned, fully used 16-byte loads.
+//   Q8_0_R  [qs: K bytes][d: K/32 fp16][pad to 16]
+//   Q6_K_R  [ql: K/2][qh: K/4][scales: K/16][d: K/256 fp16][pad to 16]
+// The values are the GGUF block's bytes, moved.
+constexpr int kTypeQ8_0R = 108;
+constexpr int kTypeQ6_KR = 114;
+
+// Bytes of one weight row of K values.
+__host__ __device__ constexpr int row_bytes(int qt, int K) {
+  return qt == kTypeQ4_K    ? (K >> 8) * kQ4KBytes
+         : qt == kTypeQ5_K  ? (K >> 8) * kQ5KBytes
+         : qt == kTypeQ6_K  ? (K >> 8) * kQ6KBytes
+         : qt == kTypeQ8_K  ? (K >> 8) * kQ8KBytes
+         : qt == kTypeQ8_0R ? ((K + (K >> 5) * 2 + 15) & ~15)
+         : qt == kTypeQ6_KR ? (((K >> 1) + (K >> 2) + (K >> 4) + (K >> 8) * 2 + 15) & ~15)
+                            : (K >> 5) * kQ8_0Bytes;
+}
+
 constexpr int kWave = 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

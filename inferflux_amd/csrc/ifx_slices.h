@@ -13,14 +13,6 @@
 namespace ifx {
 enum OutMode { kOutStore = 0, kOutAccum = 1, kOutBias = 2 };
 
-// Bytes of one weight row of K values.
-__host__ __device__ constexpr int row_bytes(int qt, int K) {
-  return qt == kTypeQ4_K   ? (K >> 8) * kQ4KBytes
-         : qt == kTypeQ5_K ? (K >> 8) * kQ5KBytes
-         : qt == kTypeQ6_K ? (K >> 8) * kQ6KBytes
-         : qt == kTypeQ8_K ? (K >> 8) * kQ8KBytes
-                           : (K >> 5) * kQ8_0Bytes;
-}
 
 // ---------------------------------------------------------------------------
 // Q4_K: slice j (0..7) of super-block b covers qs bytes 16j..16j+15, i.e.
@@ -263,20 +255,27 @@ __device__ __forceinline__ void q4k_wide(const rsrc_t Wr, rsrc_t Ar, const uint3
 // Q6_K: slice j of super-block b: group g = j >> 2, ql half cc = (j >> 1) & 1
 // (sub-blocks cc and cc + 2), values 16h..16h+15 (h = j & 1).
 // ---------------------------------------------------------------------------
-template <int MC, int R>
+// RS: the row-split Q6_K_R layout of a row of K values (ifx_common.h).
+template <int MC, int R, bool RS = false>
 __device__ __forceinline__ void q6k_slice(const rsrc_t (&Wr)[R], rsrc_t Ar, const uint32_t (&rows)[R],
-                                          uint32_t a_row, int mvalid, int s, float (&acc)[R][MC]) {
+                                          uint32_t a_row, int mvalid, int s, float (&acc)[R][MC],
+                                          int K = 0) {
   const int b = s >> 3, j = s & 7, g = j >> 2, cc = (j >> 1) & 1, h = j & 1;
   u32x4 ql[R], qh[R];
   u32x2 scw[R];
   uint16_t dbits[R];
   const uint32_t wo = b * kQ6KBytes;
+  const uint32_t qh0 = K >> 1, sc0 = qh0 + (K >> 2), d0 = sc0 + (K >> 4);
+  const uint32_t o_ql = RS ? b * 128 + g * 64 + cc * 32 + 16 * h : wo + g * 64 + cc * 32 + 16 * h;
+  const uint32_t o_qh = RS ? qh0 + b * 64 + g * 32 + 16 * h : wo + 128 + g * 32 + 16 * h;
+  const uint32_t o_sc = RS ? sc0 + b * 16 + g * 8 : wo + 192 + g * 8;
+  const uint32_t o_d = RS ? d0 + b * 2 : wo + 208;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    ql[r] = wload<u32x4>(Wr[r], wo + g * 64 + cc * 32 + 16 * h, rows[r]);
-    qh[r] = wload<u32x4>(Wr[r], wo + 128 + g * 32 + 16 * h, rows[r]);
-    scw[r] = wload<u32x2>(Wr[r], wo + 192 + g * 8, rows[r]);
-    dbits[r] = wload<uint16_t>(Wr[r], wo + 208, rows[r]);
+    ql[r] = wload<u32x4>(Wr[r], o_ql, rows[r]);
+    qh[r] = wload<u32x4>(Wr[r], o_qh, rows[r]);
+    scw[r] = wload<u32x2>(Wr[r], o_sc, rows[r]);
+    dbits[r] = wload<uint16_t>(Wr[r], o_d, rows[r]);
   }
   i32x4 xa[MC], xb[MC];
   float da[MC], db[MC];
@@ -352,11 +351,24 @@ struct Q6Wide {
   uint16_t dbits[R];
 };
 
-template <int R>
+// RS: the row-split Q6_K_R layout of a row of K values (ifx_common.h).
+template <int R, bool RS = false>
 __device__ __forceinline__ void q6k_wide_load(Q6Wide<R> &wt, const rsrc_t Wr,
                                               const uint32_t (&voff)[R], const uint32_t (&soff)[R],
-                                              int s) {
+                                              int s, int K = 0) {
   const int b = s >> 2, g = (s >> 1) & 1, h = s & 1;
+  if constexpr (RS) {
+    const uint32_t qh0 = K >> 1, sc0 = qh0 + (K >> 2), d0 = sc0 + (K >> 4);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wt.ql0[r] = wload<u32x4>(Wr, voff[r] + b * 128 + g * 64 + 16 * h, soff[r]);
+      wt.ql1[r] = wload<u32x4>(Wr, voff[r] + b * 128 + g * 64 + 32 + 16 * h, soff[r]);
+      wt.qh[r] = wload<u32x4>(Wr, voff[r] + qh0 + b * 64 + g * 32 + 16 * h, soff[r]);
+      wt.scw[r] = wload<u32x2>(Wr, voff[r] + sc0 + b * 16 + g * 8, soff[r]);
+      wt.dbits[r] = wload<uint16_t>(Wr, voff[r] + d0 + b * 2, soff[r]);
+    }
+    return;
+  }
   const uint32_t wo = b * kQ6KBytes;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -433,12 +445,12 @@ __device__ __forceinline__ void q6k_wide_compute(const Q6Wide<R> &wt, const AS &
   }
 }
 
-template <int MC, int R>
+template <int MC, int R, bool RS = false>
 __device__ __forceinline__ void q6k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
                                          const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
-                                         int s, float (&acc)[R][MC]) {
+                                         int s, float (&acc)[R][MC], int K = 0) {
   Q6Wide<R> wt;
-  q6k_wide_load<R>(wt, Wr, voff, soff, s);
+  q6k_wide_load<R, RS>(wt, Wr, voff, soff, s, K);
   q6k_wide_compute<MC, R>(wt, AGlobal{Ar, a_row}, mvalid, s, acc);
 }
 

@@ -19,6 +19,7 @@ Entry kinds:
 Kernel names: include/ifx_qgemm.h, ifx_launch_log_begin.
 """
 Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0_R, Q6_K_R = 108, 114  # row-split copies (ifx_repack) of Q8_0 / Q6_K rows
 
 # 3B: hidden 2048, Q/K/V 2048/256/256, FFN 11008; 14B: hidden 5120, Q/K/V
 # 5120/1024/1024, FFN 13824 (inferflux_amd/workloads.py)
@@ -34,6 +35,7 @@ LAUNCHES = [
     ("c2_o_m1", "gemv_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2>"]),
     ("c2_gate_up_m1", "grouped", Q4_K, 1, (11008, 11008), 2048, ["k_gemv<12,1,2,1,4,0,2>"]),
     ("c2_down_m1", "gemv_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<14,1,2,3,1,0,1>"]),
+    ("c2_down_r_m1", "gemv_accum", Q6_K_R, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1>"]),
     ("c2_qkv_m4", "grouped", Q4_K, 4, QKV3, 2048, ["k_mmvq<12,1,8,0>"]),
     ("c2_o_m4", "gemv_accum", Q4_K, 4, (2048,), 2048, ["k_mmvq<12,1,8,0>"]),
     ("c2_gate_up_m4", "grouped", Q4_K, 4, (11008, 11008), 2048, ["k_gemv_lds<4,2,2,8,0>"]),
@@ -52,6 +54,8 @@ LAUNCHES = [
     ("c3_q8_0_m8", "gemv", Q8_0, 8, (151936,), 2048, ["k_mmvq<8,1,1,0>"]),
     ("c3_q6_k_m1", "gemv", Q6_K, 1, (151936,), 2048, ["k_gemv<14,1,2,1,4,0,2>"]),
     ("c3_q6_k_m8", "gemv", Q6_K, 8, (151936,), 2048, ["k_gemv_slot<14,8,1,0,0>"]),
+    ("c3_q8_0_r_m1", "gemv", Q8_0_R, 1, (151936,), 2048, ["k_gemv<108,1,4,1,4,0,1>"]),
+    ("c3_q6_k_r_m1", "gemv", Q6_K_R, 1, (151936,), 2048, ["k_gemv<114,1,2,1,4,0,2>"]),
     # config 4: the 14B decode layer at M = 16 / 32, and its Q4_K launches at M = 1 / 8
     ("c4_qkv_m16", "grouped", Q4_K, 16, QKV14, 5120, ["k_mmvq<12,1,8,0>"]),
     ("c4_o_m16", "gemv_accum", Q4_K, 16, (5120,), 5120, ["k_mmvq<12,1,8,0>"]),

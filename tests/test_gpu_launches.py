@@ -31,8 +31,11 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     from inferflux_amd import ops, synth
     note(f"launch {lid}: {entry} type={qt} M={M} N={Ns} K={K} -> {want}")
     seed = sum(Ns) + K + M
-    ws = [synth.blocks(qt, n, K, seed=seed + i) for i, n in enumerate(Ns)]
+    raw_qt = {108: 8, 114: 14}.get(qt, qt)  # row-split types: repack raw blocks on the GPU
+    ws = [synth.blocks(raw_qt, n, K, seed=seed + i) for i, n in enumerate(Ns)]
     W = [up(w, dev) for w in ws]
+    if raw_qt != qt:
+        W = [ops.repack(raw_qt, w, n, K)[1] for w, n in zip(W, Ns)]
     rng = np.random.default_rng(seed)
     outl = 0.01 if entry.startswith("prefill") else 0.0
     x = synth.activations(M, K, seed=seed + 7, outlier_frac=outl)
@@ -94,7 +97,7 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
 
     for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):
         idx = _rows(n, seed + i)
-        ye = orc.gemv_exact(qt, w[idx], a, M, len(idx), K)
+        ye = orc.gemv_exact(raw_qt, w[idx], a, M, len(idx), K)
         if entry in ("gemv_accum", "quantize_accum"):
             ye = ye + base[:, idx]
         yd = down(y)
