@@ -168,6 +168,9 @@ def main():
         fused == "ffn": QKV with the fused RMSNorm, then ifx_decode_ffn: O
         with the fused quantizer and one grid-synchronised launch for
         RMSNorm, gate/up + SiLU and down (M = 1): 3 launches.
+        fused == "batch_swiglu" (any M <= 8): the Q8_1 producers as launches of
+        their own, except SiLU * up + Q8_1, which the gate/up launch computes
+        (ifx_qgemv_gate_up_silu): 3 producers + 4 GEMVs.
         split_down: the down projection reads a row-split copy of its Q6_K
         weights (ifx_repack, M <= 2).
         run(i, which) runs one launch kind alone ("qkv", "o", "gate_up",
@@ -232,6 +235,26 @@ def main():
                     gemv_norm("o", r, attn, None)
                 elif which == "ffn":
                     ffn_block(r, with_o=False)
+                return
+            if fused == "batch_swiglu":
+                prod = which is None or which == "producers"
+                if prod:
+                    ops.rmsnorm_quantize_q8_1(resid, norm_w["attn"], out=A["attn_in"])
+                if which is None or which == "qkv":
+                    gemv("qkv", r)
+                if prod:
+                    ops.quantize_q8_1(attn, out=A["attn_out"])
+                if which is None or which == "o":
+                    gemv("o", r)
+                if prod:
+                    ops.rmsnorm_quantize_q8_1(resid, norm_w["ffn"], out=A["ffn_in"])
+                if which is None or which == "gate_up":
+                    qt, N, K, _ = layer["gate"]
+                    ops.qgemv_gate_up_silu(qt, layer["gate"][3][r], layer["up"][3][r],
+                                           A["ffn_in"], M, N, K, want_h=False,
+                                           q8_1_out=A["ffn_act"])
+                if which is None or which == "down":
+                    gemv("down", r)
                 return
             prod = which is None or which == "producers"
             if prod and not fused:
@@ -335,6 +358,17 @@ def main():
             "kernel_us": {k: round(v, 2) for k, v in kern.items()},
             "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_layer * 1e-6), 1),
         }
+        if M > 2:
+            # SiLU * up + Q8_1 in the epilogue of the gate/up launch
+            runb = decode_layer_runner(layer3b, M, seed=10 + M, fused="batch_swiglu")
+            us_b = time_loop(runb, steps, args.warmup)
+            per_m[M]["fused_swiglu"] = {
+                "us_per_layer": round(us_b, 2),
+                "layer_GBs": round(layer_alg_bytes[M] / us_b / 1e3, 1),
+                "kernel_us": {n: round(time_loop(lambda i, n=n: runb(i, n), steps, args.warmup), 2)
+                              for n in ("qkv", "o", "gate_up", "down", "producers")},
+                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_b * 1e-6), 1),
+            }
         if M == 1:
             fb = form_kernel_bytes(layer3b, M, "reference")
             forms["reference"] = (run, us_layer, {k: kern[k] for k in fb}, fb)

@@ -67,6 +67,9 @@ hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, fl
                              const void *Wd, void *workspace, int q_dim, int hidden, int ffn,
                              hipStream_t s);
 bool gemv_slot_fits(int qtype, int M, int K);
+hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
+                                   void *H, bool f16h, void *Q, int M, int N, int K,
+                                   hipStream_t stream);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
                             int mode, hipStream_t stream);
@@ -455,16 +458,22 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   if (!W_gate || !W_up || !A_q8_1 || (!H && !q8_1_out)) return IFX_NULL_POINTER;
   if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
-  // the fused kernel serves the decode batch M <= 2 and whole Q8_1 blocks
-  // of outputs; other shapes take the grouped GEMV + SiLU producer
+  // the fused kernels serve the decode batch (M <= 2: the v_dot4 GEMV;
+  // 3 <= M <= 8, Q4_K / Q6_K: the slot-packed MFMA GEMV) and whole Q8_1
+  // blocks of outputs; other shapes take the grouped GEMV + SiLU producer
   const int max_m = (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
-  if (M < 1 || M > max_m || N % 32 != 0) return IFX_BAD_GEOMETRY;
+  const bool slot = M > max_m && ifx::gemv_slot_fits(quant_type, M, K);
+  if (M < 1 || (M > max_m && !slot) || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)
   void *probe_out = H ? H : q8_1_out;
   const int rc = check_gemm_args(quant_type, W_gate, A_q8_1, probe_out, IFX_OUT_F32, IFX_STORE,
                                  nullptr, M, N, K);
   if (rc != IFX_OK) return rc;
+  if (slot)
+    return status_of(ifx::launch_gemv_slot_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
+                                                  h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
+                                                  static_cast<hipStream_t>(stream)));
   return status_of(ifx::launch_gemv_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
                                            h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
                                            static_cast<hipStream_t>(stream)));

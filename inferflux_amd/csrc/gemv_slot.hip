@@ -45,7 +45,7 @@
 // The Q8_1 d (and s) of the current super-block go through a 1 KB per-wave
 // LDS table, since the rescaling lanes need those of other lanes' rows.
 // Grouped launches: up to three projections that share A.
-#include "ifx_common.h"
+#include "ifx_q8_1.h"
 
 #include <stdlib.h>
 
@@ -64,6 +64,10 @@ struct SlotArgs {
   int nseg;
   const uint8_t *A;
   int M, K, mode;
+  // fused gate/up/SiLU (SW): seg[0] gate, seg[1] up; h = silu(g) * u to H
+  // (fp32, fp16 with F16OUT, or none) and its Q8_1 blocks to Q (or none)
+  void *H;
+  uint8_t *Q;
 };
 
 namespace {
@@ -167,34 +171,49 @@ __device__ __forceinline__ i32x4 w_operand(const WSb<QT> &w, int j) {
 
 }  // namespace
 
-template <int QT, int MP, int KW>
+// NP: projections per workgroup (2 for the fused gate/up/SiLU launch).
+template <int QT, int MP, int KW, int NP = 1>
 constexpr int slot_lds_bytes() {
-  constexpr int table = KW * 2 * 8 * MP * 4;                     // per-wave d and s tables
-  constexpr int red = (KW > 1 ? KW - 1 : 0) * 64 * (MP / 2) * 4;  // partial results
-  return table + red;
+  constexpr int table = NP * KW * 2 * 8 * MP * 4;                     // per-wave d and s tables
+  constexpr int red = NP * (KW > 1 ? KW - 1 : 0) * 64 * (MP / 2) * 4;  // partial results
+  constexpr int gu = NP == 2 ? 2 * MP * 32 * 4 : 0;                    // gate/up outputs
+  return table + red + gu;
 }
 
-template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC>
-__global__ __launch_bounds__(64 * KW) void k_gemv_slot(const SlotArgs args) {
+// SW: fused gate/up/SiLU (the reference's FusedGateUpSiluGemvQ8_1,
+// mmvq.cuh:1686-2030, for decode batches up to 8): a workgroup of 2 KW waves
+// owns 32 outputs, waves [0, KW) the gate rows and [KW, 2 KW) the up rows,
+// each half exactly as a grouped slot launch of KW waves computes them; then
+// one wave forms h = silu(g) * u (the SiLU producer's arithmetic) and
+// quantizes each batch row's 32 values into one Q8_1 block, so h and its
+// blocks equal grouped GEMV + silu_mul_quantize bit for bit where the
+// grouped launch runs the same KW (other KW add the super-blocks' partial
+// sums in another order).
+template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool SW = false>
+__global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const SlotArgs args) {
   using G = SlotGeo<QT, MP>;
   constexpr int NM = G::kNm;
+  static_assert(!(SW && ATOMIC), "the fused gate/up/SiLU launch does not split K");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int bx = blockIdx.x;
-  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int proj = SW ? wave_all / KW : 0;  // SW: 0 gate, 1 up
+  const int wave = SW ? wave_all % KW : wave_all;  // wave within its projection
+  const int si = SW ? proj
+                 : (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
                  : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
   const SlotSeg &sg = args.seg[si];
   const int N = sg.N, M = args.M, K = args.K;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c32 = lane & 31, h = lane >> 5;
-  const int n0 = (bx - sg.blk_begin) * 32;
+  const int n0 = SW ? bx * 32 : (bx - sg.blk_begin) * 32;
   const int nsb = K >> 8;
   constexpr int kSbBytes = (QT == kTypeQ4_K) ? kQ4KBytes : kQ6KBytes;
   const uint32_t w_row = static_cast<uint32_t>(nsb) * kSbBytes;
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
   const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(N));
   const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
-  float *dl = reinterpret_cast<float *>(smem) + wave * (2 * 8 * MP);  // [8][MP] d
+  float *dl = reinterpret_cast<float *>(smem) + wave_all * (2 * 8 * MP);  // [8][MP] d
   float *sl = dl + 8 * MP;                                            // [8][MP] s
 
   const uint32_t w_voff = static_cast<uint32_t>(min(n0 + c32, N - 1)) * w_row;
@@ -334,18 +353,55 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_slot(const SlotArgs args) {
     }
   }
 
+  constexpr int kNp = SW ? 2 : 1;
   if constexpr (KW > 1) {
-    float *red = reinterpret_cast<float *>(smem) + KW * 2 * 8 * MP;  // [KW-1][NM][64]
+    float *red = reinterpret_cast<float *>(smem) + kNp * KW * 2 * 8 * MP +
+                 proj * (KW - 1) * NM * 64;  // [KW-1][NM][64] per projection
     if (wave > 0) {
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) red[((wave - 1) * NM + mi) * 64 + lane] = acc[mi];
     }
     __syncthreads();
-    if (wave > 0) return;
+    if (!SW && wave > 0) return;
+    if (wave == 0) {
 #pragma unroll
-    for (int w = 0; w < KW - 1; ++w)
+      for (int w = 0; w < KW - 1; ++w)
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi) acc[mi] += red[(w * NM + mi) * 64 + lane];
+        for (int mi = 0; mi < NM; ++mi) acc[mi] += red[(w * NM + mi) * 64 + lane];
+    }
+  }
+  if constexpr (SW) {
+    // gate/up outputs [projection][batch row][output], then h and Q8_1
+    float *gu = reinterpret_cast<float *>(smem) + kNp * KW * 2 * 8 * MP +
+                kNp * (KW > 1 ? KW - 1 : 0) * NM * 64;
+    if (wave == 0) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        const int m = 2 * (mi & ~3) + 4 * h + (mi & 3);
+        gu[(proj * MP + m) * 32 + c32] = acc[mi];
+      }
+    }
+    __syncthreads();
+    const int m = threadIdx.x >> 3, l = threadIdx.x & 7;  // wave 0: 8 lanes per batch row
+    if (threadIdx.x < 64 && m < M) {
+      const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[m * 32 + 4 * l]);
+      const f32x4 u4 = *reinterpret_cast<const f32x4 *>(&gu[(MP + m) * 32 + 4 * l]);
+      const f32x4 hv = silu_mul4(g4, u4);
+      const int64_t o = static_cast<int64_t>(m) * N + n0 + 4 * l;
+      if (args.H) {
+        if constexpr (F16OUT) {
+          const u32x2 hh = {f2h_bits(hv.x) | (f2h_bits(hv.y) << 16),
+                            f2h_bits(hv.z) | (f2h_bits(hv.w) << 16)};
+          *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(args.H) + o) = hh;
+        } else {
+          *reinterpret_cast<f32x4 *>(static_cast<float *>(args.H) + o) = hv;
+        }
+      }
+      if (args.Q)
+        quantize4_store(hv.x, hv.y, hv.z, hv.w,
+                        args.Q + (static_cast<int64_t>(m) * (N >> 5) + bx) * kQ8_1Bytes, l);
+    }
+    return;
   }
   const int n = n0 + c32;
   if (n >= N) return;
@@ -454,6 +510,33 @@ void slot_q(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
 
 }  // namespace
 
+// The fused gate/up/SiLU launch: 4 waves per projection and workgroup, no
+// K split (one workgroup per 32 outputs).  Measured on MI355X against 1, 2
+// and 8 waves (3B gate/up 11008 x 2048 at M = 3 / 4 / 8: 10.9 / 10.9 / 11.7 us
+// against 12.4 / 12.4 / 13.1 with 8; 14B 13824 x 5120 at M = 8: 24.4 against
+// 27.1).  With fewer than 4 super-blocks per row the waves match them.
+// IFX_SLOT_KW overrides, as for the plain launch.
+template <int QT, int KW>
+void slot_swiglu_launch(const SlotArgs &args, bool f16h, hipStream_t s) {
+  constexpr int lds = slot_lds_bytes<QT, 8, KW, 2>();
+  const dim3 grid(args.seg[0].N / 32);
+  if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true), grid, dim3(128 * KW), lds, s, args);
+  else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true), grid, dim3(128 * KW), lds, s, args);
+}
+
+template <int QT>
+void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
+  int kw = 4, ks = 1;
+  if (getenv("IFX_SLOT_KW")) choose_slot_work(1 << 20, args.K >> 8, false, kw, ks);
+  while (kw > 1 && kw > (args.K >> 8)) kw /= 2;
+  switch (kw) {
+  case 1: slot_swiglu_launch<QT, 1>(args, f16h, s); break;
+  case 2: slot_swiglu_launch<QT, 2>(args, f16h, s); break;
+  case 4: slot_swiglu_launch<QT, 4>(args, f16h, s); break;
+  default: slot_swiglu_launch<QT, 8>(args, f16h, s); break;
+  }
+}
+
 bool gemv_slot_fits(int qtype, int M, int K) {
   return (qtype == kTypeQ4_K || qtype == kTypeQ6_K) && M >= 1 && M <= 8 && K % 256 == 0 && K > 0;
 }
@@ -477,6 +560,28 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
   args.mode = mode;
   if (qtype == kTypeQ4_K) slot_q<kTypeQ4_K>(args, blocks, f16, stream);
   else slot_q<kTypeQ6_K>(args, blocks, f16, stream);
+  return last_error();
+}
+
+// Fused gate/up/SiLU for 1 <= M <= 8 (Q4_K / Q6_K, K % 256 == 0, N % 32 == 0;
+// checked by the caller): H (fp32 / fp16 with f16h, or NULL) and / or the
+// Q8_1 blocks Q (or NULL).
+hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
+                                   void *H, bool f16h, void *Q, int M, int N, int K,
+                                   hipStream_t stream) {
+  if (!gemv_slot_fits(qtype, M, K) || N % 32 != 0) return hipErrorInvalidValue;
+  SlotArgs args{};
+  args.seg[0] = SlotSeg{static_cast<const uint8_t *>(Wg), nullptr, nullptr, N, 0};
+  args.seg[1] = SlotSeg{static_cast<const uint8_t *>(Wu), nullptr, nullptr, N, 0};
+  args.nseg = 2;
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = 0;
+  args.H = H;
+  args.Q = static_cast<uint8_t *>(Q);
+  if (qtype == kTypeQ4_K) slot_swiglu_q<kTypeQ4_K>(args, f16h, stream);
+  else slot_swiglu_q<kTypeQ6_K>(args, f16h, stream);
   return last_error();
 }
 

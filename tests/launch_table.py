@@ -14,6 +14,7 @@ Entry kinds:
   grouped_rmsnorm     ifx_qgemv_grouped_rmsnorm (RMSNorm + Q8_1 fused in), store
   quantize_accum      ifx_qgemv_grouped_rmsnorm with norm_weight NULL (Q8_1 fused in), accumulate
   gate_up_silu_rmsnorm  ifx_qgemv_gate_up_silu_rmsnorm (Q8_1 output of silu(gate)*up)
+  gate_up_silu        ifx_qgemv_gate_up_silu (Q8_1 output of silu(gate)*up)
   prefill             ifx_qgemm_prefill
   prefill_int8        ifx_qgemm_prefill_kernel(IFX_PREFILL_INT8)
 Kernel names: include/ifx_qgemm.h, ifx_launch_log_begin.
@@ -44,6 +45,9 @@ LAUNCHES = [
     ("c2_o_m8", "gemv_accum", Q4_K, 8, (2048,), 2048, ["k_mmvq<12,1,8,0>"]),
     ("c2_gate_up_m8", "grouped", Q4_K, 8, (11008, 11008), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c2_down_m8", "gemv_accum", Q6_K, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,1>"]),
+    # config 2 at M = 4 / 8 with SiLU * up + Q8_1 in the gate/up epilogue
+    ("c2s_gate_up_m4", "gate_up_silu", Q4_K, 4, (11008,), 2048, ["k_gemv_slot<12,8,4,0,0,1>"]),
+    ("c2s_gate_up_m8", "gate_up_silu", Q4_K, 8, (11008,), 2048, ["k_gemv_slot<12,8,4,0,0,1>"]),
     # config 2, the fused layer form the benchmark's step uses at M = 1
     ("c2f_qkv_m1", "grouped_rmsnorm", Q4_K, 1, QKV3, 2048, ["k_gemv<12,1,1,1,4,0,2,1>"]),
     ("c2f_o_m1", "quantize_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2,3>"]),

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from tests.launch_table import IDS, LAUNCHES
-from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, up
+from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, same_slot_waves, up
 
 pytestmark = pytest.mark.gpu
 
@@ -71,6 +71,9 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
             wu = synth.blocks(qt, Ns[0], K, seed=seed + 11)
             h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], up(wu, dev), X, NW, M, Ns[0], K,
                                                   eps=1e-6)
+        elif entry == "gate_up_silu":
+            wu = synth.blocks(qt, Ns[0], K, seed=seed + 11)
+            h, q = ops.qgemv_gate_up_silu(qt, W[0], up(wu, dev), A, M, Ns[0], K)
         elif entry == "prefill":
             outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, prefill=True)]
         elif entry == "prefill_int8":
@@ -80,19 +83,23 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         torch.cuda.synchronize()
     assert lg.kernels == want
 
-    if entry == "gate_up_silu_rmsnorm":
+    if entry in ("gate_up_silu_rmsnorm", "gate_up_silu"):
         N = Ns[0]
         blocks = np.random.default_rng(seed).choice(N // 32, 16, replace=False)
         idx = (blocks[:, None] * 32 + np.arange(32)[None, :]).ravel()
         g = orc.gemv_exact(qt, ws[0][idx], a, M, len(idx), K)
         u = orc.gemv_exact(qt, wu[idx], a, M, len(idx), K)
-        h_ref = g / (1.0 + np.exp(-g)) * u
+        with np.errstate(over="ignore"):
+            h_ref = g / (1.0 + np.exp(-g)) * u
         check_rows(down(h)[:, idx], h_ref)
-        qb = down(q).reshape(M, N // 32, 36)[:, blocks].reshape(M, -1)
-        check_q8_1_close(qb, orc.quantize_q8_1(h_ref.astype(np.float32)), h_ref)
+        # the Q8_1 blocks are the exact quantization of the device's h
+        assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
         # the chain it replaces: grouped GEMV + SiLU producer, bit for bit
-        g2, u2 = ops.qgemv_grouped(qt, [W[0], up(wu, dev)], A, M, [N, N], K)
-        assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
+        # where the grouped launch forms the sums in the same order
+        with ops.launch_log() as lg2:
+            g2, u2 = ops.qgemv_grouped(qt, [W[0], up(wu, dev)], A, M, [N, N], K)
+        if entry == "gate_up_silu_rmsnorm" or same_slot_waves(lg2.kernels[-1], want[0]):
+            assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
         return
 
     for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):

@@ -41,6 +41,17 @@ def note(msg):
     print(msg, flush=True)
 
 
+def same_slot_waves(grouped, fused):
+    """True when a grouped launch and the fused gate/up/SiLU launch are both
+    slot-packed MFMA GEMVs with the same waves per projection (the third
+    template argument), i.e. they add the same partial sums in one order."""
+    def waves(name):
+        if not name.startswith("k_gemv_slot<"):
+            return None
+        return name[len("k_gemv_slot<"):-1].split(",")[2]
+    return waves(grouped) is not None and waves(grouped) == waves(fused)
+
+
 def check_rows(y, ye, tol=TOL):
     y = np.asarray(y, np.float64)
     err = np.abs(y - ye).max(axis=1)
@@ -768,15 +779,57 @@ def test_gate_up_silu_rmsnorm_not_handled(dev):
 
 
 def test_gate_up_silu_not_handled(dev):
-    """M > 2 or N % 32 != 0: not handled (positive status), nothing launched."""
+    """M > 8, M > 2 for types without the slot kernel, or N % 32 != 0: not
+    handled (positive status), nothing launched."""
     import torch
     from inferflux_amd import ops
     w = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
-    a = torch.zeros(1 << 12, dtype=torch.uint8, device=dev)
-    with pytest.raises(ops.NotHandled):
-        ops.qgemv_gate_up_silu(Q4_K, w, w, a, 3, 32, 256)
-    with pytest.raises(ops.NotHandled):
-        ops.qgemv_gate_up_silu(Q8_0, w, w, a, 1, 20, 32)
+    a = torch.zeros(1 << 14, dtype=torch.uint8, device=dev)
+    with ops.launch_log() as lg:
+        for qt, M, N, K in ((Q4_K, 9, 32, 256), (Q8_0, 3, 32, 256), (Q8_0, 1, 20, 32),
+                            (Q6_K, 4, 48, 256)):
+            with pytest.raises(ops.NotHandled):
+                ops.qgemv_gate_up_silu(qt, w, w, a, M, N, K)
+    assert lg.kernels == []
+
+
+@pytest.mark.parametrize("qtype,M,N,K", [(Q4_K, 8, 11008, 2048), (Q4_K, 5, 11008, 2048),
+                                         (Q4_K, 4, 11008, 2048), (Q4_K, 3, 96, 512),
+                                         (Q6_K, 6, 64, 2048), (Q6_K, 8, 8192, 1024),
+                                         (Q4_K, 7, 13824, 5120)])
+def test_gate_up_silu_batch(orc, dev, qtype, M, N, K):
+    """3 <= M <= 8 on the slot-packed MFMA GEMV with the SiLU / Q8_1
+    epilogue: within the bar of the oracle, and bit for bit the grouped
+    GEMV + SiLU producer wherever the grouped launch runs the same kernel."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gate_up_silu batch type={qtype} M={M} N={N} K={K}")
+    wg = synth.blocks(qtype, N, K, seed=N + 3)
+    wu = synth.blocks(qtype, N, K, seed=N + 4)
+    x = synth.activations(M, K, seed=K + M, outlier_frac=0.01) * 0.1  # h well inside fp16
+    a = orc.quantize_q8_1(x)
+    Wg, Wu, A = up(wg, dev), up(wu, dev), up(a, dev)
+    with ops.launch_log() as lg:
+        h, q = ops.qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K)
+    assert len(lg.kernels) == 1 and lg.kernels[0].startswith("k_gemv_slot<")
+    idx = np.unique(np.random.default_rng(N).choice(N // 32, 24)) * 32
+    idx = (idx[:, None] + np.arange(32)[None, :]).ravel()  # whole Q8_1 blocks
+    g_ref = orc.gemv_exact(qtype, wg[idx], a, M, len(idx), K)
+    u_ref = orc.gemv_exact(qtype, wu[idx], a, M, len(idx), K)
+    h_ref = g_ref / (1.0 + np.exp(-g_ref)) * u_ref
+    check_rows(down(h)[:, idx], h_ref)
+    # the Q8_1 blocks are the exact quantization of the device's h
+    assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
+    with ops.launch_log() as lg2:
+        g, u = ops.qgemv_grouped(qtype, [Wg, Wu], A, M, [N, N], K)
+    if same_slot_waves(lg2.kernels[-1], lg.kernels[0]):
+        assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g, u)))
+        np.testing.assert_allclose(down(h), orc.silu_mul_values(down(g), down(u)), rtol=1e-6,
+                                   atol=1e-30)
+    h16, none = ops.qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, want_q8_1=False,
+                                       h_dtype=torch.float16)
+    assert none is None
+    assert np.array_equal(down(h16), down(h).astype(np.float16))
 
 
 def test_gemv_only_types_not_handled(dev):
