@@ -40,7 +40,13 @@ enum ifx_quant_type {
    * id): each row's block fields in separate 16-byte-aligned sections.
    * ifx_qgemv / ifx_qgemv_grouped at M <= 2 only. */
   IFX_TYPE_Q8_0_R = 108, /* [qs: K bytes][d: K/32 fp16][pad to 16] per row */
-  IFX_TYPE_Q6_K_R = 114  /* [ql: K/2][qh: K/4][scales: K/16][d: K/256 fp16][pad to 16] */
+  IFX_TYPE_Q6_K_R = 114, /* [ql: K/2][qh: K/4][scales: K/16][d: K/256 fp16][pad to 16] */
+  /* The tiled layouts ifx_repack_tiled writes (this library's own): rows in
+   * groups of 32, one tile per group and super-block holding the group's
+   * super-blocks in the byte order of the MFMA batch kernels' loads.
+   * ifx_qgemv / ifx_qgemv_grouped / ifx_qgemv_gate_up_silu at M <= 32. */
+  IFX_TYPE_Q4_K_T = 212, /* 4608-byte tiles: 32 headers, then qs in 16-byte pieces */
+  IFX_TYPE_Q6_K_T = 214  /* 6720-byte tiles: ql, qh pieces, 32 x scales, 32 x d */
 };
 
 enum ifx_status {
@@ -290,6 +296,25 @@ int64_t ifx_repacked_bytes(int quant_type, int64_t n_rows, int K);
  * (BuildDownProjMmqLayout / transform_downproj_mmq_layout,
  * fused_quant_gemm.h:213-234, fused_quant_gemm.cu:573-596, 1966-2032). */
 int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K, void *stream);
+
+/* Bytes of the tiled copy of n_rows x K Q4_K or Q6_K weights: whole groups
+ * of 32 rows (0 for another type or K % 256 != 0). */
+int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K);
+
+/* Load-time repack of raw GGUF Q4_K / Q6_K rows into the tiled layout
+ * IFX_TYPE_Q4_K_T / IFX_TYPE_Q6_K_T (W_out: ifx_tiled_bytes, caller owned,
+ * 16-byte aligned; the rows of a last partial group are written as zeros).
+ * The batch kernels (slot-packed int8 MFMA at M <= 8, fp16-dequant MFMA at
+ * 9 <= M <= 32) give each lane one weight row, so on raw rows every load
+ * instruction touches 32 rows; on tiles it reads one contiguous kilobyte
+ * (3B gate 11008 x 2048 at M = 8: 5.7 against 6.8 us; Q6_K down 2048 x
+ * 11008: 8.2 against 12.5 us).  Sums are the raw layout's, bit for bit, for
+ * the same kernel and split.  The copy serves M <= 32 only (not the M <= 2
+ * v_dot4 GEMV, not the prefill GEMM).  Like the row-split copy, it plays
+ * the role of the reference's load-time MMQ re-tiling (BuildDownProjMmqLayout,
+ * fused_quant_gemm.h:213-234, fused_quant_gemm.cu:573-596, 1966-2032). */
+int ifx_repack_tiled(int quant_type, const void *W, void *W_out, int64_t n_rows, int K,
+                     void *stream);
 
 /* Whole-tensor dequantization of n_rows x K weights to fp32 or fp16.
  * Replaces dequantize_q4_k / dequantize_q6_k / dequantize_q8_0

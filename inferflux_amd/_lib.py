@@ -34,6 +34,8 @@ SIGNATURES = {
     "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_repacked_bytes": ([_i32, _i64, _i32], _i64),
     "ifx_repack": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
+    "ifx_tiled_bytes": ([_i32, _i64, _i32], _i64),
+    "ifx_repack_tiled": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_launch_log_begin": ([_i32], None),

@@ -61,6 +61,8 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
 hipError_t scratch_address(void **out);
 hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, int K,
                          hipStream_t stream);
+hipError_t launch_repack_tiled(int qtype, const void *W, void *out, int64_t n_rows, int K,
+                               hipStream_t stream);
 bool decode_ffn_fits(int hidden, int ffn);
 hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, float *resid,
                              const uint16_t *norm_w, float eps, const void *Wg, const void *Wu,
@@ -222,15 +224,24 @@ bool gemv_only(int t) { return t == IFX_TYPE_Q5_K || t == IFX_TYPE_Q8_K; }
 // the row-split layouts of ifx_repack: the v_dot4 GEMV at M <= 2 only
 bool row_split(int t) { return t == IFX_TYPE_Q8_0_R || t == IFX_TYPE_Q6_K_R; }
 constexpr int kMaxRowSplitM = 2;
+// the tiled layouts of ifx_repack_tiled: the MFMA batch GEMVs, M <= 32
+bool tiled(int t) { return t == IFX_TYPE_Q4_K_T || t == IFX_TYPE_Q6_K_T; }
+constexpr int kMaxTiledM = 32;
+constexpr int kMaxSlotM = 8;
+// a layout of this library, served by some entry points only
+bool repacked(int t) { return row_split(t) || tiled(t); }
 
 bool is_weight_type(int t) {
   return t == IFX_TYPE_Q4_K || t == IFX_TYPE_Q6_K || t == IFX_TYPE_Q8_0 || gemv_only(t) ||
-         row_split(t);
+         repacked(t);
 }
 
-// Bytes of an N x K weight tensor (0 for an unknown type).
+// Bytes of an N x K weight tensor (0 for an unknown type); tiled tensors
+// hold whole groups of 32 rows.
 uint64_t weight_bytes(int t, int N, int K) {
-  return ifx_block_elems(t) ? static_cast<uint64_t>(N) * ifx::row_bytes(t, K) : 0;
+  if (!ifx_block_elems(t)) return 0;
+  const uint64_t rows = tiled(t) ? (static_cast<uint64_t>(N) + 31) / 32 * 32 : N;
+  return rows * ifx::row_bytes(t, K);
 }
 
 int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int out_dtype,
@@ -244,6 +255,7 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   if (K % ifx_block_elems(quant_type) != 0) return IFX_BAD_GEOMETRY;
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return IFX_BAD_GEOMETRY;
   if (row_split(quant_type) && M > kMaxRowSplitM) return IFX_BAD_GEOMETRY;
+  if (tiled(quant_type) && M > kMaxTiledM) return IFX_BAD_GEOMETRY;
   // Kernels address W and A with 32-bit byte offsets (buffer loads).
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
   const uint64_t w_bytes = weight_bytes(quant_type, N, K);
@@ -265,7 +277,8 @@ int ifx_block_bytes(int quant_type) {
   case IFX_TYPE_Q8_0: return ifx::kQ8_0Bytes;
   case IFX_TYPE_Q8_1: return ifx::kQ8_1Bytes;
   case IFX_TYPE_Q8_0_R: return ifx::kQ8_0Bytes;
-  case IFX_TYPE_Q6_K_R: return ifx::kQ6KBytes;
+  case IFX_TYPE_Q6_K_R: case IFX_TYPE_Q6_K_T: return ifx::kQ6KBytes;
+  case IFX_TYPE_Q4_K_T: return ifx::kQ4KBytes;
   default: return 0;
   }
 }
@@ -273,7 +286,7 @@ int ifx_block_bytes(int quant_type) {
 int ifx_block_elems(int quant_type) {
   switch (quant_type) {
   case IFX_TYPE_Q4_K: case IFX_TYPE_Q5_K: case IFX_TYPE_Q6_K: case IFX_TYPE_Q8_K:
-  case IFX_TYPE_Q6_K_R: return 256;
+  case IFX_TYPE_Q6_K_R: case IFX_TYPE_Q4_K_T: case IFX_TYPE_Q6_K_T: return 256;
   case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: case IFX_TYPE_Q8_0_R: return 32;
   default: return 0;
   }
@@ -296,6 +309,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % ifx_block_elems(quant_type)) return 0;
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return 0;
   if (row_split(quant_type) && M > kMaxRowSplitM) return 0;
+  if (tiled(quant_type) && M > kMaxTiledM) return 0;
   if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
   const uint64_t w_bytes = weight_bytes(quant_type, N, K);
   if (w_bytes >= (1ull << 32) || static_cast<uint64_t>(M) * (K / 32) * 36 >= (1ull << 32)) return 0;
@@ -304,6 +318,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
+  if (tiled(quant_type)) return M <= kMaxSlotM ? 2 : 5;
   if (gemv_only(quant_type) || row_split(quant_type) || use_lds(quant_type, M, K, N)) return 1;
   if (M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K)) return 4;
   if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
@@ -364,6 +379,12 @@ int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int ou
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
+  if (tiled(quant_type)) {  // M <= 32 (checked): the MFMA batch GEMVs
+    if (M <= kMaxSlotM)
+      return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
+    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s));
+  }
   if (!gemv_only(quant_type) && M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K))
     return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
   if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
@@ -397,6 +418,14 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
+  if (tiled(quant_type)) {
+    if (M <= kMaxSlotM)
+      return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M,
+                                             K, mode, s));
+    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
+    return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                         mode, 0, s));
+  }
   if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
       (M > kMaxSkinnyM && K % 256 != 0))
     return status_of(
@@ -461,7 +490,8 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   // the fused kernels serve the decode batch (M <= 2: the v_dot4 GEMV;
   // 3 <= M <= 8, Q4_K / Q6_K: the slot-packed MFMA GEMV) and whole Q8_1
   // blocks of outputs; other shapes take the grouped GEMV + SiLU producer
-  const int max_m = (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
+  const int max_m = tiled(quant_type) ? 0
+                    : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
   const bool slot = M > max_m && ifx::gemv_slot_fits(quant_type, M, K);
   if (M < 1 || (M > max_m && !slot) || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
@@ -505,7 +535,7 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
                       int mode, const void *bias, int M, int N, int K, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
+  if (gemv_only(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;  // no MFMA kernel for the type
   const bool f16 = out_dtype == IFX_OUT_F16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (use_f16_gemm(quant_type, M, K))
@@ -519,7 +549,7 @@ int ifx_qgemm_prefill(int quant_type, const void *W, const void *A_q8_1, void *Y
 constexpr int kMinWorkspaceN = 16384;
 
 int64_t ifx_qgemm_prefill_workspace_bytes(int quant_type, int M, int N, int K) {
-  if (!is_weight_type(quant_type) || gemv_only(quant_type) || row_split(quant_type) || M <= 0 ||
+  if (!is_weight_type(quant_type) || gemv_only(quant_type) || repacked(quant_type) || M <= 0 ||
       N <= 0 || K <= 0)
     return 0;
   if (!use_f16_gemm(quant_type, M, K) || !ifx::gemm_f16_fits(quant_type, K) || N < kMinWorkspaceN)
@@ -532,7 +562,7 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
                          int64_t workspace_bytes, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
   if (need == 0 || !workspace)
     return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
@@ -548,7 +578,7 @@ int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1,
                               void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const int64_t need = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
   if (need == 0)
     return ifx_qgemm_prefill(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream);
@@ -610,7 +640,7 @@ int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, 
                              int kernel, int splits, void *stream) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
-  if (gemv_only(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (gemv_only(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;
   const bool f16 = out_dtype == IFX_OUT_F16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (kernel == IFX_PREFILL_INT8)
@@ -644,10 +674,28 @@ int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K
   return status_of(ifx::launch_repack(quant_type, W, W_out, n_rows, K, static_cast<hipStream_t>(stream)));
 }
 
+int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K) {
+  const int tt = quant_type == IFX_TYPE_Q4_K ? IFX_TYPE_Q4_K_T
+                 : quant_type == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_T : 0;
+  if (!tt || n_rows < 0 || K <= 0 || K % 256) return 0;
+  return (n_rows + 31) / 32 * 32 * static_cast<int64_t>(ifx::row_bytes(tt, K));
+}
+
+int ifx_repack_tiled(int quant_type, const void *W, void *W_out, int64_t n_rows, int K,
+                     void *stream) {
+  if (!W || !W_out) return IFX_NULL_POINTER;
+  if (quant_type != IFX_TYPE_Q4_K && quant_type != IFX_TYPE_Q6_K) return IFX_UNSUPPORTED_TYPE;
+  if (n_rows < 0 || K <= 0 || K % 256) return IFX_BAD_GEOMETRY;
+  if (ifx_tiled_bytes(quant_type, n_rows, K) >= (int64_t{1} << 32))
+    return IFX_BAD_GEOMETRY;  // the GEMVs address tiles with 32-bit offsets
+  return status_of(ifx::launch_repack_tiled(quant_type, W, W_out, n_rows, K,
+                                            static_cast<hipStream_t>(stream)));
+}
+
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,
                    void *stream) {
   if (!W || !out) return IFX_NULL_POINTER;
-  if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (!is_weight_type(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (out_dtype != IFX_OUT_F32 && out_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   if (n_rows < 0 || K <= 0 || K % ifx_block_elems(quant_type)) return IFX_BAD_GEOMETRY;
   if (n_rows * static_cast<int64_t>((K / ifx_block_elems(quant_type)) * ifx_block_bytes(quant_type)) >= (int64_t{1} << 32))

@@ -203,4 +203,63 @@ hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, in
   return last_error();
 }
 
+// ---------------------------------------------------------------------------
+// Tiled repack (ifx_repack_tiled): raw Q4_K / Q6_K rows into the 32-row
+// tiles of the batch kernels (layouts in ifx_common.h).  One thread per
+// (group, super-block, row of the group); rows past n_rows are zeros.
+// ---------------------------------------------------------------------------
+template <int QT>
+__global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t *__restrict__ W,
+                                                      uint8_t *__restrict__ out, int64_t n_rows,
+                                                      int K) {
+  constexpr int kBytes = QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes;
+  constexpr int kTile = kTileRows * kBytes;
+  const int nsb = K / 256;
+  const int64_t groups = (n_rows + kTileRows - 1) / kTileRows;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= groups * nsb * kTileRows) return;
+  const int c = static_cast<int>(t % kTileRows);
+  const int64_t gb = t / kTileRows;  // group * nsb + super-block: the tile index
+  const int64_t row = (gb / nsb) * kTileRows + c;
+  const int b = static_cast<int>(gb % nsb);
+  uint8_t *tile = out + gb * kTile;
+  uint8_t src[kBytes];
+  if (row < n_rows) {
+    const uint8_t *p = W + (row * nsb + b) * kBytes;
+    for (int i = 0; i < kBytes; ++i) src[i] = p[i];
+  } else {
+    for (int i = 0; i < kBytes; ++i) src[i] = 0;
+  }
+  if constexpr (QT == kTypeQ4_K) {
+    for (int i = 0; i < 16; ++i) tile[16 * c + i] = src[i];
+    for (int p = 0; p < 4; ++p)
+      for (int h = 0; h < 2; ++h)
+        for (int i = 0; i < 16; ++i) tile[512 + 1024 * p + 512 * h + 16 * c + i] = src[16 + 32 * p + 16 * h + i];
+  } else {
+    for (int q = 0; q < 4; ++q)
+      for (int h = 0; h < 2; ++h)
+        for (int i = 0; i < 16; ++i) tile[1024 * q + 512 * h + 16 * c + i] = src[32 * q + 16 * h + i];
+    for (int g = 0; g < 2; ++g)
+      for (int h = 0; h < 2; ++h)
+        for (int i = 0; i < 16; ++i)
+          tile[4096 + 1024 * g + 512 * h + 16 * c + i] = src[128 + 32 * g + 16 * h + i];
+    for (int i = 0; i < 16; ++i) tile[6144 + 16 * c + i] = src[192 + i];
+    tile[6656 + 2 * c] = src[208];
+    tile[6656 + 2 * c + 1] = src[209];
+  }
+}
+
+hipError_t launch_repack_tiled(int qtype, const void *W, void *out, int64_t n_rows, int K,
+                               hipStream_t stream) {
+  const int64_t n = (n_rows + kTileRows - 1) / kTileRows * (K / 256) * kTileRows;
+  if (n == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  const uint8_t *w = static_cast<const uint8_t *>(W);
+  uint8_t *o = static_cast<uint8_t *>(out);
+  if (qtype == kTypeQ4_K) IFX_LAUNCH(k_repack_tiled, (kTypeQ4_K), grid, dim3(256), 0, stream, w, o, n_rows, K);
+  else if (qtype == kTypeQ6_K) IFX_LAUNCH(k_repack_tiled, (kTypeQ6_K), grid, dim3(256), 0, stream, w, o, n_rows, K);
+  else return hipErrorInvalidValue;
+  return last_error();
+}
+
 }  // namespace ifx

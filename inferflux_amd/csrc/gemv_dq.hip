@@ -132,9 +132,25 @@ struct RawW<kTypeQ8_0> {  // codes 16h .. 16h+15 and d of the 8 blocks
   uint32_t d[8];
 };
 
-template <int QT>
-__device__ __forceinline__ void fetch_w(RawW<QT> &r, rsrc_t Wr, uint32_t row_off, int sb, int h) {
-  if constexpr (QT == kTypeQ4_K) {
+// TL: the tiled layout (ifx_common.h); row_off = the first tile of the
+// lane's 32-row group, c = lane % 32.
+template <int QT, bool TL = false>
+__device__ __forceinline__ void fetch_w(RawW<QT> &r, rsrc_t Wr, uint32_t row_off, int sb, int h,
+                                        int c = 0) {
+  if constexpr (TL && QT == kTypeQ4_K) {
+    const uint32_t o = row_off + sb * (kTileRows * kQ4KBytes) + 16 * c;
+    r.hdr = wload<u32x4>(Wr, o, 0);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.qs[p] = wload<u32x4>(Wr, o + 512 + 1024 * p + 512 * h, 0);
+  } else if constexpr (TL) {
+    const uint32_t t = row_off + sb * (kTileRows * kQ6KBytes), o = t + 16 * c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.ql[i] = wload<u32x4>(Wr, o + 1024 * i + 512 * h, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) r.qh[g] = wload<u32x4>(Wr, o + 4096 + 1024 * g + 512 * h, 0);
+    r.sc = wload<u32x4>(Wr, o + 6144, 0);
+    r.d = wload<uint16_t>(Wr, t + 6656 + 2 * c, 0);
+  } else if constexpr (QT == kTypeQ4_K) {
     const uint32_t o = row_off + sb * kQ4KBytes;
     r.hdr = wload<u32x4>(Wr, o, 0);
 #pragma unroll
@@ -287,7 +303,7 @@ __device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint
 
 // grid: x = row groups of 128 (all projections), y = super-block splits.
 // Dynamic LDS: (M + 1) rows of pitch = sb_per * 256 + 8 halves (row M zero).
-template <int QT, bool F16OUT, bool ATOMIC>
+template <int QT, bool F16OUT, bool ATOMIC, bool TL = false>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int bx = blockIdx.x;
@@ -305,10 +321,12 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
   const uint32_t w_row = static_cast<uint32_t>(
       QT == kTypeQ8_0 ? (K >> 5) * kQ8_0Bytes : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
-  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(N));
+  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(TL ? (N + 31) & ~31 : N));
   const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
   const int n = (bx - sg.blk_begin) * kRowsPerWg + wave * 32 + l32;
-  const uint32_t row_off = static_cast<uint32_t>(min(n, N - 1)) * w_row;
+  // tiled: the group's first tile (group-major tiles of 32 rows x 1 super-block)
+  const uint32_t row_off = TL ? static_cast<uint32_t>(n >> 5) * 32 * w_row
+                              : static_cast<uint32_t>(min(n, N - 1)) * w_row;
   // batch rows past M read the zero row M
   const _Float16 *arow = lds + (l32 < M ? l32 : M) * pitch;
 
@@ -319,15 +337,15 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   // Three super-blocks of weights in flight per wave (register ring), the
   // first two issued before the activation stage is built.
   RawW<QT> w0, w1, w2;
-  if (cnt > 0) fetch_w<QT>(w0, Wr, row_off, sb_begin, h);
-  if (cnt > 1) fetch_w<QT>(w1, Wr, row_off, sb_begin + 1, h);
+  if (cnt > 0) fetch_w<QT, TL>(w0, Wr, row_off, sb_begin, h, l32);
+  if (cnt > 1) fetch_w<QT, TL>(w1, Wr, row_off, sb_begin + 1, h, l32);
   for (int i = tid; i < pitch / 8; i += 64 * kWaves)
     reinterpret_cast<u32x4 *>(lds + M * pitch)[i] = u32x4{0, 0, 0, 0};
   stage_a(lds, pitch, Ar, a_row, M, sb_begin, cnt, tid);
   __syncthreads();
 
   auto step = [&](const RawW<QT> &cur, RawW<QT> &fut, int i) {
-    if (i + 2 < cnt) fetch_w<QT>(fut, Wr, row_off, sb_begin + i + 2, h);
+    if (i + 2 < cnt) fetch_w<QT, TL>(fut, Wr, row_off, sb_begin + i + 2, h, l32);
     compute<QT>(cur, arow + 256 * i, h, acc0, acc1);
   };
   for (int i = 0; i < cnt; i += 3) {
@@ -380,7 +398,7 @@ int dq_splits(int groups, int nsb, int M, bool f16) {
   return max(need, min(nsb, (target + groups - 1) / groups));
 }
 
-template <int QT>
+template <int QT, bool TL>
 hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   int groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
@@ -397,9 +415,11 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
   const dim3 grid(groups, ks), block(64 * kWaves);
   if (f16) {
-    IFX_LAUNCH(k_gemv_dq, (QT, true, false), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, true, false, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, true, false), grid, block, shm, s, args);
   } else if (ks == 1) {
-    IFX_LAUNCH(k_gemv_dq, (QT, false, false), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, false, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, false, false), grid, block, shm, s, args);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -409,7 +429,8 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
       }
       if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return last_error();
     }
-    IFX_LAUNCH(k_gemv_dq, (QT, false, true), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, true, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, false, true), grid, block, shm, s, args);
   }
   return last_error();
 }
@@ -418,7 +439,8 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
 
 // fp16 outputs are not split: their K must fit one activation stage.
 bool gemv_dq_fits(int qtype, int M, int K) {
-  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ8_0) && M >= 1 &&
+  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ8_0 || qtype == kTypeQ4_KT ||
+          qtype == kTypeQ6_KT) && M >= 1 &&
          M <= kMaxM && K % 256 == 0;
 }
 
@@ -439,9 +461,11 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
   args.K = K;
   args.mode = mode;
   switch (qtype) {
-  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(args, f16, splits_req, stream);
-  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(args, f16, splits_req, stream);
-  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(args, f16, splits_req, stream);
+  case kTypeQ4_K: return launch_qt<kTypeQ4_K, false>(args, f16, splits_req, stream);
+  case kTypeQ6_K: return launch_qt<kTypeQ6_K, false>(args, f16, splits_req, stream);
+  case kTypeQ8_0: return launch_qt<kTypeQ8_0, false>(args, f16, splits_req, stream);
+  case kTypeQ4_KT: return launch_qt<kTypeQ4_K, true>(args, f16, splits_req, stream);
+  case kTypeQ6_KT: return launch_qt<kTypeQ6_K, true>(args, f16, splits_req, stream);
   default: return hipErrorInvalidValue;
   }
 }

@@ -116,10 +116,23 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int QT>
+// TL: the tiled layout (ifx_common.h), voff = 16 * (lane % 32) and sb_off
+// the tile's byte offset.
+template <int QT, bool TL = false>
 __device__ __forceinline__ void load_w(WSb<QT> &w, rsrc_t Wr, uint32_t voff, uint32_t sb_off,
                                        int h) {
-  if constexpr (QT == kTypeQ4_K) {
+  if constexpr (TL && QT == kTypeQ4_K) {
+    w.hdr = wload<u32x4>(Wr, voff, sb_off);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) w.q[p] = wload<u32x4>(Wr, voff + 512 + 1024 * p + 512 * h, sb_off);
+  } else if constexpr (TL) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.ql[i] = wload<u32x4>(Wr, voff + 1024 * i + 512 * h, sb_off);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) w.qh[hf] = wload<u32x4>(Wr, voff + 4096 + 1024 * hf + 512 * h, sb_off);
+    w.sc = wload<u32x4>(Wr, voff + 6144, sb_off);
+    w.d = wload<uint16_t>(Wr, 6656 + (voff >> 3), sb_off);
+  } else if constexpr (QT == kTypeQ4_K) {
     w.hdr = wload<u32x4>(Wr, voff, sb_off);
 #pragma unroll
     for (int p = 0; p < 4; ++p) w.q[p] = wload<u32x4>(Wr, voff + 16 + 32 * p + 16 * h, sb_off);
@@ -189,7 +202,7 @@ constexpr int slot_lds_bytes() {
 // blocks equal grouped GEMV + silu_mul_quantize bit for bit where the
 // grouped launch runs the same KW (other KW add the super-blocks' partial
 // sums in another order).
-template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool SW = false>
+template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool SW = false, bool TL = false>
 __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const SlotArgs args) {
   using G = SlotGeo<QT, MP>;
   constexpr int NM = G::kNm;
@@ -211,12 +224,16 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
   constexpr int kSbBytes = (QT == kTypeQ4_K) ? kQ4KBytes : kQ6KBytes;
   const uint32_t w_row = static_cast<uint32_t>(nsb) * kSbBytes;
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
-  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(N));
+  // tiled: whole 32-row groups; tile (group, super-block) at (group * nsb + sb) * kTile
+  constexpr int kTile = kTileRows * kSbBytes;
+  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(TL ? (N + 31) & ~31 : N));
   const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
   float *dl = reinterpret_cast<float *>(smem) + wave_all * (2 * 8 * MP);  // [8][MP] d
   float *sl = dl + 8 * MP;                                            // [8][MP] s
 
-  const uint32_t w_voff = static_cast<uint32_t>(min(n0 + c32, N - 1)) * w_row;
+  const uint32_t w_voff = TL ? 16u * c32 : static_cast<uint32_t>(min(n0 + c32, N - 1)) * w_row;
+  const uint32_t w_soff = TL ? static_cast<uint32_t>(n0 / 32) * nsb * kTile : 0u;  // group's first tile
+  constexpr int kSbStep = TL ? kTile : kSbBytes;  // bytes between a row's super-blocks
   // activation operand: MFMA row r = c32 = batch row (r % MP) of slot r / MP
   const int am = c32 % MP, aslot = c32 / MP;
   constexpr uint32_t kOob = 0x80000000u;  // past any A range: loads zeros
@@ -253,7 +270,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
   WSb<QT> wc;
   ASb<QT, MP> ac;
   if (sb < nsb) {
-    load_w<QT>(wc, Wr, w_voff, sb * kSbBytes, h);
+    load_w<QT, TL>(wc, Wr, w_voff, w_soff + sb * kSbStep, h);
     load_a<QT, MP>(ac, Ar, a_off, ds_off, sb * 8 * kQ8_1Bytes);
   }
   for (; sb < nsb; sb += step) {
@@ -261,7 +278,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
     ASb<QT, MP> an;
     const bool more = sb + step < nsb;
     if (more) {
-      load_w<QT>(wn, Wr, w_voff, (sb + step) * kSbBytes, h);
+      load_w<QT, TL>(wn, Wr, w_voff, w_soff + (sb + step) * kSbStep, h);
       load_a<QT, MP>(an, Ar, a_off, ds_off, (sb + step) * 8 * kQ8_1Bytes);
     }
     // d and s of this super-block's 8 x MP activation blocks
@@ -461,19 +478,23 @@ void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
   ks = f16 ? 1 : max(1, min(ks, nsb / kw));
 }
 
-template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC>
+template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool TL>
 void slot_launch(const SlotArgs &args, int blocks, int ks, hipStream_t s) {
   constexpr int lds = slot_lds_bytes<QT, MP, KW>();
-  IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC), dim3(blocks, ks), dim3(64 * KW), lds,
-                     s, args);
+  if constexpr (TL)
+    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC, false, true), dim3(blocks, ks),
+               dim3(64 * KW), lds, s, args);
+  else
+    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC), dim3(blocks, ks), dim3(64 * KW), lds,
+               s, args);
 }
 
-template <int QT, int MP, int KW>
+template <int QT, int MP, int KW, bool TL>
 void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t s) {
   if (f16) {
-    slot_launch<QT, MP, KW, true, false>(args, blocks, 1, s);
+    slot_launch<QT, MP, KW, true, false, TL>(args, blocks, 1, s);
   } else if (ks == 1) {
-    slot_launch<QT, MP, KW, false, false>(args, blocks, 1, s);
+    slot_launch<QT, MP, KW, false, false, TL>(args, blocks, 1, s);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -484,28 +505,28 @@ void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t 
       // a failed fill stays set for the caller's hipGetLastError
       if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return;
     }
-    slot_launch<QT, MP, KW, false, true>(args, blocks, ks, s);
+    slot_launch<QT, MP, KW, false, true, TL>(args, blocks, ks, s);
   }
 }
 
-template <int QT, int MP>
+template <int QT, int MP, bool TL>
 void slot_kw(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
   int kw = 8, ks = 1;
   choose_slot_work(blocks, args.K >> 8, f16, kw, ks);
   switch (kw) {
-  case 1: slot_split<QT, MP, 1>(args, blocks, ks, f16, s); break;
-  case 2: slot_split<QT, MP, 2>(args, blocks, ks, f16, s); break;
-  case 4: slot_split<QT, MP, 4>(args, blocks, ks, f16, s); break;
-  default: slot_split<QT, MP, 8>(args, blocks, ks, f16, s); break;
+  case 1: slot_split<QT, MP, 1, TL>(args, blocks, ks, f16, s); break;
+  case 2: slot_split<QT, MP, 2, TL>(args, blocks, ks, f16, s); break;
+  case 4: slot_split<QT, MP, 4, TL>(args, blocks, ks, f16, s); break;
+  default: slot_split<QT, MP, 8, TL>(args, blocks, ks, f16, s); break;
   }
 }
 
 // MP = 16 (two slots) is instantiable but measured slower than the
 // LDS-staged MFMA kernel for 9 <= M <= 16 (twice the rescale work per lane
 // at 2-3 waves per SIMD), so only M <= 8 is routed here.
-template <int QT>
+template <int QT, bool TL>
 void slot_q(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
-  slot_kw<QT, 8>(args, blocks, f16, s);
+  slot_kw<QT, 8, TL>(args, blocks, f16, s);
 }
 
 }  // namespace
@@ -516,29 +537,35 @@ void slot_q(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
 // against 12.4 / 12.4 / 13.1 with 8; 14B 13824 x 5120 at M = 8: 24.4 against
 // 27.1).  With fewer than 4 super-blocks per row the waves match them.
 // IFX_SLOT_KW overrides, as for the plain launch.
-template <int QT, int KW>
+template <int QT, int KW, bool TL>
 void slot_swiglu_launch(const SlotArgs &args, bool f16h, hipStream_t s) {
   constexpr int lds = slot_lds_bytes<QT, 8, KW, 2>();
   const dim3 grid(args.seg[0].N / 32);
-  if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true), grid, dim3(128 * KW), lds, s, args);
-  else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true), grid, dim3(128 * KW), lds, s, args);
+  if constexpr (TL) {
+    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true, true), grid, dim3(128 * KW), lds, s, args);
+    else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true, true), grid, dim3(128 * KW), lds, s, args);
+  } else {
+    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true), grid, dim3(128 * KW), lds, s, args);
+    else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true), grid, dim3(128 * KW), lds, s, args);
+  }
 }
 
-template <int QT>
+template <int QT, bool TL>
 void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
   int kw = 4, ks = 1;
   if (getenv("IFX_SLOT_KW")) choose_slot_work(1 << 20, args.K >> 8, false, kw, ks);
   while (kw > 1 && kw > (args.K >> 8)) kw /= 2;
   switch (kw) {
-  case 1: slot_swiglu_launch<QT, 1>(args, f16h, s); break;
-  case 2: slot_swiglu_launch<QT, 2>(args, f16h, s); break;
-  case 4: slot_swiglu_launch<QT, 4>(args, f16h, s); break;
-  default: slot_swiglu_launch<QT, 8>(args, f16h, s); break;
+  case 1: slot_swiglu_launch<QT, 1, TL>(args, f16h, s); break;
+  case 2: slot_swiglu_launch<QT, 2, TL>(args, f16h, s); break;
+  case 4: slot_swiglu_launch<QT, 4, TL>(args, f16h, s); break;
+  default: slot_swiglu_launch<QT, 8, TL>(args, f16h, s); break;
   }
 }
 
 bool gemv_slot_fits(int qtype, int M, int K) {
-  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K) && M >= 1 && M <= 8 && K % 256 == 0 && K > 0;
+  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ4_KT || qtype == kTypeQ6_KT) &&
+         M >= 1 && M <= 8 && K % 256 == 0 && K > 0;
 }
 
 // count projections (1..3) share A; geometry checked by the caller
@@ -558,8 +585,12 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
   args.M = M;
   args.K = K;
   args.mode = mode;
-  if (qtype == kTypeQ4_K) slot_q<kTypeQ4_K>(args, blocks, f16, stream);
-  else slot_q<kTypeQ6_K>(args, blocks, f16, stream);
+  switch (qtype) {
+  case kTypeQ4_K: slot_q<kTypeQ4_K, false>(args, blocks, f16, stream); break;
+  case kTypeQ6_K: slot_q<kTypeQ6_K, false>(args, blocks, f16, stream); break;
+  case kTypeQ4_KT: slot_q<kTypeQ4_K, true>(args, blocks, f16, stream); break;
+  default: slot_q<kTypeQ6_K, true>(args, blocks, f16, stream); break;
+  }
   return last_error();
 }
 
@@ -580,8 +611,12 @@ hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, co
   args.mode = 0;
   args.H = H;
   args.Q = static_cast<uint8_t *>(Q);
-  if (qtype == kTypeQ4_K) slot_swiglu_q<kTypeQ4_K>(args, f16h, stream);
-  else slot_swiglu_q<kTypeQ6_K>(args, f16h, stream);
+  switch (qtype) {
+  case kTypeQ4_K: slot_swiglu_q<kTypeQ4_K, false>(args, f16h, stream); break;
+  case kTypeQ6_K: slot_swiglu_q<kTypeQ6_K, false>(args, f16h, stream); break;
+  case kTypeQ4_KT: slot_swiglu_q<kTypeQ4_K, true>(args, f16h, stream); break;
+  default: slot_swiglu_q<kTypeQ6_K, true>(args, f16h, stream); break;
+  }
   return last_error();
 }
 

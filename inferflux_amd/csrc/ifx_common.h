@@ -72,9 +72,25 @@ constexpr int kQ8_1Bytes = 36;
 constexpr int kTypeQ8_0R = 108;
 constexpr int kTypeQ6_KR = 114;
 
+// Tiled layouts of this library (ifx_repack_tiled): the rows in groups of
+// 32, and per group and super-block one tile that holds the group's 32
+// super-blocks with their bytes in the order the batch kernels' lanes load
+// them (lane l: row l % 32, 16-byte pieces of K half l / 32), so each wave
+// load instruction reads one contiguous kilobyte.  Tiles are ordered group
+// major; the rows of a last, partial group are zero.
+//   Q4_K_T (4608 B): [0, 512)   the 16-byte header (d, dmin, scales) of row c at 16 c
+//                    512 + 1024 p + 512 h + 16 c: qs bytes 32 p + 16 h .. +15 of row c
+//   Q6_K_T (6720 B): 1024 i + 512 h + 16 c: ql bytes 32 i + 16 h .. +15 (i = 0..3)
+//                    4096 + 1024 g + 512 h + 16 c: qh bytes 32 g + 16 h .. +15 (g = 0, 1)
+//                    6144 + 16 c: scales[16];  6656 + 2 c: d
+constexpr int kTypeQ4_KT = 212;
+constexpr int kTypeQ6_KT = 214;
+constexpr int kTileRows = 32;
+
 // Bytes of one weight row of K values.
 __host__ __device__ constexpr int row_bytes(int qt, int K) {
-  return qt == kTypeQ4_K    ? (K >> 8) * kQ4KBytes
+  return (qt == kTypeQ4_K || qt == kTypeQ4_KT) ? (K >> 8) * kQ4KBytes
+         : qt == kTypeQ6_KT ? (K >> 8) * kQ6KBytes
          : qt == kTypeQ5_K  ? (K >> 8) * kQ5KBytes
          : qt == kTypeQ6_K  ? (K >> 8) * kQ6KBytes
          : qt == kTypeQ8_K  ? (K >> 8) * kQ8KBytes

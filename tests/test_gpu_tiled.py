@@ -1,0 +1,175 @@
+"""The tiled repack (ifx_repack_tiled) and the MFMA batch GEMVs on its
+layouts: the tiled bytes against an independent numpy restatement of the
+layout, the GEMVs on tiled weights against the fp64 oracle on the raw blocks
+(1e-3 * ||y_row||_2), and bit for bit against the raw-layout launch wherever
+the dispatch runs the same kernel and split on both."""
+import numpy as np
+import pytest
+
+from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, up
+
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K = 12, 14
+Q4_K_T, Q6_K_T = 212, 214
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def tile_rows(qtype, w, N, K):
+    """numpy restatement of the tiled layouts (include/ifx_qgemm.h): per
+    group of 32 rows and super-block, the rows' 16-byte pieces in lane
+    order (piece j of row c at 512 j + 16 c for the K-half-major pieces)."""
+    nb = 144 if qtype == Q4_K else 210
+    nsb = K // 256
+    G = (N + 31) // 32
+    b = np.zeros((G * 32, nsb, nb), np.uint8)
+    b[:N] = w.reshape(N, nsb, nb)
+    b = b.reshape(G, 32, nsb, nb).transpose(0, 2, 1, 3)  # [group][sb][row][bytes]
+    if qtype == Q4_K:
+        hdr = b[:, :, :, :16].reshape(G, nsb, 512)
+        qs = b[:, :, :, 16:].reshape(G, nsb, 32, 8, 16).transpose(0, 1, 3, 2, 4)  # [p*2+h][row]
+        tile = np.concatenate([hdr, qs.reshape(G, nsb, 4096)], axis=2)
+    else:
+        q = b[:, :, :, :192].reshape(G, nsb, 32, 12, 16).transpose(0, 1, 3, 2, 4)
+        sc = b[:, :, :, 192:208].reshape(G, nsb, 512)
+        d = b[:, :, :, 208:].reshape(G, nsb, 64)
+        tile = np.concatenate([q.reshape(G, nsb, 6144), sc, d], axis=2)
+    return tile.reshape(-1)
+
+
+def _args(name):
+    return name[:name.index("<")], name[name.index("<") + 1:-1].split(",")
+
+
+def raw_launch(tiled_name):
+    """The launch-log name of the same kernel on raw rows: the template
+    arguments before the layout flag (slot: 5, dq: 3)."""
+    k, a = _args(tiled_name)
+    return f"{k}<{','.join(a[:5] if k == 'k_gemv_slot' else a[:3])}>"
+
+
+def atomic(name):
+    """A K split with fp32 atomics (its bits vary run to run)."""
+    k, a = _args(name)
+    return a[4 if k == "k_gemv_slot" else 2] == "1"
+
+
+@pytest.mark.parametrize("qtype,N,K", [(Q4_K, 64, 512), (Q4_K, 100, 2048), (Q6_K, 33, 256),
+                                       (Q6_K, 2048, 1024)])
+def test_tiled_layout(dev, qtype, N, K):
+    from inferflux_amd import ops, synth
+    note(f"tiled layout type={qtype} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=N + K)
+    tt, out = ops.repack_tiled(qtype, up(w, dev), N, K)
+    want = tile_rows(qtype, w, N, K)
+    assert tt == qtype + 200
+    assert out.numel() == want.size == ops.weight_bytes(tt, N, K)
+    assert np.array_equal(down(out), want)
+
+
+CASES = [(Q4_K, M, 1000, 2048) for M in (1, 2, 3, 5, 8, 9, 16, 17, 32)]
+CASES += [(Q6_K, M, 1000, 2048) for M in (1, 4, 8, 12, 32)]
+CASES += [(Q4_K, 8, 100, 5120), (Q6_K, 5, 77, 11008), (Q6_K, 32, 2048, 5120), (Q4_K, 24, 31, 256)]
+
+
+@pytest.mark.parametrize("qtype,M,N,K", CASES)
+def test_gemv_tiled(orc, dev, qtype, M, N, K):
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gemv tiled type={qtype} M={M} N={N} K={K}")
+    w = synth.blocks(qtype, N, K, seed=N * 5 + K + M)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=K + M, outlier_frac=0.01))
+    W, A = up(w, dev), up(a, dev)
+    tt, WT = ops.repack_tiled(qtype, W, N, K)
+    ye = orc.gemv_exact(qtype, w, a, M, N, K)
+    with ops.launch_log() as lg:
+        y = down(ops.qgemv(tt, WT, A, M, N, K))
+    fam = "k_gemv_slot<" if M <= 8 else "k_gemv_dq<"
+    assert len(lg.kernels) >= 1 and lg.kernels[-1].startswith(fam) and lg.kernels[-1].endswith(",1>")
+    check_rows(y, ye)
+    # the raw layout on the same kernel (same arguments but the layout flag)
+    # and without a K split: the same bits
+    with ops.launch_log() as lr:
+        yr = down(ops.qgemv(qtype, W, A, M, N, K))
+    if lr.kernels[-1] == raw_launch(lg.kernels[-1]) and not atomic(lr.kernels[-1]):
+        assert np.array_equal(y.view(np.uint32), yr.view(np.uint32))
+    rng = np.random.default_rng(N + M)
+    base = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    check_rows(down(ops.qgemv(tt, WT, A, M, N, K, out=up(base, dev), mode=ops.ACCUM)), ye + base)
+    check_rows(down(ops.qgemv(tt, WT, A, M, N, K, mode=ops.BIAS, bias=up(bias, dev))),
+               ye + bias[None, :])
+    try:  # fp16 outputs above M = 8 only where K fits one activation stage
+        y16 = ops.qgemv(tt, WT, A, M, N, K, out_dtype=torch.float16)
+    except ops.NotHandled:
+        assert M > 8
+    else:
+        check_rows(down(y16).astype(np.float64), ye, tol=2e-3)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+def test_grouped_tiled(orc, dev, M):
+    """Q/K/V-shaped siblings (ragged N) in one launch."""
+    from inferflux_amd import ops, synth
+    note(f"grouped tiled M={M}")
+    K, Ns = 1024, (300, 70, 70)
+    ws = [synth.blocks(Q4_K, n, K, seed=n + M) for n in Ns]
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=9 + M))
+    WT = [ops.repack_tiled(Q4_K, up(w, dev), n, K)[1] for w, n in zip(ws, Ns)]
+    outs = ops.qgemv_grouped(Q4_K_T, WT, up(a, dev), M, list(Ns), K)
+    for w, n, y in zip(ws, Ns, outs):
+        check_rows(down(y), orc.gemv_exact(Q4_K, w, a, M, n, K))
+
+
+@pytest.mark.parametrize("qtype,M", [(Q4_K, 1), (Q4_K, 4), (Q4_K, 8), (Q6_K, 3)])
+def test_gate_up_silu_tiled(orc, dev, qtype, M):
+    from inferflux_amd import ops, synth
+    note(f"gate_up_silu tiled type={qtype} M={M}")
+    N, K = 512, 1024
+    wg = synth.blocks(qtype, N, K, seed=M + 1)
+    wu = synth.blocks(qtype, N, K, seed=M + 2)
+    x = synth.activations(M, K, seed=K + M) * 0.1
+    a = orc.quantize_q8_1(x)
+    A = up(a, dev)
+    tt, WG = ops.repack_tiled(qtype, up(wg, dev), N, K)
+    WU = ops.repack_tiled(qtype, up(wu, dev), N, K)[1]
+    with ops.launch_log() as lg:
+        h, q = ops.qgemv_gate_up_silu(tt, WG, WU, A, M, N, K)
+    assert len(lg.kernels) == 1 and lg.kernels[0].endswith(",1,1>")
+    g = orc.gemv_exact(qtype, wg, a, M, N, K)
+    u = orc.gemv_exact(qtype, wu, a, M, N, K)
+    check_rows(down(h), g / (1.0 + np.exp(-g)) * u)
+    assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
+    if M >= 3:  # the raw layout runs the same kernel: the same bits
+        hr, qr = ops.qgemv_gate_up_silu(qtype, up(wg, dev), up(wu, dev), A, M, N, K)
+        assert np.array_equal(down(h).view(np.uint32), down(hr).view(np.uint32))
+        assert np.array_equal(down(q), down(qr))
+
+
+def test_tiled_not_handled(dev):
+    """Tiled weights above M = 32, on the prefill, fused-RMSNorm and
+    dequantize entries, or tiling a type without a tiled layout: not
+    handled, nothing launched."""
+    import torch
+    from inferflux_amd import ops
+    w = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    a = torch.zeros(1 << 18, dtype=torch.uint8, device=dev)
+    x = torch.zeros(64, 256, device=dev)
+    nw = torch.ones(256, dtype=torch.float16, device=dev)
+    with ops.launch_log() as lg:
+        for fn in (lambda: ops.qgemv(Q4_K_T, w, a, 33, 64, 256),
+                   lambda: ops.qgemv(Q6_K_T, w, a, 1, 64, 256, prefill=True),
+                   lambda: ops.qgemm_prefill_kernel(Q4_K_T, w, a, 64, 64, 256, ops.PREFILL_F16),
+                   lambda: ops.qgemv_grouped_rmsnorm(Q4_K_T, [w], x[:1], nw, 1, [64], 256),
+                   lambda: ops.dequantize(Q4_K_T, w, 64, 256),
+                   lambda: ops.repack_tiled(8, w, 4, 256)):
+            with pytest.raises((ops.NotHandled, KeyError)):
+                fn()
+    assert lg.kernels == []
