@@ -122,6 +122,30 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
                       const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                       void *stream);
 
+/* Deterministic variants of ifx_qgemv / ifx_qgemv_grouped with a caller
+ * workspace.  Where the chosen kernel splits K over workgroups (the
+ * slot-packed MFMA GEMV on narrow long-K launches such as a down projection,
+ * the fp16-dequant MFMA GEMV at 17 <= M <= 32 and on tiled weights), each
+ * split stores its fp32 partial sums in the workspace and the last
+ * workgroup of a tile to finish adds them in split order and writes Y: the
+ * bits are the same run to run, and there is no zero-fill launch and no
+ * atomic on Y.  Other launches are those of the plain entries.  workspace:
+ * at least ifx_qgemv_workspace_bytes bytes, 256-byte aligned; its leading
+ * counters must be zero before the first call (zero the buffer once after
+ * allocating it) and every call leaves them zero.  Calls that share a
+ * workspace must not overlap.  No reference counterpart (the reference's
+ * split kernels add with fp32 atomics, mmvq.cuh:280-401). */
+int ifx_qgemv_ws(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
+                 int mode, const void *bias, int M, int N, int K, void *workspace,
+                 int64_t workspace_bytes, void *stream);
+int ifx_qgemv_grouped_ws(int quant_type, int count, const void *const *W, void *const *Y,
+                         const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
+                         void *workspace, int64_t workspace_bytes, void *stream);
+/* Workspace bytes the _ws entries need for count projections of N[i] rows
+ * (count = 1 for ifx_qgemv_ws); 0 when the launch does not split K. */
+int64_t ifx_qgemv_workspace_bytes(int quant_type, int count, const int *N, int out_dtype, int M,
+                                  int K);
+
 /* RMSNorm + Q8_1 fused into the grouped GEMV that consumes it: for each
  * batch row m, a[m] = Q8_1((x[m] * rms(x[m])) * norm_weight), exactly as
  * ifx_rmsnorm_quantize_q8_1 computes it, then y_i (op)= W_i . a as

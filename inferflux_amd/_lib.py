@@ -35,6 +35,10 @@ SIGNATURES = {
     "ifx_repacked_bytes": ([_i32, _i64, _i32], _i64),
     "ifx_repack": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
     "ifx_tiled_bytes": ([_i32, _i64, _i32], _i64),
+    "ifx_qgemv_ws": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _vp], _i32),
+    "ifx_qgemv_grouped_ws": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64,
+                              _vp], _i32),
+    "ifx_qgemv_workspace_bytes": ([_i32, _i32, _vp, _i32, _i32, _i32], _i64),
     "ifx_repack_tiled": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),

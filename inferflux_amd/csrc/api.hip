@@ -57,7 +57,8 @@ bool gemv_dq_fits(int qtype, int M, int K);
 bool gemv_dq_fits_f16(int M, int K);
 hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
-                          int mode, int splits_req, hipStream_t stream);
+                          int mode, int splits_req, hipStream_t stream, void *ws = nullptr);
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K);
 hipError_t scratch_address(void **out);
 hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, int K,
                          hipStream_t stream);
@@ -74,7 +75,8 @@ hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, co
                                    hipStream_t stream);
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
-                            int mode, hipStream_t stream);
+                            int mode, hipStream_t stream, void *ws = nullptr);
+int64_t gemv_slot_workspace_bytes(int count, const int *N, bool f16, int M, int K);
 }  // namespace ifx
 
 // ---------------------------------------------------------------- launch log
@@ -264,6 +266,124 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   return IFX_OK;
 }
 
+// Kernel route of ifx_qgemv (grouped = false) and ifx_qgemv_grouped
+// (grouped = true) for valid arguments; n_total = sum of the projections' N.
+enum class Route { F16Gemm, Gemv, Lds, Slot, Dq, Skinny, Mmvq, Mfma, PerProjection };
+Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
+  if (tiled(qt)) return M <= kMaxSlotM ? Route::Slot : Route::Dq;
+  if (!grouped && !gemv_only(qt) && M > kMaxSkinnyM && use_f16_gemm(qt, M, K)) return Route::F16Gemm;
+  if (gemv_only(qt) || row_split(qt) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
+    return Route::Gemv;
+  if (use_lds(qt, M, K, n_total)) return Route::Lds;
+  if (use_slot(qt, M, K, n_total, f16)) return Route::Slot;
+  if (use_dq(qt, M, K, f16)) return Route::Dq;
+  if (M <= kMaxSkinnyM) return (use_skinny(M) && K % 256 == 0) ? Route::Skinny : Route::Mmvq;
+  return grouped ? Route::PerProjection : Route::Mfma;
+}
+
+// The ordered-split workspace of a slot / dq launch: nullptr when there is
+// none (atomics) or the launch does not split; rc = IFX_BAD_GEOMETRY when
+// the caller's workspace is too small or not 256-byte aligned.
+void *split_ws(Route r, void *ws, int64_t ws_bytes, int count, const int *N, bool f16, int M,
+               int K, int &rc) {
+  rc = IFX_OK;
+  if (!ws) return nullptr;
+  const int64_t need = r == Route::Slot ? ifx::gemv_slot_workspace_bytes(count, N, f16, M, K)
+                                        : ifx::gemv_dq_workspace_bytes(count, N, f16, M, K);
+  if (need == 0) return nullptr;
+  if (ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) rc = IFX_BAD_GEOMETRY;
+  return ws;
+}
+
+int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,
+               const void *bias, int M, int N, int K, void *stream, void *ws, int64_t ws_bytes) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  const Route r = route(quant_type, M, K, N, f16, false);
+  int wrc = IFX_OK;
+  switch (r) {
+  case Route::F16Gemm:
+    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
+  case Route::Gemv:
+    return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  case Route::Lds:
+    return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  case Route::Slot: {
+    void *w = split_ws(r, ws, ws_bytes, 1, &N, f16, M, K, wrc);
+    if (wrc != IFX_OK) return wrc;
+    return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s, w));
+  }
+  case Route::Dq: {
+    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;  // tiled weights
+    void *w = split_ws(r, ws, ws_bytes, 1, &N, f16, M, K, wrc);
+    if (wrc != IFX_OK) return wrc;
+    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s, w));
+  }
+  case Route::Skinny:
+    return status_of(ifx::launch_mmq_skinny(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  case Route::Mmvq:
+    return status_of(ifx::launch_mmvq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
+  default:
+    return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  }
+}
+
+int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y, const int *N,
+                 const void *A_q8_1, int out_dtype, int mode, int M, int K, void *stream, void *ws,
+                 int64_t ws_bytes) {
+  if (!W || !Y || !N) return IFX_NULL_POINTER;
+  if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
+  if (mode == IFX_BIAS) return IFX_BAD_GEOMETRY;
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_gemm_args(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M,
+                                   N[i], K);
+    if (rc != IFX_OK) return rc;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  int n_total = 0;
+  for (int i = 0; i < count; ++i) n_total += N[i];
+  const Route r = route(quant_type, M, K, n_total, f16, true);
+  int wrc = IFX_OK;
+  switch (r) {
+  case Route::Gemv:
+    return status_of(
+        ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
+  case Route::Lds:
+    return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
+  case Route::Slot: {
+    void *w = split_ws(r, ws, ws_bytes, count, N, f16, M, K, wrc);
+    if (wrc != IFX_OK) return wrc;
+    return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                           mode, s, w));
+  }
+  case Route::Dq: {
+    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;  // tiled weights
+    void *w = split_ws(r, ws, ws_bytes, count, N, f16, M, K, wrc);
+    if (wrc != IFX_OK) return wrc;
+    return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                         mode, 0, s, w));
+  }
+  case Route::Skinny:
+    return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M,
+                                            K, mode, s));
+  case Route::Mmvq:
+    return status_of(ifx::launch_mmvq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
+                                      mode, s));
+  default:
+    break;
+  }
+  // batched decode and prefill: one launch per projection (each fills the chip)
+  for (int i = 0; i < count; ++i) {
+    const int rc = qgemv_impl(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],
+                              K, stream, ws, ws_bytes);
+    if (rc != IFX_OK) return rc;
+  }
+  return IFX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -318,12 +438,13 @@ int ifx_supports(int quant_type, int M, int N, int K) {
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {
   if (!ifx_supports(quant_type, M, N, K)) return 0;
-  if (tiled(quant_type)) return M <= kMaxSlotM ? 2 : 5;
-  if (gemv_only(quant_type) || row_split(quant_type) || use_lds(quant_type, M, K, N)) return 1;
-  if (M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K)) return 4;
-  if (M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0)) return 1;
-  if (!use_slot(quant_type, M, K, N, false) && use_dq(quant_type, M, K, false)) return 5;
-  return M <= kMaxSkinnyM ? 2 : 3;
+  switch (route(quant_type, M, K, N, false, false)) {
+  case Route::Gemv: case Route::Lds: return 1;
+  case Route::Slot: case Route::Skinny: case Route::Mmvq: return 2;
+  case Route::F16Gemm: return 4;
+  case Route::Dq: return 5;
+  default: return 3;
+  }
 }
 
 void ifx_launch_log_begin(int dry_run) {
@@ -375,85 +496,48 @@ int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void
 
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,
               const void *bias, int M, int N, int K, void *stream) {
-  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
-  if (rc != IFX_OK) return rc;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool f16 = out_dtype == IFX_OUT_F16;
-  if (tiled(quant_type)) {  // M <= 32 (checked): the MFMA batch GEMVs
-    if (M <= kMaxSlotM)
-      return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
-    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
-    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s));
-  }
-  if (!gemv_only(quant_type) && M > kMaxSkinnyM && use_f16_gemm(quant_type, M, K))
-    return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, nullptr, Y, bias, f16, M, N, K, mode, 0, s));
-  if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
-      (M > kMaxSkinnyM && K % 256 != 0))
-    return status_of(ifx::launch_gemv(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
-  if (use_lds(quant_type, M, K, N))
-    return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
-  if (use_slot(quant_type, M, K, N, f16))
-    return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
-  if (use_dq(quant_type, M, K, f16))
-    return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s));
-  if (M <= kMaxSkinnyM) {
-    if (use_skinny(M) && K % 256 == 0)
-      return status_of(
-          ifx::launch_mmq_skinny(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
-    return status_of(ifx::launch_mmvq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
-  }
-  return status_of(ifx::launch_gemm_mfma(quant_type, W, A_q8_1, Y, bias, f16, M, N, K, mode, s));
+  return qgemv_impl(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream, nullptr, 0);
+}
+
+int ifx_qgemv_ws(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
+                 int mode, const void *bias, int M, int N, int K, void *workspace,
+                 int64_t workspace_bytes, void *stream) {
+  if (!workspace) return IFX_NULL_POINTER;
+  return qgemv_impl(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream, workspace,
+                    workspace_bytes);
 }
 
 int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *const *Y,
                       const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                       void *stream) {
-  if (!W || !Y || !N) return IFX_NULL_POINTER;
-  if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
-  if (mode == IFX_BIAS) return IFX_BAD_GEOMETRY;
-  for (int i = 0; i < count; ++i) {
-    const int rc = check_gemm_args(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M,
-                                   N[i], K);
-    if (rc != IFX_OK) return rc;
-  }
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool f16 = out_dtype == IFX_OUT_F16;
-  if (tiled(quant_type)) {
-    if (M <= kMaxSlotM)
-      return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M,
-                                             K, mode, s));
-    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
-    return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
-                                         mode, 0, s));
-  }
-  if (gemv_only(quant_type) || row_split(quant_type) || M <= max_gemv_m() ||
-      (M > kMaxSkinnyM && K % 256 != 0))
-    return status_of(
-        ifx::launch_gemv_grouped(quant_type, count, W, Y, N, A_q8_1, f16, M, K, mode, s));
+  return grouped_impl(quant_type, count, W, Y, N, A_q8_1, out_dtype, mode, M, K, stream, nullptr,
+                      0);
+}
+
+int ifx_qgemv_grouped_ws(int quant_type, int count, const void *const *W, void *const *Y,
+                         const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
+                         void *workspace, int64_t workspace_bytes, void *stream) {
+  if (!workspace) return IFX_NULL_POINTER;
+  return grouped_impl(quant_type, count, W, Y, N, A_q8_1, out_dtype, mode, M, K, stream,
+                      workspace, workspace_bytes);
+}
+
+int64_t ifx_qgemv_workspace_bytes(int quant_type, int count, const int *N, int out_dtype, int M,
+                                  int K) {
+  if (!N || count < 1 || count > 3 || !is_weight_type(quant_type) || M <= 0 || K <= 0 ||
+      K % ifx_block_elems(quant_type))
+    return 0;
   int n_total = 0;
-  for (int i = 0; i < count; ++i) n_total += N[i];
-  if (use_lds(quant_type, M, K, n_total))
-    return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
-  if (use_slot(quant_type, M, K, n_total, f16))
-    return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
-                                           mode, s));
-  if (use_dq(quant_type, M, K, f16))
-    return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
-                                         mode, 0, s));
-  if (M <= kMaxSkinnyM) {
-    if (use_skinny(M) && K % 256 == 0)
-      return status_of(ifx::launch_mmq_skinny(quant_type, count, W, Y, N, nullptr, A_q8_1, f16,
-                                              M, K, mode, s));
-    return status_of(ifx::launch_mmvq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
-                                      mode, s));
-  }
-  // batched decode and prefill: one launch per projection (each fills the chip)
   for (int i = 0; i < count; ++i) {
-    const int rc = ifx_qgemv(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],
-                             K, stream);
-    if (rc != IFX_OK) return rc;
+    if (N[i] <= 0) return 0;
+    n_total += N[i];
   }
-  return IFX_OK;
+  const bool f16 = out_dtype == IFX_OUT_F16;
+  switch (route(quant_type, M, K, n_total, f16, count > 1)) {
+  case Route::Slot: return ifx::gemv_slot_workspace_bytes(count, N, f16, M, K);
+  case Route::Dq: return ifx::gemv_dq_workspace_bytes(count, N, f16, M, K);
+  default: return 0;
+  }
 }
 
 int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, void *const *Y,

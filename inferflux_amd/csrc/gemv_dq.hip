@@ -61,6 +61,7 @@ struct DqArgs {
   int nseg;
   const uint8_t *A;
   int M, K, mode, sb_per;
+  SplitWs ws;  // ordered split: counters per row group, 16 KB slot per (group, split)
 };
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -303,7 +304,10 @@ __device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint
 
 // grid: x = row groups of 128 (all projections), y = super-block splits.
 // Dynamic LDS: (M + 1) rows of pitch = sb_per * 256 + 8 halves (row M zero).
-template <int QT, bool F16OUT, bool ATOMIC, bool TL = false>
+// SPLIT: 0 one workgroup per row group; 1 K split, fp32 atomics into Y
+// (zeroed first in store / bias mode); 2 K split, ordered reduction through
+// args.ws (split_arrive_last).
+template <int QT, bool F16OUT, int SPLIT, bool TL = false>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int bx = blockIdx.x;
@@ -354,15 +358,39 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
     if (i + 2 < cnt) step(w2, w1, i + 2);
   }
 
-  if (n >= N) return;
   // lane holds column n and batch rows 8*(i/4) + 4*h + (i%4)
+  float yv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) yv[i] = acc0[i] + acc1[i];
+  if constexpr (SPLIT == 2) {
+    const int ks = gridDim.y;
+    constexpr int kSlot = 64 * 16;  // floats per wave and split
+    float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * kWaves * kSlot +
+                  wave * kSlot + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (8 * (i >> 2) + 4 * h + (i & 3) < M) st_dev(mine + 64 * i, yv[i]);
+    wait_own_memory();
+    if (!split_arrive_last(args.ws.cnt + bx, ks)) return;
+    const float *slot0 = args.ws.part + static_cast<int64_t>(bx) * ks * kWaves * kSlot + wave * kSlot + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (8 * (i >> 2) + 4 * h + (i & 3) >= M) continue;
+      float t = 0.0f;
+      for (int sp = 0; sp < ks; ++sp)
+        t += sp == static_cast<int>(blockIdx.y) ? yv[i] : ld_dev(slot0 + sp * kWaves * kSlot + 64 * i);
+      yv[i] = t;
+    }
+    split_reset(args.ws.cnt + bx);
+  }
+  if (n >= N) return;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int m = 8 * (i >> 2) + 4 * h + (i & 3);
     if (m >= M) continue;
     const int64_t o = static_cast<int64_t>(m) * N + n;
-    float y = acc0[i] + acc1[i];
-    if constexpr (ATOMIC) {
+    float y = yv[i];
+    if constexpr (SPLIT == 1) {
       if (args.mode == 2 && blockIdx.y == 0) y += static_cast<const float *>(sg.bias)[n];
       atomicAdd(static_cast<float *>(sg.Y) + o, y);
     } else if constexpr (F16OUT) {
@@ -398,28 +426,38 @@ int dq_splits(int groups, int nsb, int M, bool f16) {
   return max(need, min(nsb, (target + groups - 1) / groups));
 }
 
-template <int QT, bool TL>
-hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
-  int groups = 0;
+// Row groups and K splits of a launch (sets blk_begin and sb_per).
+void dq_plan(DqArgs &args, bool f16, int splits_req, int &groups, int &ks) {
+  groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = groups;
     groups += (args.seg[i].N + kRowsPerWg - 1) / kRowsPerWg;
   }
   const int nsb = args.K >> 8;
   const int need = (nsb + dq_sb_max(args.M) - 1) / dq_sb_max(args.M);
-  int ks = (splits_req > 0 && !f16) ? max(need, min(splits_req, nsb))
-                                    : dq_splits(groups, nsb, args.M, f16);
-  if (f16 && ks > 1) return hipErrorInvalidValue;  // fp16 outputs cannot be split
+  ks = (splits_req > 0 && !f16) ? max(need, min(splits_req, nsb))
+                                : dq_splits(groups, nsb, args.M, f16);
   args.sb_per = (nsb + ks - 1) / ks;
   ks = (nsb + args.sb_per - 1) / args.sb_per;
+}
+
+template <int QT, bool TL>
+hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
+  const bool ordered = args.ws.cnt != nullptr;
+  int groups = 0, ks = 1;
+  dq_plan(args, f16, splits_req, groups, ks);
+  if (f16 && ks > 1) return hipErrorInvalidValue;  // fp16 outputs cannot be split
   const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
   const dim3 grid(groups, ks), block(64 * kWaves);
   if (f16) {
-    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, true, false, true), grid, block, shm, s, args);
-    else IFX_LAUNCH(k_gemv_dq, (QT, true, false), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, true, 0, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, true, 0), grid, block, shm, s, args);
   } else if (ks == 1) {
-    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, false, true), grid, block, shm, s, args);
-    else IFX_LAUNCH(k_gemv_dq, (QT, false, false), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, 0, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, false, 0), grid, block, shm, s, args);
+  } else if (ordered) {
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, 2, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, false, 2), grid, block, shm, s, args);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -429,8 +467,8 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
       }
       if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return last_error();
     }
-    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, true, true), grid, block, shm, s, args);
-    else IFX_LAUNCH(k_gemv_dq, (QT, false, true), grid, block, shm, s, args);
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, false, 1, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, false, 1), grid, block, shm, s, args);
   }
   return last_error();
 }
@@ -448,11 +486,35 @@ bool gemv_dq_fits_f16(int M, int K) { return M <= kMaxM && K / 256 <= dq_sb_max(
 
 // count projections (1..3) of one quant type share A; bias only with
 // count == 1.  splits_req: 0 = chosen from the shape.
+// Workspace bytes of the ordered split (0: the launch does not split):
+// counters (256-byte aligned) then one 16 KB slot per (row group, split).
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K) {
+  DqArgs args{};
+  for (int i = 0; i < count; ++i) args.seg[i].N = N[i];
+  args.nseg = count;
+  args.M = M;
+  args.K = K;
+  int groups = 0, ks = 1;
+  dq_plan(args, f16, 0, groups, ks);
+  if (ks <= 1 || f16) return 0;
+  return (static_cast<int64_t>(groups) * 4 + 255) / 256 * 256 +
+         static_cast<int64_t>(groups) * ks * kWaves * 64 * 16 * 4;
+}
+
+// ws: the ordered-split workspace (gemv_dq_workspace_bytes, counters zero),
+// or nullptr for atomics.
 hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
-                          int mode, int splits_req, hipStream_t stream) {
+                          int mode, int splits_req, hipStream_t stream, void *ws) {
   if (!gemv_dq_fits(qtype, M, K) || count < 1 || count > 3) return hipErrorInvalidValue;
   DqArgs args{};
+  if (ws) {
+    int groups = 0;
+    for (int i = 0; i < count; ++i) groups += (N[i] + kRowsPerWg - 1) / kRowsPerWg;
+    args.ws.cnt = static_cast<uint32_t *>(ws);
+    args.ws.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                             (static_cast<int64_t>(groups) * 4 + 255) / 256 * 256);
+  }
   for (int i = 0; i < count; ++i)
     args.seg[i] = DqSeg{static_cast<const uint8_t *>(W[i]), Y[i], i == 0 ? bias : nullptr, N[i], 0};
   args.nseg = count;

@@ -64,6 +64,7 @@ struct SlotArgs {
   int nseg;
   const uint8_t *A;
   int M, K, mode;
+  SplitWs ws;  // ordered split: counters per row group, 1 KB slot per (group, split)
   // fused gate/up/SiLU (SW): seg[0] gate, seg[1] up; h = silu(g) * u to H
   // (fp32, fp16 with F16OUT, or none) and its Q8_1 blocks to Q (or none)
   void *H;
@@ -202,11 +203,14 @@ constexpr int slot_lds_bytes() {
 // blocks equal grouped GEMV + silu_mul_quantize bit for bit where the
 // grouped launch runs the same KW (other KW add the super-blocks' partial
 // sums in another order).
-template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool SW = false, bool TL = false>
+// SPLIT: 0 one workgroup per row group; 1 K split over gridDim.y with fp32
+// atomics into Y (zeroed first in store / bias mode); 2 K split with the
+// ordered reduction through args.ws (split_arrive_last, ifx_common.h).
+template <int QT, int MP, int KW, bool F16OUT, int SPLIT, bool SW = false, bool TL = false>
 __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const SlotArgs args) {
   using G = SlotGeo<QT, MP>;
   constexpr int NM = G::kNm;
-  static_assert(!(SW && ATOMIC), "the fused gate/up/SiLU launch does not split K");
+  static_assert(!(SW && SPLIT), "the fused gate/up/SiLU launch does not split K");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int bx = blockIdx.x;
   const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -265,8 +269,8 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
   for (int i = 0; i < NM; ++i) acc[i] = 0.0f;
 
   // this wave's super-blocks: wave index over the split, stride KS * KW
-  const int step = ATOMIC ? KW * static_cast<int>(gridDim.y) : KW;
-  int sb = (ATOMIC ? static_cast<int>(blockIdx.y) * KW : 0) + wave;
+  const int step = SPLIT ? KW * static_cast<int>(gridDim.y) : KW;
+  int sb = (SPLIT ? static_cast<int>(blockIdx.y) * KW : 0) + wave;
   WSb<QT> wc;
   ASb<QT, MP> ac;
   if (sb < nsb) {
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       for (int mi = 0; mi < NM; ++mi) red[((wave - 1) * NM + mi) * 64 + lane] = acc[mi];
     }
     __syncthreads();
-    if (!SW && wave > 0) return;
+    if (!SW && SPLIT != 2 && wave > 0) return;
     if (wave == 0) {
 #pragma unroll
       for (int w = 0; w < KW - 1; ++w)
@@ -420,6 +424,27 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
     }
     return;
   }
+  if constexpr (SPLIT == 2) {
+    const int ks = gridDim.y;
+    float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * 64 * NM + lane;
+    if (wave == 0) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+        if (2 * (mi & ~3) + 4 * h + (mi & 3) < M) st_dev(mine + 64 * mi, acc[mi]);
+      wait_own_memory();
+    }
+    if (!split_arrive_last(args.ws.cnt + bx, ks) || wave > 0) return;
+    const float *slot0 = args.ws.part + static_cast<int64_t>(bx) * ks * 64 * NM + lane;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      if (2 * (mi & ~3) + 4 * h + (mi & 3) >= M) continue;
+      float t = 0.0f;
+      for (int sp = 0; sp < ks; ++sp)
+        t += sp == static_cast<int>(blockIdx.y) ? acc[mi] : ld_dev(slot0 + sp * 64 * NM + 64 * mi);
+      acc[mi] = t;
+    }
+    split_reset(args.ws.cnt + bx);
+  }
   const int n = n0 + c32;
   if (n >= N) return;
   const int mode = args.mode;
@@ -429,7 +454,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
     if (m >= M) continue;
     const int64_t o = static_cast<int64_t>(m) * N + n;
     float y = acc[mi];
-    if constexpr (ATOMIC) {
+    if constexpr (SPLIT == 1) {
       // Y was zeroed (store/bias) or holds the accumulate base
       if (mode == 2 && blockIdx.y == 0) y += static_cast<const float *>(sg.bias)[n];
       atomicAdd(static_cast<float *>(sg.Y) + o, y);
@@ -478,23 +503,25 @@ void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
   ks = f16 ? 1 : max(1, min(ks, nsb / kw));
 }
 
-template <int QT, int MP, int KW, bool F16OUT, bool ATOMIC, bool TL>
+template <int QT, int MP, int KW, bool F16OUT, int SPLIT, bool TL>
 void slot_launch(const SlotArgs &args, int blocks, int ks, hipStream_t s) {
   constexpr int lds = slot_lds_bytes<QT, MP, KW>();
   if constexpr (TL)
-    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC, false, true), dim3(blocks, ks),
+    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, SPLIT, false, true), dim3(blocks, ks),
                dim3(64 * KW), lds, s, args);
   else
-    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, ATOMIC), dim3(blocks, ks), dim3(64 * KW), lds,
+    IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, F16OUT, SPLIT), dim3(blocks, ks), dim3(64 * KW), lds,
                s, args);
 }
 
 template <int QT, int MP, int KW, bool TL>
 void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t s) {
   if (f16) {
-    slot_launch<QT, MP, KW, true, false, TL>(args, blocks, 1, s);
+    slot_launch<QT, MP, KW, true, 0, TL>(args, blocks, 1, s);
   } else if (ks == 1) {
-    slot_launch<QT, MP, KW, false, false, TL>(args, blocks, 1, s);
+    slot_launch<QT, MP, KW, false, 0, TL>(args, blocks, 1, s);
+  } else if (args.ws.cnt) {
+    slot_launch<QT, MP, KW, false, 2, TL>(args, blocks, ks, s);
   } else {
     if (args.mode != 1) {  // store / bias: the splits add into zeroed outputs
       FillArgs f{};
@@ -505,7 +532,7 @@ void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t 
       // a failed fill stays set for the caller's hipGetLastError
       if (launch_fill_zero(f, args.nseg, s) != hipSuccess) return;
     }
-    slot_launch<QT, MP, KW, false, true, TL>(args, blocks, ks, s);
+    slot_launch<QT, MP, KW, false, 1, TL>(args, blocks, ks, s);
   }
 }
 
@@ -570,15 +597,35 @@ bool gemv_slot_fits(int qtype, int M, int K) {
 
 // count projections (1..3) share A; geometry checked by the caller
 // (gemv_slot_fits, 32-bit byte ranges).
+// Workspace bytes of the ordered split (0: the launch does not split):
+// counters (256-byte aligned) then one 1 KB slot per (row group, split).
+int64_t gemv_slot_workspace_bytes(int count, const int *N, bool f16, int M, int K) {
+  (void)M;
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) blocks += (N[i] + 31) / 32;
+  int kw = 8, ks = 1;
+  choose_slot_work(blocks, K >> 8, f16, kw, ks);
+  if (ks <= 1 || f16) return 0;
+  return (static_cast<int64_t>(blocks) * 4 + 255) / 256 * 256 +
+         static_cast<int64_t>(blocks) * ks * 64 * 4 * 4;
+}
+
+// ws: the ordered-split workspace (gemv_slot_workspace_bytes, counters
+// zero), or nullptr for atomics.
 hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *const *Y,
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
-                            int mode, hipStream_t stream) {
+                            int mode, hipStream_t stream, void *ws) {
   if (!gemv_slot_fits(qtype, M, K) || count < 1 || count > 3) return hipErrorInvalidValue;
   SlotArgs args{};
   int blocks = 0;
   for (int i = 0; i < count; ++i) {
     args.seg[i] = SlotSeg{static_cast<const uint8_t *>(W[i]), Y[i], i == 0 ? bias : nullptr, N[i], blocks};
     blocks += (N[i] + 31) / 32;
+  }
+  if (ws) {
+    args.ws.cnt = static_cast<uint32_t *>(ws);
+    args.ws.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                             (static_cast<int64_t>(blocks) * 4 + 255) / 256 * 256);
   }
   args.nseg = count;
   args.A = static_cast<const uint8_t *>(A);

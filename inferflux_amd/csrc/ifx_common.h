@@ -236,6 +236,51 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
+// Waits until every memory operation this wave issued has completed (its
+// device-coherent stores included).  The compiler fences keep the memory
+// operations around it on their side.
+__device__ __forceinline__ void wait_own_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Device-coherent fp32 store / load (relaxed, agent scope): data that other
+// workgroups of the same launch read, on any XCD, without cache write-back
+// or invalidation.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Ordered K-split reduction (the workspace entry points): every workgroup of
+// a split tile stores its fp32 partial sums to its own workspace slot with
+// st_dev, each wave waits for its stores (wait_own_memory), and the
+// workgroup then counts itself in on the tile's counter.  The workgroup that
+// arrives last adds the slots in split order 0, 1, ... (ld_dev), so the
+// result does not depend on which workgroup finishes last, applies the
+// epilogue and resets the counter to zero for the next launch.  No
+// workgroup waits for another, so no co-residency is assumed.  Returns true
+// in the last workgroup (all threads).
+struct SplitWs {
+  uint32_t *cnt;  // one counter per tile, zero between launches
+  float *part;    // partial-sum slots
+};
+__device__ __forceinline__ bool split_arrive_last(uint32_t *cnt, int ks) {
+  __shared__ uint32_t last;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           static_cast<uint32_t>(ks - 1);
+  __syncthreads();
+  return last != 0;
+}
+__device__ __forceinline__ void split_reset(uint32_t *cnt) {
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Zeroes up to three fp32 outputs before a split-K launch adds into them
 // (mmq_skinny.hip); blockIdx.y selects the output.
 struct FillArgs {

@@ -63,14 +63,6 @@ constexpr int kFfnR = 3;           // gate (up) rows per half-wave: 16 half-wave
 constexpr int kFfnGuRows = 16 * kFfnR;  // outputs per workgroup at most
 constexpr int kFfnDownWaves = 12;  // waves 4-15 hold the down rows
 
-// Waits until every memory operation this wave issued has completed (its
-// device-coherent stores included).  The compiler fences keep the memory
-// operations around it on their side.
-__device__ __forceinline__ void wait_own_memory() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // Grid barrier over all workgroups of the launch (all resident: one per CU),
 // in two halves so a workgroup can issue loads between arriving and

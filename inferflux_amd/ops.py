@@ -114,8 +114,10 @@ def silu_mul_quantize_q8_1(gate, up, out=None, stream=None):
 
 
 def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, bias=None,
-          stream=None, prefill=False):
-    """y [M, N] (op)= W . a with raw GGUF W and Q8_1 A (all device tensors)."""
+          stream=None, prefill=False, workspace=None):
+    """y [M, N] (op)= W . a with raw GGUF W and Q8_1 A (all device tensors).
+    workspace: a uint8 device tensor (qgemv_workspace_bytes, zeroed once)
+    for the deterministic K-split reduction (ifx_qgemv_ws)."""
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=W.device)
     od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
@@ -129,11 +131,27 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     if out.numel() < M * N:
         raise ValueError("out is smaller than M x N")
     bptr = _dev(bias, "bias") if bias is not None else None
+    if workspace is not None:
+        rc = _lib.load().ifx_qgemv_ws(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"), od,
+                                      mode, bptr, M, N, K, _dev(workspace, "workspace"),
+                                      workspace.numel() * workspace.element_size(),
+                                      _stream(stream))
+        _check(rc, "ifx_qgemv_ws")
+        return out
     fn = _lib.load().ifx_qgemm_prefill if prefill else _lib.load().ifx_qgemv
     rc = fn(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"), od, mode, bptr, M, N, K,
             _stream(stream))
     _check(rc, "ifx_qgemm_prefill" if prefill else "ifx_qgemv")
     return out
+
+
+def qgemv_workspace_bytes(qtype, Ns, M, K, out_dtype=torch.float32):
+    """Bytes of workspace the deterministic split of qgemv / qgemv_grouped
+    needs for projections of Ns rows (0: the launch does not split)."""
+    import ctypes
+    nn = (ctypes.c_int * len(Ns))(*Ns)
+    od = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    return int(_lib.load().ifx_qgemv_workspace_bytes(qtype, len(Ns), nn, od, M, K))
 
 
 def prefill_workspace_bytes(qtype, M, N, K):
@@ -204,7 +222,7 @@ def qgemm_prefill_kernel(qtype, W, A, M, N, K, kernel, splits=0, out=None,
 
 
 def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mode=STORE,
-                  stream=None):
+                  stream=None, workspace=None):
     """Sibling projections over one Q8_1 A: [W_i . a for W_i in Ws], one launch
     for M <= 2.  Returns the list of outputs [M, N_i]."""
     import ctypes
@@ -224,6 +242,13 @@ def qgemv_grouped(qtype, Ws, A, M, Ns, K, outs=None, out_dtype=torch.float32, mo
     wp = (ctypes.c_void_p * count)(*[_dev(w, "W") for w in Ws])
     yp = (ctypes.c_void_p * count)(*[_dev(y, "out") for y in outs])
     nn = (ctypes.c_int * count)(*Ns)
+    if workspace is not None:
+        rc = _lib.load().ifx_qgemv_grouped_ws(qtype, count, wp, yp, nn, _dev(A, "A"), od, mode, M,
+                                              K, _dev(workspace, "workspace"),
+                                              workspace.numel() * workspace.element_size(),
+                                              _stream(stream))
+        _check(rc, "ifx_qgemv_grouped_ws")
+        return outs
     rc = _lib.load().ifx_qgemv_grouped(qtype, count, wp, yp, nn, _dev(A, "A"), od, mode, M, K,
                                        _stream(stream))
     _check(rc, "ifx_qgemv_grouped")
