@@ -153,7 +153,13 @@ def main():
         return {"median_us": round(float(med), 2), "p10_us": round(float(p10), 2),
                 "p90_us": round(float(p90), 2), "replays": reps, "calls_per_replay": steps}
 
-    def decode_layer_runner(layer, M, seed, fused=False, split_down=False):
+    def tiled_layer(layer):
+        """The layer's weights as tiled copies (ifx_repack_tiled), per replica."""
+        return {name: (qt + 200, N, K, [ops.repack_tiled(qt, w, N, K)[1] for w in reps])
+                for name, (qt, N, K, reps) in layer.items()}
+
+    def decode_layer_runner(layer, M, seed, fused=False, split_down=False, tiled=None,
+                            ordered=False):
         """One decode layer at batch M as a chain over an fp32 residual
         stream: RMSNorm+Q8_1 -> grouped QKV -> Q8_1 of the attention output
         (synthetic: attention itself is not on this path) -> O accumulated
@@ -173,8 +179,13 @@ def main():
         (ifx_qgemv_gate_up_silu): 3 producers + 4 GEMVs.
         split_down: the down projection reads a row-split copy of its Q6_K
         weights (ifx_repack, M <= 2).
+        tiled: the layer's tiled copy (tiled_layer) the GEMVs read instead
+        (M <= 32).  ordered: K-split launches reduce in split order through a
+        workspace per launch (ifx_qgemv_ws / ifx_qgemv_grouped_ws).
         run(i, which) runs one launch kind alone ("qkv", "o", "gate_up",
         "down", "producers"; "ffn": the FFN kernel of the "ffn" form alone)."""
+        if tiled is not None:
+            layer = tiled
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
         rng = np.random.default_rng(seed)
         resid = torch.from_numpy(rng.standard_normal((M, hidden)).astype(np.float32)).to(dev)
@@ -194,6 +205,13 @@ def main():
         if split_down:
             qt, N, K, reps = layer["down"]
             down_w = (ops.Q6_K_R, N, K, [ops.repack(qt, w, N, K)[1] for w in reps])
+        wsd = {}
+        if ordered:
+            for l in workloads.DECODE_LAUNCHES:
+                qt_, _, K_, _ = layer[l[1][0]]
+                nb = ops.qgemv_workspace_bytes(qt_, [layer[p][1] for p in l[1]], M, K_)
+                if nb:
+                    wsd[l[0]] = torch.zeros(nb, dtype=torch.uint8, device=dev)
         ws = None
         if fused == "ffn":
             ws = torch.zeros(ops.decode_ffn_workspace_bytes(M, ffn), dtype=torch.uint8, device=dev)
@@ -205,11 +223,13 @@ def main():
             if len(projs) == 1:
                 p = down_w if projs[0] == "down" else layer[projs[0]]
                 qt = p[0]
-                ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode)
+                ops.qgemv(qt, p[3][r], A[src], M, p[1], K, out=Y[projs[0]], mode=mode,
+                          workspace=wsd.get(lname))
             else:
                 ops.qgemv_grouped(qt, [layer[p][3][r] for p in projs], A[src], M,
                                   [layer[p][1] for p in projs], K,
-                                  outs=[Y[p] for p in projs], mode=mode)
+                                  outs=[Y[p] for p in projs], mode=mode,
+                                  workspace=wsd.get(lname))
 
         def gemv_norm(lname, r, x, nw):
             _, projs, _, accum = launches[lname]
@@ -335,6 +355,7 @@ def main():
                        for M in (1, 4, 8)}
     per_m = {}
     forms = {}  # M = 1 layer forms: name -> (runner, us per layer, kernel us, kernel bytes)
+    layer3b_t = tiled_layer(layer3b)  # the batch forms' tiled copy (M = 4, 8)
     for M in (1, 4, 8):
         run = decode_layer_runner(layer3b, M, seed=10 + M)
         steps = args.steps if M == 1 else max(20, args.steps // 2)
@@ -368,6 +389,17 @@ def main():
                 "kernel_us": {n: round(time_loop(lambda i, n=n: runb(i, n), steps, args.warmup), 2)
                               for n in ("qkv", "o", "gate_up", "down", "producers")},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_b * 1e-6), 1),
+            }
+            # the same on the tiled weights, K splits reduced in order
+            runt = decode_layer_runner(layer3b, M, seed=10 + M, fused="batch_swiglu",
+                                       tiled=layer3b_t, ordered=True)
+            us_t = time_loop(runt, steps, args.warmup)
+            per_m[M]["tiled_swiglu_ordered"] = {
+                "us_per_layer": round(us_t, 2),
+                "layer_GBs": round(layer_alg_bytes[M] / us_t / 1e3, 1),
+                "kernel_us": {n: round(time_loop(lambda i, n=n: runt(i, n), steps, args.warmup), 2)
+                              for n in ("qkv", "o", "gate_up", "down", "producers")},
+                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_t * 1e-6), 1),
             }
         if M == 1:
             fb = form_kernel_bytes(layer3b, M, "reference")
@@ -446,7 +478,7 @@ def main():
     p_us = time_loop(probe_step, 200, 10)
     result["roofline"]["read_probe_same_bytes_GBs"] = round(wbytes / p_us / 1e3, 1)
     del big
-    del layer3b, forms, step_run
+    del layer3b, layer3b_t, forms, step_run
     torch.cuda.empty_cache()
 
     if not args.quick:
@@ -502,20 +534,26 @@ def main():
         projs14 = workloads.QWEN14B_LAYER
         layer14 = make_layer(projs14, seed=4, replicas=n_replicas(layer_bytes(projs14)))
         c4 = {}
+        layer14_t = tiled_layer(layer14)
         for M in (16, 32):
-            run = decode_layer_runner(layer14, M, seed=40 + M)
-            steps = max(20, args.steps // 4)
-            us_layer = time_loop(run, steps, 5)
-            kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
-                    for l in workloads.DECODE_LAUNCHES}
             all_bytes = sum(launch_bytes(layer14, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
-            c4[f"M{M}"] = {
-                "us_per_layer": round(us_layer, 2),
-                "layer_GBs": round(all_bytes / us_layer / 1e3, 1),
-                "gemv_GBs": round(all_bytes / sum(kern.values()) / 1e3, 1),
-                "kernel_us": {k: round(v, 2) for k, v in kern.items()},
-                "tokens_per_s_equiv": round(M / (workloads.QWEN14B_LAYERS * us_layer * 1e-6), 1),
-            }
+            steps = max(20, args.steps // 4)
+            for key, kw in ((f"M{M}", {}),
+                            (f"M{M}_tiled_ordered", {"tiled": layer14_t, "ordered": True})):
+                run = decode_layer_runner(layer14, M, seed=40 + M, **kw)
+                us_layer = time_loop(run, steps, 5)
+                kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
+                        for l in workloads.DECODE_LAUNCHES}
+                kern["producers_x4"] = time_loop(lambda i: run(i, "producers"), steps, 5)
+                c4[key] = {
+                    "us_per_layer": round(us_layer, 2),
+                    "layer_GBs": round(all_bytes / us_layer / 1e3, 1),
+                    "gemv_GBs": round(all_bytes / sum(v for k, v in kern.items()
+                                                      if k != "producers_x4") / 1e3, 1),
+                    "kernel_us": {k: round(v, 2) for k, v in kern.items()},
+                    "tokens_per_s_equiv": round(M / (workloads.QWEN14B_LAYERS * us_layer * 1e-6), 1),
+                }
+        del layer14_t
         # the Q4_K launches of the 14B layer at M = 1 and 8 (the 70 %-of-HBM
         # target names the 3B and the 14B shapes at those M)
         q4 = {}

@@ -155,7 +155,7 @@ int64_t ifx_qgemv_workspace_bytes(int quant_type, int count, const int *N, int o
  * first weight loads, so the producer's launch and the Q8_1 round trip
  * through memory disappear from the decode layer.  residual [M][K] fp32 or
  * fp16 (residual_dtype: ifx_out_dtype), norm_weight fp16 [K] or NULL.  Handles
- * Q4_K, 1 <= M <= 2, M * K/32 * 36 <= 65536; other shapes return
+ * Q4_K, 1 <= M <= 2, M * (80 K/64 + K/8) <= 65536; other shapes return
  * IFX_BAD_GEOMETRY (not handled: use the two calls).  mode: IFX_STORE or
  * IFX_ACCUM.  No reference counterpart as one call: it fuses
  * FusedQuantGemm::FusedRmsNormQuantizeQ8_1 (fused_quant_gemm.h:131-150)

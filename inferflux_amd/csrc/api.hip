@@ -8,7 +8,7 @@
 // reference, launch errors are checked (hipGetLastError after each launch)
 // and returned as a negative status.
 #include "../../include/ifx_qgemm.h"
-#include "ifx_common.h"
+#include "ifx_q8_1.h"
 
 #include <stdlib.h>
 
@@ -557,7 +557,7 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
     if (rc != IFX_OK) return rc;
   }
   if (quant_type != IFX_TYPE_Q4_K || M > 2 ||
-      static_cast<int64_t>(M) * (K / 32) * ifx::kQ8_1Bytes > 65536)
+      static_cast<int64_t>(M) * ifx::split_row_bytes(K) > 65536)  // the LDS activation rows
     return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_gemv_rmsnorm(count, W, Y, N, residual,
                                             residual_dtype == IFX_OUT_F16, norm_weight, eps,
@@ -703,7 +703,7 @@ int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype
     rc = check_gemm_args(o_type, W_o, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M, hidden,
                          q_dim);
     // the O launch: the fused-quantizer GEMV's activation tile fits its LDS
-    if (rc == IFX_OK && (q_dim % 256 || q_dim / 32 * ifx::kQ8_1Bytes > 65536))
+    if (rc == IFX_OK && (q_dim % 256 || ifx::split_row_bytes(q_dim) > 65536))
       rc = IFX_BAD_GEOMETRY;
   }
   if (rc == IFX_OK)

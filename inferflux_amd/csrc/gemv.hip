@@ -195,7 +195,8 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   const int nslice = K / SV;
   if constexpr (NORM != 0) {
     constexpr bool kXF16 = NORM == 2 || NORM == 4, kRms = NORM <= 2;
-    extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // [MC][K/32] Q8_1
+    extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // [MC] split rows
+    const uint32_t a_str = split_row_bytes(K);
     __shared__ float npart[4 * MC];
     const int s0 = gw * LPR + lt;
     Q4Wide<R> wt;
@@ -206,36 +207,38 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       f32x4 xr[MC][2];
       u32x2 wr[MC][2];
 #pragma unroll
-      for (int c = 0; c < MC; ++c)
-        if (c < mvalid)
-          rmsnorm_row_load<kXF16, 2>(args.x, static_cast<int64_t>(col0 + c) * K,
-                                     kRms ? args.norm_w : nullptr, K, threadIdx.x, xr[c], wr[c]);
-      if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
+      for (int c = 0; c < MC; ++c)  // columns past M re-read the last one (unused)
+        rmsnorm_row_load_nb<kXF16, 2, kRms>(args.x, static_cast<int64_t>(col0 + min(c, mvalid - 1)) * K,
+                                            args.norm_w, K, threadIdx.x, xr[c], wr[c]);
+      // keep the activation loads ahead of the weight loads in issue order
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_sched_barrier(0);
+      q4k_wide_load<R>(wt, Wr, voff, soff, min(s0, nslice - 1));  // unconditional: no wait on it
 #pragma unroll
       for (int c = 0; c < MC; ++c)
         if (c < mvalid) {
           if constexpr (kRms)
-            rmsnorm_row_finish<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
+            rmsnorm_row_finish<2, true>(xr[c], wr[c], a_lds + c * a_str, K, args.eps, npart + 4 * c,
                                   threadIdx.x);
           else
-            quantize_row_finish<2>(xr[c], a_lds + c * a_row, K, threadIdx.x);
+            quantize_row_finish<2, true>(xr[c], a_lds + c * a_str, K, threadIdx.x);
         }
     } else {
 #pragma unroll
       for (int c = 0; c < MC; ++c)
         if (c < mvalid) {
           if constexpr (kRms)
-            rmsnorm_quantize_row<kXF16>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w,
-                                        a_lds + c * a_row, K, args.eps, npart + 4 * c,
+            rmsnorm_quantize_row<kXF16, true>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w,
+                                        a_lds + c * a_str, K, args.eps, npart + 4 * c,
                                         threadIdx.x);
           else
-            quantize_row<kXF16>(args.x, static_cast<int64_t>(col0 + c) * K, a_lds + c * a_row, K,
+            quantize_row<kXF16, true>(args.x, static_cast<int64_t>(col0 + c) * K, a_lds + c * a_str, K,
                                 threadIdx.x);
         }
       if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
     }
     __syncthreads();
-    const ALds as{a_lds, a_row};
+    const ALdsS as{a_lds, a_str, static_cast<uint32_t>(K / 64 * 80)};
     for (int s = s0; s < nslice; s += LPR * G) {
       if (s != s0) q4k_wide_load<R>(wt, Wr, voff, soff, s);
       q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);
@@ -439,7 +442,7 @@ static void launch_norm_t(GemvArgs args, bool f16, hipStream_t s) {
     blocks += (groups + P - 1) / P;
   }
   const dim3 grid(blocks, (args.M + MC - 1) / MC);
-  const size_t shm = static_cast<size_t>(MC) * (args.K >> 5) * kQ8_1Bytes;
+  const size_t shm = static_cast<size_t>(MC) * split_row_bytes(args.K);
   if (f16)
     IFX_LAUNCH(k_gemv, (kTypeQ4_K, MC, R, G, P, true, H, NORM), grid, dim3(256), shm, s,
                        args);
@@ -614,7 +617,7 @@ template <int MC, bool F16H, int NORM>
 __global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args) {
   constexpr int R = 2;
   __shared__ float gu[2][MC][32];  // [gate/up][column][output]
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[NORM ? MC * (kSwigluWideMaxK / 32) * kQ8_1Bytes : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[NORM ? MC * split_row_bytes(kSwigluWideMaxK) : 1];
   __shared__ float npart[4 * MC];
   const int M = args.M, N = args.N, K = args.K;
   const int lane = threadIdx.x & 63;
@@ -646,14 +649,16 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args
     const bool prod = threadIdx.x < 256;  // waves 0-3
     f32x4 xr[MC][2];
     u32x2 wr[MC][2];
-    if (prod) {
+    // every wave loads (the non-producer waves the producers' elements,
+    // unused), so no branch surrounds the loads
 #pragma unroll
-      for (int c = 0; c < MC; ++c)
-        if (c < mvalid)
-          rmsnorm_row_load<kXF16, 2>(args.x, static_cast<int64_t>(col0 + c) * K, args.norm_w, K,
-                                     threadIdx.x, xr[c], wr[c]);
-    }
-    if (lt < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, lt);
+    for (int c = 0; c < MC; ++c)
+      rmsnorm_row_load_nb<kXF16, 2, true>(args.x, static_cast<int64_t>(col0 + min(c, mvalid - 1)) * K,
+                                          args.norm_w, K, threadIdx.x, xr[c], wr[c]);
+    // keep the activation loads ahead of the weight loads in issue order
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    q4k_wide_load<R>(wt, Wr, voff, soff, min(lt, nslice - 1));  // unconditional (see above)
     if (prod) {
 #pragma unroll
       for (int c = 0; c < MC; ++c)
@@ -664,11 +669,11 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args
 #pragma unroll
       for (int c = 0; c < MC; ++c)
         if (c < mvalid)
-          rmsnorm_row_apply<2>(xr[c], wr[c], a_lds + c * a_row, K, args.eps, npart + 4 * c,
+          rmsnorm_row_apply<2, true>(xr[c], wr[c], a_lds + c * split_row_bytes(K), K, args.eps, npart + 4 * c,
                                threadIdx.x);
     }
     __syncthreads();
-    const ALds as{a_lds, a_row};
+    const ALdsS as{a_lds, static_cast<uint32_t>(split_row_bytes(K)), static_cast<uint32_t>(K / 64 * 80)};
     for (int s = lt; s < nslice; s += 32) {
       if (s != lt) q4k_wide_load<R>(wt, Wr, voff, soff, s);
       q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);

@@ -434,15 +434,29 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       wait_own_memory();
     }
     if (!split_arrive_last(args.ws.cnt + bx, ks) || wave > 0) return;
+    // all slots, this workgroup's included, in split order; eight slots'
+    // loads in flight at a time
     const float *slot0 = args.ws.part + static_cast<int64_t>(bx) * ks * 64 * NM + lane;
+    float t[NM];
 #pragma unroll
-    for (int mi = 0; mi < NM; ++mi) {
-      if (2 * (mi & ~3) + 4 * h + (mi & 3) >= M) continue;
-      float t = 0.0f;
-      for (int sp = 0; sp < ks; ++sp)
-        t += sp == static_cast<int>(blockIdx.y) ? acc[mi] : ld_dev(slot0 + sp * 64 * NM + 64 * mi);
-      acc[mi] = t;
+    for (int mi = 0; mi < NM; ++mi) t[mi] = 0.0f;
+    for (int sp0 = 0; sp0 < ks; sp0 += 8) {
+      float v[8][NM];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float *src = slot0 + min(sp0 + j, ks - 1) * 64 * NM;
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) v[j][mi] = ld_dev(src + 64 * mi);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (sp0 + j < ks) {
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) t[mi] += v[j][mi];
+        }
     }
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) acc[mi] = t[mi];
     split_reset(args.ws.cnt + bx);
   }
   const int n = n0 + c32;

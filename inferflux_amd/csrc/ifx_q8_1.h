@@ -25,8 +25,8 @@ __device__ __forceinline__ void store_dev(uint32_t *p, uint32_t v) {
 #pragma clang fp contract(off)
 // DEV: write the block with device-coherent stores (store_dev).
 template <bool DEV = false>
-__device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, float x3,
-                                                uint8_t *blk, int l) {
+__device__ __forceinline__ void quantize4_store_to(float x0, float x1, float x2, float x3,
+                                                   uint8_t *codes, uint8_t *ds_p, int l) {
   // max and the integer sum over the 8 lanes of the block: DPP moves
   // (VALU, no LDS round trip): swap pairs, swap pairs of pairs, then the
   // mirror within each 8 lanes pairs every lane with one of the other quad.
@@ -53,14 +53,43 @@ __device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, fl
                           ((static_cast<uint32_t>(q1) & 0xFFu) << 8) |
                           ((static_cast<uint32_t>(q2) & 0xFFu) << 16) |
                           ((static_cast<uint32_t>(q3) & 0xFFu) << 24);
-  if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(blk + 4 + 4 * l), packed);
-  else *reinterpret_cast<uint32_t *>(blk + 4 + 4 * l) = packed;
+  if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(codes + 4 * l), packed);
+  else *reinterpret_cast<uint32_t *>(codes + 4 * l) = packed;
   if (l == 0) {
     const float s = materialize_f32(d * static_cast<float>(sum));  // fp32 first, then fp16
     const uint32_t ds = f2h_bits(d) | (f2h_bits(s) << 16);
-    if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(blk), ds);
-    else *reinterpret_cast<uint32_t *>(blk) = ds;
+    if constexpr (DEV) store_dev(reinterpret_cast<uint32_t *>(ds_p), ds);
+    else *reinterpret_cast<uint32_t *>(ds_p) = ds;
   }
+}
+
+// One Q8_1 block at blk (codes at blk + 4, d | s at blk).
+template <bool DEV = false>
+__device__ __forceinline__ void quantize4_store(float x0, float x1, float x2, float x3,
+                                                uint8_t *blk, int l) {
+  quantize4_store_to<DEV>(x0, x1, x2, x3, blk + 4, blk, l);
+}
+
+// The LDS activation layout of the fused-producer GEMVs (split): per row of
+// K values, the codes of block pairs in 80-byte slots (block 2q at 80 q,
+// 2q + 1 at 80 q + 32; the 16-byte pad puts the 64-byte reads of
+// consecutive lanes on distinct bank groups), then d | s of block b at
+// 80 K / 64 + 4 b.  Every field is read with aligned 16- / 8-byte loads.
+__host__ __device__ constexpr int split_row_bytes(int K) { return K / 64 * 80 + K / 8; }
+__device__ __forceinline__ uint8_t *split_codes(uint8_t *row, int b) {
+  return row + (b >> 1) * 80 + (b & 1) * 32;
+}
+__device__ __forceinline__ uint8_t *split_ds(uint8_t *row, int K, int b) {
+  return row + K / 64 * 80 + 4 * b;
+}
+// Block b of a row in the layout SPLIT selects.
+template <bool SPLIT>
+__device__ __forceinline__ void quantize4_row_store(float x0, float x1, float x2, float x3,
+                                                    uint8_t *row, int K, int b, int l) {
+  if constexpr (SPLIT)
+    quantize4_store_to(x0, x1, x2, x3, split_codes(row, b), split_ds(row, K, b), l);
+  else
+    quantize4_store(x0, x1, x2, x3, row + b * kQ8_1Bytes, l);
 }
 
 // fp32 or fp16 (IEEE binary16 bits) activations, four at element i.
@@ -84,7 +113,7 @@ __device__ __forceinline__ f32x4 load4(const void *p, int64_t i) {
 // (the standalone producer and that GEMV) runs this same code, so their
 // codes are identical.  The square root and division are correctly
 // rounded (the reference evaluates rsqrtf).
-template <bool F16>
+template <bool F16, bool SPLIT = false>
 __device__ __forceinline__ void rmsnorm_quantize_row(const void *x, int64_t base,
                                                      const uint16_t *w, uint8_t *orow, int K,
                                                      float eps, float *part, int tid) {
@@ -109,7 +138,7 @@ __device__ __forceinline__ void rmsnorm_quantize_row(const void *x, int64_t base
     const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
     const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
     const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
-    quantize4_store(y0, y1, y2, y3, orow + b * kQ8_1Bytes, l);
+    quantize4_row_store<SPLIT>(y0, y1, y2, y3, orow, K, b, l);
   }
 }
 
@@ -143,6 +172,24 @@ __device__ __forceinline__ void rmsnorm_row_load(const void *x, int64_t base, co
   }
 }
 
+// rmsnorm_row_load with no branch around the loads, for kernels that issue
+// their weight loads right after it: a load under a branch makes the
+// compiler wait for every outstanding load (the weights included) at the
+// branch's end, before the producer's arithmetic.  Elements past K re-read
+// element K - 4 (their values are never used); thread t may be any thread
+// id (its low 8 bits select the elements).  HAS_W: load the norm weight.
+template <bool F16, int NIT, bool HAS_W>
+__device__ __forceinline__ void rmsnorm_row_load_nb(const void *x, int64_t base,
+                                                    const uint16_t *w, int K, int tid,
+                                                    f32x4 (&xr)[NIT], u32x2 (&wr)[NIT]) {
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int i = min(4 * (tid & 255) + 1024 * j, K - 4);
+    xr[j] = load4<F16>(x, base + i);
+    if constexpr (HAS_W) wr[j] = ldg<u32x2>(w + i);
+  }
+}
+
 // rmsnorm_row_finish in two phases around a barrier that the caller
 // executes (a workgroup larger than the 256 producer threads runs the
 // barrier on every wave): rmsnorm_row_partial writes the four waves' sums of
@@ -159,7 +206,7 @@ __device__ __forceinline__ void rmsnorm_row_partial(const f32x4 (&xr)[NIT], int 
   if ((tid & 63) == 63) part[tid >> 6] = ss;
 }
 
-template <int NIT>
+template <int NIT, bool SPLIT = false>
 __device__ __forceinline__ void rmsnorm_row_apply(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
                                                   uint8_t *orow, int K, float eps,
                                                   const float *part, int tid) {
@@ -176,19 +223,19 @@ __device__ __forceinline__ void rmsnorm_row_apply(const f32x4 (&xr)[NIT], const 
       const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
       const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
       const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
-      quantize4_store(y0, y1, y2, y3, orow + (i >> 5) * kQ8_1Bytes, l);
+      quantize4_row_store<SPLIT>(y0, y1, y2, y3, orow, K, i >> 5, l);
     }
   }
 }
 
 // 256 threads exactly.
-template <int NIT>
+template <int NIT, bool SPLIT = false>
 __device__ __forceinline__ void rmsnorm_row_finish(const f32x4 (&xr)[NIT], const u32x2 (&wr)[NIT],
                                                    uint8_t *orow, int K, float eps, float *part,
                                                    int tid) {
   rmsnorm_row_partial<NIT>(xr, K, part, tid);
   __syncthreads();
-  rmsnorm_row_apply<NIT>(xr, wr, orow, K, eps, part, tid);
+  rmsnorm_row_apply<NIT, SPLIT>(xr, wr, orow, K, eps, part, tid);
 }
 
 // SiLU(g) * u (the standalone producer's arithmetic), of one and of four values.
@@ -205,24 +252,24 @@ __device__ __forceinline__ f32x4 silu_mul4(f32x4 g, f32x4 u) {
 // Plain Q8_1 of one row (no norm) in the same element-to-thread mapping:
 // thread t quantizes elements 4t + 1024j as one of the 8 lanes of their
 // block, which is exactly what the standalone quantizer computes per block.
-template <int NIT>
+template <int NIT, bool SPLIT = false>
 __device__ __forceinline__ void quantize_row_finish(const f32x4 (&xr)[NIT], uint8_t *orow, int K,
                                                     int tid) {
   const int l = tid & 7;
 #pragma unroll
   for (int j = 0; j < NIT; ++j) {
     const int i = 4 * tid + 1024 * j;
-    if (i < K) quantize4_store(xr[j].x, xr[j].y, xr[j].z, xr[j].w, orow + (i >> 5) * kQ8_1Bytes, l);
+    if (i < K) quantize4_row_store<SPLIT>(xr[j].x, xr[j].y, xr[j].z, xr[j].w, orow, K, i >> 5, l);
   }
 }
 
-template <bool F16>
+template <bool F16, bool SPLIT = false>
 __device__ __forceinline__ void quantize_row(const void *x, int64_t base, uint8_t *orow, int K,
                                              int tid) {
   const int l = tid & 7;
   for (int i = 4 * tid; i < K; i += 1024) {
     const f32x4 v = load4<F16>(x, base + i);
-    quantize4_store(v.x, v.y, v.z, v.w, orow + (i >> 5) * kQ8_1Bytes, l);
+    quantize4_row_store<SPLIT>(v.x, v.y, v.z, v.w, orow, K, i >> 5, l);
   }
 }
 

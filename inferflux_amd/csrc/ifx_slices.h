@@ -160,6 +160,18 @@ struct ALds {
   }
 };
 
+// Q8_1 activations in LDS in the split layout of ifx_q8_1.h (split_codes,
+// split_ds): per batch column `stride` bytes.
+struct ALdsS {
+  const uint8_t *p;
+  uint32_t stride;
+  uint32_t ds0;  // offset of the d | s words in a column: 80 K / 64
+};
+template <typename AS>
+inline constexpr bool kSplitA = false;
+template <>
+inline constexpr bool kSplitA<ALdsS> = true;
+
 // The weight bytes of wide slice s of R rows, loaded before their use.
 template <int R>
 struct Q4Wide {
@@ -192,13 +204,27 @@ __device__ __forceinline__ void q4k_wide_compute(const Q4Wide<R> &wt, const AS &
 #pragma unroll
   for (int c = 0; c < MC; ++c) {
     if (c == 0 || c < mvalid) {  // mvalid >= 1
-      const uint32_t ao = (b * 8 + 2 * w) * kQ8_1Bytes;
-      const uint32_t dsa = as.template get<uint32_t>(ao, c);
-      const uint32_t dsb = as.template get<uint32_t>(ao + kQ8_1Bytes, c);
-      xa0[c] = as.template get<i32x4>(ao + 4, c);
-      xa1[c] = as.template get<i32x4>(ao + 20, c);
-      xb0[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 4, c);
-      xb1[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 20, c);
+      uint32_t dsa, dsb;
+      if constexpr (kSplitA<AS>) {
+        // blocks 8b + 2w and + 1: one 80-byte slot, one 8-byte d | s pair
+        const uint8_t *col = as.p + c * as.stride;
+        const uint8_t *q = col + (b * 4 + w) * 80;
+        const u32x2 ds2 = ldg<u32x2>(col + as.ds0 + (b * 8 + 2 * w) * 4);
+        dsa = ds2.x;
+        dsb = ds2.y;
+        xa0[c] = ldg<i32x4>(q);
+        xa1[c] = ldg<i32x4>(q + 16);
+        xb0[c] = ldg<i32x4>(q + 32);
+        xb1[c] = ldg<i32x4>(q + 48);
+      } else {
+        const uint32_t ao = (b * 8 + 2 * w) * kQ8_1Bytes;
+        dsa = as.template get<uint32_t>(ao, c);
+        dsb = as.template get<uint32_t>(ao + kQ8_1Bytes, c);
+        xa0[c] = as.template get<i32x4>(ao + 4, c);
+        xa1[c] = as.template get<i32x4>(ao + 20, c);
+        xb0[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 4, c);
+        xb1[c] = as.template get<i32x4>(ao + kQ8_1Bytes + 20, c);
+      }
       da[c] = h2f(dsa & 0xFFFFu);
       db[c] = h2f(dsb & 0xFFFFu);
       sa[c] = h2f(dsa >> 16);
