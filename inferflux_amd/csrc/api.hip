@@ -270,7 +270,16 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
 // (grouped = true) for valid arguments; n_total = sum of the projections' N.
 enum class Route { F16Gemm, Gemv, Lds, Slot, Dq, Skinny, Mmvq, Mfma, PerProjection };
 Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
-  if (tiled(qt)) return M <= kMaxSlotM ? Route::Slot : Route::Dq;
+  if (tiled(qt)) {
+    // measured on MI355X (14B / 3B shapes, cold weights): the slot-packed
+    // GEMV (two 16-row slots above M = 8) up to M = 16, except wide Q4_K
+    // launches from M = 9 (14B gate+up M = 12: 25.6 us on the fp16-dequant
+    // GEMV against 29.5); the fp16-dequant GEMV above M = 16 (Q6_K down
+    // 5120 x 13824 M = 16: 19.0 us on the slot GEMV, 20.9 on fp16-dequant)
+    if (M <= kMaxSlotM) return Route::Slot;
+    if (M <= 2 * kMaxSlotM && (qt == IFX_TYPE_Q6_K_T || n_total < 8192)) return Route::Slot;
+    return Route::Dq;
+  }
   if (!grouped && !gemv_only(qt) && M > kMaxSkinnyM && use_f16_gemm(qt, M, K)) return Route::F16Gemm;
   if (gemv_only(qt) || row_split(qt) || M <= max_gemv_m() || (M > kMaxSkinnyM && K % 256 != 0))
     return Route::Gemv;
@@ -576,7 +585,7 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   // blocks of outputs; other shapes take the grouped GEMV + SiLU producer
   const int max_m = tiled(quant_type) ? 0
                     : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
-  const bool slot = M > max_m && ifx::gemv_slot_fits(quant_type, M, K);
+  const bool slot = M > max_m && M <= kMaxSlotM && ifx::gemv_slot_fits(quant_type, M, K);
   if (M < 1 || (M > max_m && !slot) || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)

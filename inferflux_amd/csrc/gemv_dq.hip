@@ -372,15 +372,29 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
       if (8 * (i >> 2) + 4 * h + (i & 3) < M) st_dev(mine + 64 * i, yv[i]);
     wait_own_memory();
     if (!split_arrive_last(args.ws.cnt + bx, ks)) return;
+    // all slots, this workgroup's included, in split order; four slots'
+    // loads in flight at a time (rows past M were not stored and are unused)
     const float *slot0 = args.ws.part + static_cast<int64_t>(bx) * ks * kWaves * kSlot + wave * kSlot + lane;
+    float t[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (8 * (i >> 2) + 4 * h + (i & 3) >= M) continue;
-      float t = 0.0f;
-      for (int sp = 0; sp < ks; ++sp)
-        t += sp == static_cast<int>(blockIdx.y) ? yv[i] : ld_dev(slot0 + sp * kWaves * kSlot + 64 * i);
-      yv[i] = t;
+    for (int i = 0; i < 16; ++i) t[i] = 0.0f;
+    for (int sp0 = 0; sp0 < ks; sp0 += 4) {
+      float v[4][16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float *src = slot0 + min(sp0 + j, ks - 1) * kWaves * kSlot;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[j][i] = ld_dev(src + 64 * i);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (sp0 + j < ks) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) t[i] += v[j][i];
+        }
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) yv[i] = t[i];
     split_reset(args.ws.cnt + bx);
   }
   if (n >= N) return;

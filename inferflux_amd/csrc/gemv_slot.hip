@@ -567,7 +567,8 @@ void slot_kw(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
 // at 2-3 waves per SIMD), so only M <= 8 is routed here.
 template <int QT, bool TL>
 void slot_q(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
-  slot_kw<QT, 8, TL>(args, blocks, f16, s);
+  if (TL && args.M > 8) slot_kw<QT, 16, TL>(args, blocks, f16, s);
+  else slot_kw<QT, 8, TL>(args, blocks, f16, s);
 }
 
 }  // namespace
@@ -605,8 +606,9 @@ void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
 }
 
 bool gemv_slot_fits(int qtype, int M, int K) {
-  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ4_KT || qtype == kTypeQ6_KT) &&
-         M >= 1 && M <= 8 && K % 256 == 0 && K > 0;
+  const bool t = qtype == kTypeQ4_KT || qtype == kTypeQ6_KT;
+  return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || t) && M >= 1 && M <= (t ? 16 : 8) &&
+         K % 256 == 0 && K > 0;
 }
 
 // count projections (1..3) share A; geometry checked by the caller
@@ -614,14 +616,14 @@ bool gemv_slot_fits(int qtype, int M, int K) {
 // Workspace bytes of the ordered split (0: the launch does not split):
 // counters (256-byte aligned) then one 1 KB slot per (row group, split).
 int64_t gemv_slot_workspace_bytes(int count, const int *N, bool f16, int M, int K) {
-  (void)M;
   int blocks = 0;
   for (int i = 0; i < count; ++i) blocks += (N[i] + 31) / 32;
   int kw = 8, ks = 1;
   choose_slot_work(blocks, K >> 8, f16, kw, ks);
   if (ks <= 1 || f16) return 0;
+  const int nm = M > 8 ? 8 : 4;  // fp32 sums per lane (MP / 2)
   return (static_cast<int64_t>(blocks) * 4 + 255) / 256 * 256 +
-         static_cast<int64_t>(blocks) * ks * 64 * 4 * 4;
+         static_cast<int64_t>(blocks) * ks * 64 * nm * 4;
 }
 
 // ws: the ordered-split workspace (gemv_slot_workspace_bytes, counters
@@ -661,7 +663,7 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
 hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
                                    void *H, bool f16h, void *Q, int M, int N, int K,
                                    hipStream_t stream) {
-  if (!gemv_slot_fits(qtype, M, K) || N % 32 != 0) return hipErrorInvalidValue;
+  if (!gemv_slot_fits(qtype, M, K) || M > 8 || N % 32 != 0) return hipErrorInvalidValue;
   SlotArgs args{};
   args.seg[0] = SlotSeg{static_cast<const uint8_t *>(Wg), nullptr, nullptr, N, 0};
   args.seg[1] = SlotSeg{static_cast<const uint8_t *>(Wu), nullptr, nullptr, N, 0};

@@ -99,8 +99,9 @@ def test_decode_ffn_routing():
 
 
 def test_tiled_routing():
-    """Tiled weights: the slot-packed int8 MFMA GEMV for M <= 8 and the
-    fp16-dequant MFMA GEMV for 9 <= M <= 32, both with the layout flag; the
+    """Tiled weights: the slot-packed int8 MFMA GEMV for M <= 16 (wide Q4_K
+    launches: M <= 8) and the fp16-dequant MFMA GEMV above, both with the
+    layout flag; the
     gate/up/SiLU entry on the slot kernel from M = 1; M > 32 not handled."""
     from inferflux_amd import _lib, ops
     L = _lib.load()
@@ -109,6 +110,8 @@ def test_tiled_routing():
         assert rc == 0 and k == ["k_gemv_slot<12,8,8,0,0,0,1>"]
     rc, k = dry_dispatch("gemv", ops.Q6_K_T, 8, (2048,), 11008)  # few row groups: K split
     assert rc == 0 and k == ["k_fill_zero", "k_gemv_slot<14,8,4,0,1,0,1>"]
+    rc, k = dry_dispatch("grouped", ops.Q4_K_T, 16, (5120, 1024, 1024), 5120)
+    assert rc == 0 and k == ["k_fill_zero", "k_gemv_slot<12,16,4,0,1,0,1>"]
     rc, k = dry_dispatch("grouped", ops.Q4_K_T, 32, (5120, 1024, 1024), 5120)
     assert rc == 0 and k[-1] == "k_gemv_dq<12,0,1,1>"
     for M in (1, 4, 8):
@@ -117,7 +120,9 @@ def test_tiled_routing():
     assert dry_dispatch("gemv", ops.Q4_K_T, 33, (64,), 256)[0] == 2
     assert dry_dispatch("prefill", ops.Q4_K_T, 512, (64,), 256)[0] == 2
     assert L.ifx_kernel_family(ops.Q4_K_T, 8, 64, 256) == 2
-    assert L.ifx_kernel_family(ops.Q6_K_T, 9, 64, 256) == 5
+    assert L.ifx_kernel_family(ops.Q6_K_T, 9, 64, 256) == 2  # two 16-row slots
+    assert L.ifx_kernel_family(ops.Q4_K_T, 16, 16384, 256) == 5  # wide Q4_K from M = 9
+    assert L.ifx_kernel_family(ops.Q6_K_T, 17, 64, 256) == 5
     assert L.ifx_kernel_family(ops.Q6_K_T, 33, 64, 256) == 0
     assert L.ifx_tiled_bytes(ops.Q4_K, 33, 512) == 64 * 2 * 144
     assert L.ifx_tiled_bytes(ops.Q8_0, 32, 512) == 0

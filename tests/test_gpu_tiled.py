@@ -91,7 +91,7 @@ def test_gemv_tiled(orc, dev, qtype, M, N, K):
     ye = orc.gemv_exact(qtype, w, a, M, N, K)
     with ops.launch_log() as lg:
         y = down(ops.qgemv(tt, WT, A, M, N, K))
-    fam = "k_gemv_slot<" if M <= 8 else "k_gemv_dq<"
+    fam = "k_gemv_slot<" if M <= 16 else "k_gemv_dq<"  # N < 8192 here
     assert len(lg.kernels) >= 1 and lg.kernels[-1].startswith(fam) and lg.kernels[-1].endswith(",1>")
     check_rows(y, ye)
     # the raw layout on the same kernel (same arguments but the layout flag)
