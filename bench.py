@@ -495,6 +495,16 @@ def main():
             gb = gemv_bytes(ops, qt, M, [N], K) / us / 1e3
             c1[f"M{M}"] = {"us": round(us, 3), "GBs": round(gb, 1),
                            "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
+        # the same weights as a tiled copy (ifx_repack_tiled) at M = 8; GB/s
+        # over the raw layout's algorithmic bytes
+        treps = [ops.repack_tiled(qt, w_, N, K)[1] for w_ in reps]
+        A = ops.quantize_q8_1(torch.from_numpy(synth.activations(8, K, seed=0)).to(dev))
+        Y = torch.empty((8, N), dtype=torch.float32, device=dev)
+        us = time_loop(lambda i: ops.qgemv(ops.Q4_K_T, treps[i % len(treps)], A, 8, N, K, out=Y),
+                       max(args.steps, 200), args.warmup)
+        gb = gemv_bytes(ops, qt, 8, [N], K) / us / 1e3
+        c1["M8_tiled"] = {"us": round(us, 3), "GBs": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
+        del treps
         extras["config1_q4k_11008x2048"] = c1
         del reps, w
         torch.cuda.empty_cache()
