@@ -130,8 +130,9 @@ class FusedQuantGemm {
 
   // fused_quant_gemm.h:281-307: silu(gate . a) * (up . a) in one launch, fp16
   // out; the WithEpilogue variant also writes the Q8_1 blocks of the result
-  // (act_q8_1_out, may be null) for the down projection.  M <= 2 and N %
-  // 32 == 0 (else false: grouped GEMV + SiluMulQuantizeQ8_1).
+  // (act_q8_1_out, may be null) for the down projection.  N % 32 == 0 and
+  // M <= 2, or 3 <= M <= 8 for Q4_K / Q6_K with K % 256 == 0 (else false:
+  // grouped GEMV + SiluMulQuantizeQ8_1).
   static bool FusedGateUpSiluGemvQ8_1(const QuantizedWeightInfo &gate_raw,
                                       const QuantizedWeightInfo &up_raw, const void *act_q8_1,
                                       uint16_t *output, int M, int N, int K, hipStream_t stream);
