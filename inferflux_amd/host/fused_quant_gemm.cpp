@@ -218,7 +218,8 @@ int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
 // fused_quant_gemm.cu:830-923):
 //  * includes_rmsnorm: the RMSNorm + Q8_1 producer fused into the GEMV
 //    (ifx_qgemv_grouped_rmsnorm) is Q4_K only, M <= 2, with the batch's Q8_1
-//    rows in 64 KiB of LDS; larger batches take the producer + GEMV;
+//    rows (80 K / 64 + K / 8 bytes each) in 64 KiB of LDS; larger batches
+//    take the producer + GEMV;
 //  * K: the Q8_1 activations [M][K/32] are addressed with 32-bit offsets.
 int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,
                                               const FusedDispatchGeometry &geometry) {
@@ -228,7 +229,10 @@ int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,
   if (geometry.includes_rmsnorm) {
     if (quant_type != static_cast<int>(TensorType::Q4_K)) return 0;
     t = std::min<int64_t>(t, 2);
-    if (a_row > 0) t = std::min<int64_t>(t, 65536 / a_row);
+    // the LDS row of the fused producer: codes in 80-byte slots per 64
+    // values, then 4 bytes of d | s per block of 32
+    const int64_t lds_row = geometry.K > 0 ? static_cast<int64_t>(geometry.K / 64) * 80 + geometry.K / 8 : 0;
+    if (lds_row > 0) t = std::min<int64_t>(t, 65536 / lds_row);
   }
   if (a_row > 0) t = std::min<int64_t>(t, ((int64_t{1} << 32) - 1) / a_row);
   return static_cast<int>(t);

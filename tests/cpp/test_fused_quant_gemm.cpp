@@ -165,13 +165,13 @@ void TestPolicy() {
 
   // thresholds: no crossover to a fallback on gfx950
   EXPECT(FusedQuantGemm::GetAdaptiveThreshold(Q4_K) == FusedQuantGemm::kMaxFusedM);
-  {  // the geometry narrows it: fused RMSNorm (Q4_K, M <= 2, Q8_1 rows in 64 KiB
-     // of LDS) and 32-bit activation offsets
+  {  // the geometry narrows it: fused RMSNorm (Q4_K, M <= 2, activation rows in
+     // 64 KiB of LDS) and 32-bit activation offsets
     FusedDispatchGeometry g{1, 2048, 2048, 1, false, true};
     EXPECT(FusedQuantGemm::GetGeometryAwareThreshold(Q4_K, g) == 2);
     EXPECT(FusedQuantGemm::GetGeometryAwareThreshold(Q6_K, g) == 0);
     EXPECT(!FusedQuantGemm::ShouldUseFusedPath(Q4_K, FusedDispatchGeometry{3, 2048, 2048, 1, false, true}));
-    g.K = 40960;  // 1280 blocks of 36 bytes: one row in 64 KiB
+    g.K = 40960;  // an LDS row of 56320 bytes: one row in 64 KiB
     EXPECT(FusedQuantGemm::GetGeometryAwareThreshold(Q4_K, g) == 1);
     FusedDispatchGeometry h{1, 64, 2048, 1, false, false};
     EXPECT(FusedQuantGemm::GetGeometryAwareThreshold(Q4_K, h) == 1864135);  // (2^32 - 1) / 2304
