@@ -758,8 +758,9 @@ def profile_kernels_run(args, dev):
     """Eager launches for rocprofv3 counter runs of the batch kernels:
     `steps` launches each of the config-5 prefill GEMMs on the fp16 kernel
     (and, where the shape uses one, with the activation workspace) and (a
-    quarter as many) on the int8 kernel, and of the config-4 14B
-    grouped gate+up and down launches at M = 32 (weights rotating over
+    quarter as many) on the int8 kernel, of the config-4 14B grouped
+    gate+up and down launches at M = 32, and of config 1 and the 3B down
+    projection at M = 8 on raw and on tiled rows (weights rotating over
     >= 512 MB of replicas), then 20 copies of exactly 64 MiB for counter
     calibration.  Prints one JSON line of event timings."""
     import torch
@@ -810,6 +811,25 @@ def profile_kernels_run(args, dev):
         out[f"decode14b_{launch}_m32_us"] = timed(
             lambda i: ops.qgemv_grouped(qt, reps[i % R], A, M, Ns, K, outs=Ys), args.steps)
         del reps, ws
+        torch.cuda.empty_cache()
+    # raw against tiled rows (ifx_repack_tiled) on the slot-packed GEMV: config 1
+    # and the 3B down projection at M = 8 (down: ordered K split on the tiled copy)
+    for key, qt, N, K in (("config1", ops.Q4_K, 11008, 2048), ("down3b", ops.Q6_K, 2048, 11008)):
+        M = 8
+        w = torch.from_numpy(synth.blocks(qt, N, K, seed=9)).to(dev)
+        R = max(2, -(-ROTATE_BYTES // w.numel()))
+        reps = [w] + [w.clone() for _ in range(R - 1)]
+        treps = [ops.repack_tiled(qt, x, N, K)[1] for x in reps]
+        A = ops.quantize_q8_1(torch.from_numpy(synth.activations(M, K, seed=9)).to(dev))
+        Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        nb = ops.qgemv_workspace_bytes(qt + 200, [N], M, K)
+        wsd = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev) if nb else None
+        out[f"{key}_m8_raw_us"] = timed(lambda i: ops.qgemv(qt, reps[i % R], A, M, N, K, out=Y),
+                                        args.steps)
+        out[f"{key}_m8_tiled_us"] = timed(
+            lambda i: ops.qgemv(qt + 200, treps[i % R], A, M, N, K, out=Y, workspace=wsd),
+            args.steps)
+        del reps, treps, w
         torch.cuda.empty_cache()
     lib = probe_lib()
     big = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
