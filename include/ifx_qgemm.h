@@ -45,6 +45,7 @@ enum ifx_quant_type {
    * groups of 32, one tile per group and super-block holding the group's
    * super-blocks in the byte order of the MFMA batch kernels' loads.
    * ifx_qgemv / ifx_qgemv_grouped / ifx_qgemv_gate_up_silu at M <= 32. */
+  IFX_TYPE_Q8_0_T = 208, /* 8704-byte tiles per 256 values: codes in 16-byte pieces, then d */
   IFX_TYPE_Q4_K_T = 212, /* 4608-byte tiles: 32 headers, then qs in 16-byte pieces */
   IFX_TYPE_Q6_K_T = 214  /* 6720-byte tiles: ql, qh pieces, 32 x scales, 32 x d */
 };
@@ -321,12 +322,13 @@ int64_t ifx_repacked_bytes(int quant_type, int64_t n_rows, int K);
  * fused_quant_gemm.h:213-234, fused_quant_gemm.cu:573-596, 1966-2032). */
 int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K, void *stream);
 
-/* Bytes of the tiled copy of n_rows x K Q4_K or Q6_K weights: whole groups
- * of 32 rows (0 for another type or K % 256 != 0). */
+/* Bytes of the tiled copy of n_rows x K Q4_K, Q6_K or Q8_0 weights: whole
+ * groups of 32 rows (0 for another type or K % 256 != 0). */
 int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K);
 
-/* Load-time repack of raw GGUF Q4_K / Q6_K rows into the tiled layout
- * IFX_TYPE_Q4_K_T / IFX_TYPE_Q6_K_T (W_out: ifx_tiled_bytes, caller owned,
+/* Load-time repack of raw GGUF Q4_K / Q6_K / Q8_0 rows (Q8_0: K % 256 == 0)
+ * into the tiled layout IFX_TYPE_Q4_K_T / IFX_TYPE_Q6_K_T / IFX_TYPE_Q8_0_T
+ * (W_out: ifx_tiled_bytes, caller owned,
  * 16-byte aligned; the rows of a last partial group are written as zeros).
  * The batch kernels (slot-packed int8 MFMA at M <= 8, fp16-dequant MFMA at
  * 9 <= M <= 32) give each lane one weight row, so on raw rows every load

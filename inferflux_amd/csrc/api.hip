@@ -227,7 +227,7 @@ bool gemv_only(int t) { return t == IFX_TYPE_Q5_K || t == IFX_TYPE_Q8_K; }
 bool row_split(int t) { return t == IFX_TYPE_Q8_0_R || t == IFX_TYPE_Q6_K_R; }
 constexpr int kMaxRowSplitM = 2;
 // the tiled layouts of ifx_repack_tiled: the MFMA batch GEMVs, M <= 32
-bool tiled(int t) { return t == IFX_TYPE_Q4_K_T || t == IFX_TYPE_Q6_K_T; }
+bool tiled(int t) { return t == IFX_TYPE_Q4_K_T || t == IFX_TYPE_Q6_K_T || t == IFX_TYPE_Q8_0_T; }
 constexpr int kMaxTiledM = 32;
 constexpr int kMaxSlotM = 8;
 // a layout of this library, served by some entry points only
@@ -408,6 +408,7 @@ int ifx_block_bytes(int quant_type) {
   case IFX_TYPE_Q8_0_R: return ifx::kQ8_0Bytes;
   case IFX_TYPE_Q6_K_R: case IFX_TYPE_Q6_K_T: return ifx::kQ6KBytes;
   case IFX_TYPE_Q4_K_T: return ifx::kQ4KBytes;
+  case IFX_TYPE_Q8_0_T: return 8 * ifx::kQ8_0Bytes;  // the 256 values of a tile row
   default: return 0;
   }
 }
@@ -415,7 +416,7 @@ int ifx_block_bytes(int quant_type) {
 int ifx_block_elems(int quant_type) {
   switch (quant_type) {
   case IFX_TYPE_Q4_K: case IFX_TYPE_Q5_K: case IFX_TYPE_Q6_K: case IFX_TYPE_Q8_K:
-  case IFX_TYPE_Q6_K_R: case IFX_TYPE_Q4_K_T: case IFX_TYPE_Q6_K_T: return 256;
+  case IFX_TYPE_Q6_K_R: case IFX_TYPE_Q4_K_T: case IFX_TYPE_Q6_K_T: case IFX_TYPE_Q8_0_T: return 256;
   case IFX_TYPE_Q8_0: case IFX_TYPE_Q8_1: case IFX_TYPE_Q8_0_R: return 32;
   default: return 0;
   }
@@ -769,7 +770,8 @@ int ifx_repack(int quant_type, const void *W, void *W_out, int64_t n_rows, int K
 
 int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K) {
   const int tt = quant_type == IFX_TYPE_Q4_K ? IFX_TYPE_Q4_K_T
-                 : quant_type == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_T : 0;
+                 : quant_type == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_T
+                 : quant_type == IFX_TYPE_Q8_0 ? IFX_TYPE_Q8_0_T : 0;
   if (!tt || n_rows < 0 || K <= 0 || K % 256) return 0;
   return (n_rows + 31) / 32 * 32 * static_cast<int64_t>(ifx::row_bytes(tt, K));
 }
@@ -777,7 +779,8 @@ int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K) {
 int ifx_repack_tiled(int quant_type, const void *W, void *W_out, int64_t n_rows, int K,
                      void *stream) {
   if (!W || !W_out) return IFX_NULL_POINTER;
-  if (quant_type != IFX_TYPE_Q4_K && quant_type != IFX_TYPE_Q6_K) return IFX_UNSUPPORTED_TYPE;
+  if (quant_type != IFX_TYPE_Q4_K && quant_type != IFX_TYPE_Q6_K && quant_type != IFX_TYPE_Q8_0)
+    return IFX_UNSUPPORTED_TYPE;
   if (n_rows < 0 || K <= 0 || K % 256) return IFX_BAD_GEOMETRY;
   if (ifx_tiled_bytes(quant_type, n_rows, K) >= (int64_t{1} << 32))
     return IFX_BAD_GEOMETRY;  // the GEMVs address tiles with 32-bit offsets

@@ -212,7 +212,8 @@ template <int QT>
 __global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t *__restrict__ W,
                                                       uint8_t *__restrict__ out, int64_t n_rows,
                                                       int K) {
-  constexpr int kBytes = QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes;
+  // bytes of a row's 256 values: one super-block, or eight Q8_0 blocks
+  constexpr int kBytes = QT == kTypeQ4_K ? kQ4KBytes : QT == kTypeQ8_0 ? 8 * kQ8_0Bytes : kQ6KBytes;
   constexpr int kTile = kTileRows * kBytes;
   const int nsb = K / 256;
   const int64_t groups = (n_rows + kTileRows - 1) / kTileRows;
@@ -230,7 +231,14 @@ __global__ __launch_bounds__(256) void k_repack_tiled(const uint8_t *__restrict_
   } else {
     for (int i = 0; i < kBytes; ++i) src[i] = 0;
   }
-  if constexpr (QT == kTypeQ4_K) {
+  if constexpr (QT == kTypeQ8_0) {
+    for (int j = 0; j < 8; ++j) {
+      tile[8192 + 16 * c + 2 * j] = src[34 * j];
+      tile[8192 + 16 * c + 2 * j + 1] = src[34 * j + 1];
+      for (int h = 0; h < 2; ++h)
+        for (int i = 0; i < 16; ++i) tile[1024 * j + 512 * h + 16 * c + i] = src[34 * j + 2 + 16 * h + i];
+    }
+  } else if constexpr (QT == kTypeQ4_K) {
     for (int i = 0; i < 16; ++i) tile[16 * c + i] = src[i];
     for (int p = 0; p < 4; ++p)
       for (int h = 0; h < 2; ++h)
@@ -258,6 +266,7 @@ hipError_t launch_repack_tiled(int qtype, const void *W, void *out, int64_t n_ro
   uint8_t *o = static_cast<uint8_t *>(out);
   if (qtype == kTypeQ4_K) IFX_LAUNCH(k_repack_tiled, (kTypeQ4_K), grid, dim3(256), 0, stream, w, o, n_rows, K);
   else if (qtype == kTypeQ6_K) IFX_LAUNCH(k_repack_tiled, (kTypeQ6_K), grid, dim3(256), 0, stream, w, o, n_rows, K);
+  else if (qtype == kTypeQ8_0) IFX_LAUNCH(k_repack_tiled, (kTypeQ8_0), grid, dim3(256), 0, stream, w, o, n_rows, K);
   else return hipErrorInvalidValue;
   return last_error();
 }

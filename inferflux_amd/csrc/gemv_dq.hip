@@ -138,7 +138,15 @@ struct RawW<kTypeQ8_0> {  // codes 16h .. 16h+15 and d of the 8 blocks
 template <int QT, bool TL = false>
 __device__ __forceinline__ void fetch_w(RawW<QT> &r, rsrc_t Wr, uint32_t row_off, int sb, int h,
                                         int c = 0) {
-  if constexpr (TL && QT == kTypeQ4_K) {
+  if constexpr (TL && QT == kTypeQ8_0) {
+    const uint32_t o = row_off + sb * (kTileRows * 8 * kQ8_0Bytes) + 16 * c;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) r.q[b] = wload<u32x4>(Wr, o + 1024 * b + 512 * h, 0);
+    const u32x4 dd = wload<u32x4>(Wr, o + 8192, 0);
+    const uint32_t dw[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+    for (int b = 0; b < 8; ++b) r.d[b] = (dw[b >> 1] >> (16 * (b & 1))) & 0xFFFFu;
+  } else if constexpr (TL && QT == kTypeQ4_K) {
     const uint32_t o = row_off + sb * (kTileRows * kQ4KBytes) + 16 * c;
     r.hdr = wload<u32x4>(Wr, o, 0);
 #pragma unroll
@@ -492,7 +500,7 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
 // fp16 outputs are not split: their K must fit one activation stage.
 bool gemv_dq_fits(int qtype, int M, int K) {
   return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ8_0 || qtype == kTypeQ4_KT ||
-          qtype == kTypeQ6_KT) && M >= 1 &&
+          qtype == kTypeQ6_KT || qtype == kTypeQ8_0T) && M >= 1 &&
          M <= kMaxM && K % 256 == 0;
 }
 
@@ -542,6 +550,7 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
   case kTypeQ8_0: return launch_qt<kTypeQ8_0, false>(args, f16, splits_req, stream);
   case kTypeQ4_KT: return launch_qt<kTypeQ4_K, true>(args, f16, splits_req, stream);
   case kTypeQ6_KT: return launch_qt<kTypeQ6_K, true>(args, f16, splits_req, stream);
+  case kTypeQ8_0T: return launch_qt<kTypeQ8_0, true>(args, f16, splits_req, stream);
   default: return hipErrorInvalidValue;
   }
 }

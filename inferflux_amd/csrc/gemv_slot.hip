@@ -77,7 +77,7 @@ namespace {
 template <int QT, int MP>
 struct SlotGeo {
   static constexpr int kSlots = 32 / MP;
-  static constexpr int kTpc = (QT == kTypeQ4_K) ? kSlots : kSlots / 2;
+  static constexpr int kTpc = (QT == kTypeQ6_K) ? kSlots / 2 : kSlots;
   static constexpr int kCh = 8 / kTpc;
   static constexpr int kNm = MP / 2;  // batch rows per lane
 };
@@ -88,6 +88,11 @@ template <>
 struct WSb<kTypeQ4_K> {
   u32x4 hdr;   // d | dmin, scales[12]
   u32x4 q[4];  // qs[32p + 16h .. +16]: sub-blocks 2p (low), 2p+1 (high)
+};
+template <>
+struct WSb<kTypeQ8_0> {  // tiled rows only
+  u32x4 q[8];  // codes 16h .. 16h+15 of blocks 0..7
+  u32x4 d;     // the eight blocks' fp16 d
 };
 template <>
 struct WSb<kTypeQ6_K> {
@@ -122,7 +127,12 @@ __device__ __forceinline__ void wave_sync() {
 template <int QT, bool TL = false>
 __device__ __forceinline__ void load_w(WSb<QT> &w, rsrc_t Wr, uint32_t voff, uint32_t sb_off,
                                        int h) {
-  if constexpr (TL && QT == kTypeQ4_K) {
+  static_assert(TL || QT != kTypeQ8_0, "Q8_0 runs on tiled rows only");
+  if constexpr (QT == kTypeQ8_0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w.q[j] = wload<u32x4>(Wr, voff + 1024 * j + 512 * h, sb_off);
+    w.d = wload<u32x4>(Wr, voff + 8192, sb_off);
+  } else if constexpr (TL && QT == kTypeQ4_K) {
     w.hdr = wload<u32x4>(Wr, voff, sb_off);
 #pragma unroll
     for (int p = 0; p < 4; ++p) w.q[p] = wload<u32x4>(Wr, voff + 512 + 1024 * p + 512 * h, sb_off);
@@ -166,7 +176,9 @@ __device__ __forceinline__ i32x16 mfma_acc(i32x4 a, i32x4 b, i32x16 c) {
 // Weight operand of block j (K half h of this lane) as int8 codes.
 template <int QT>
 __device__ __forceinline__ i32x4 w_operand(const WSb<QT> &w, int j) {
-  if constexpr (QT == kTypeQ4_K) {
+  if constexpr (QT == kTypeQ8_0) {
+    return __builtin_bit_cast(i32x4, w.q[j]);
+  } else if constexpr (QT == kTypeQ4_K) {
     const u32x4 q = w.q[j >> 1];
     const int sh = 4 * (j & 1);
     return i32x4{static_cast<int>((q.x >> sh) & 0x0F0F0F0Fu), static_cast<int>((q.y >> sh) & 0x0F0F0F0Fu),
@@ -225,7 +237,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
   const int c32 = lane & 31, h = lane >> 5;
   const int n0 = SW ? bx * 32 : (bx - sg.blk_begin) * 32;
   const int nsb = K >> 8;
-  constexpr int kSbBytes = (QT == kTypeQ4_K) ? kQ4KBytes : kQ6KBytes;
+  constexpr int kSbBytes = (QT == kTypeQ4_K) ? kQ4KBytes : (QT == kTypeQ8_0) ? 8 * kQ8_0Bytes : kQ6KBytes;
   const uint32_t w_row = static_cast<uint32_t>(nsb) * kSbBytes;
   const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
   // tiled: whole 32-row groups; tile (group, super-block) at (group * nsb + sb) * kTile
@@ -337,6 +349,28 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       const float d = h2f(wc.hdr.x & 0xFFFFu), dmin = h2f(wc.hdr.x >> 16);
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) acc[mi] += d * part[mi] - dmin * pm[mi];
+    } else if constexpr (QT == kTypeQ8_0) {
+      // per block: the exact integer dot times d_w * d_a (mmvq.cuh:886-889)
+      const uint32_t dw4[4] = {wc.d.x, wc.d.y, wc.d.z, wc.d.w};
+#pragma unroll
+      for (int c = 0; c < G::kCh; ++c) {
+        i32x16 C = {0};
+#pragma unroll
+        for (int t = 0; t < G::kTpc; ++t) {
+          const int j = c * G::kTpc + t;
+          const i32x4 a = ac.c[c] & static_cast<int>(amask[t]);
+          C = mfma_acc(a, w_operand<QT>(wc, j), C);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int s = (8 * (i >> 2)) / MP;
+          const int j = c * G::kTpc + s;
+          const int mi = ((8 * (i >> 2)) % MP) / 2 + (i & 3);
+          const float dw = h2f((dw4[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+          const float da = dl[j * MP + 2 * (mi & ~3) + 4 * h + (mi & 3)];
+          acc[mi] += static_cast<float>(C[i]) * (dw * da);
+        }
+      }
     } else {
       const uint32_t scw[4] = {wc.sc.x, wc.sc.y, wc.sc.z, wc.sc.w};
 #pragma unroll
@@ -606,7 +640,7 @@ void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
 }
 
 bool gemv_slot_fits(int qtype, int M, int K) {
-  const bool t = qtype == kTypeQ4_KT || qtype == kTypeQ6_KT;
+  const bool t = qtype == kTypeQ4_KT || qtype == kTypeQ6_KT || qtype == kTypeQ8_0T;
   return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || t) && M >= 1 && M <= (t ? 16 : 8) &&
          K % 256 == 0 && K > 0;
 }
@@ -652,6 +686,7 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
   case kTypeQ4_K: slot_q<kTypeQ4_K, false>(args, blocks, f16, stream); break;
   case kTypeQ6_K: slot_q<kTypeQ6_K, false>(args, blocks, f16, stream); break;
   case kTypeQ4_KT: slot_q<kTypeQ4_K, true>(args, blocks, f16, stream); break;
+  case kTypeQ8_0T: slot_q<kTypeQ8_0, true>(args, blocks, f16, stream); break;
   default: slot_q<kTypeQ6_K, true>(args, blocks, f16, stream); break;
   }
   return last_error();
@@ -678,6 +713,7 @@ hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, co
   case kTypeQ4_K: slot_swiglu_q<kTypeQ4_K, false>(args, f16h, stream); break;
   case kTypeQ6_K: slot_swiglu_q<kTypeQ6_K, false>(args, f16h, stream); break;
   case kTypeQ4_KT: slot_swiglu_q<kTypeQ4_K, true>(args, f16h, stream); break;
+  case kTypeQ8_0T: slot_swiglu_q<kTypeQ8_0, true>(args, f16h, stream); break;
   default: slot_swiglu_q<kTypeQ6_K, true>(args, f16h, stream); break;
   }
   return last_error();

@@ -83,6 +83,9 @@ constexpr int kTypeQ6_KR = 114;
 //   Q6_K_T (6720 B): 1024 i + 512 h + 16 c: ql bytes 32 i + 16 h .. +15 (i = 0..3)
 //                    4096 + 1024 g + 512 h + 16 c: qh bytes 32 g + 16 h .. +15 (g = 0, 1)
 //                    6144 + 16 c: scales[16];  6656 + 2 c: d
+//   Q8_0_T (8704 B, per 256 values): 1024 j + 512 h + 16 c: codes 16 h .. +15
+//                    of block j (j = 0..7);  8192 + 16 c + 2 j: d of block j
+constexpr int kTypeQ8_0T = 208;
 constexpr int kTypeQ4_KT = 212;
 constexpr int kTypeQ6_KT = 214;
 constexpr int kTileRows = 32;

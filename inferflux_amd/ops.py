@@ -13,11 +13,11 @@ from . import _lib
 
 Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 8, 9, 12, 13, 14, 15
 Q8_0_R, Q6_K_R = 108, 114  # row-split layouts written by repack()
-Q4_K_T, Q6_K_T = 212, 214  # tiled layouts written by repack_tiled()
+Q8_0_T, Q4_K_T, Q6_K_T = 208, 212, 214  # tiled layouts written by repack_tiled()
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_1: 36, Q8_K: 292}
 BLOCK_ELEMS = {Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_1: 32, Q8_K: 256}
 TYPE_NAMES = {Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0", Q8_1: "Q8_1", Q8_K: "Q8_K",
-              108: "Q8_0_R", 114: "Q6_K_R", 212: "Q4_K_T", 214: "Q6_K_T"}
+              108: "Q8_0_R", 114: "Q6_K_R", 208: "Q8_0_T", 212: "Q4_K_T", 214: "Q6_K_T"}
 
 STORE, ACCUM, BIAS = 0, 1, 2
 OUT_F32, OUT_F16 = 0, 1
@@ -60,8 +60,9 @@ def _dev(t, name):
 def weight_bytes(qtype, n_rows, K):
     if qtype in (Q8_0_R, Q6_K_R):
         return n_rows * _row_split_bytes(qtype, K)
-    if qtype in (Q4_K_T, Q6_K_T):  # whole groups of 32 rows
-        return (n_rows + 31) // 32 * 32 * (K // 256) * BLOCK_BYTES[qtype - 200]
+    if qtype in (Q8_0_T, Q4_K_T, Q6_K_T):  # whole groups of 32 rows
+        raw = qtype - 200
+        return (n_rows + 31) // 32 * 32 * (K // BLOCK_ELEMS[raw]) * BLOCK_BYTES[raw]
     return n_rows * (K // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
 
 
@@ -123,7 +124,7 @@ def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, b
     od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
     if out.dtype not in (torch.float16, torch.float32):
         raise TypeError("out must be float32 or float16")
-    if (qtype in BLOCK_BYTES or qtype in (Q8_0_R, Q6_K_R, Q4_K_T, Q6_K_T)) and \
+    if (qtype in BLOCK_BYTES or qtype in (Q8_0_R, Q6_K_R, Q8_0_T, Q4_K_T, Q6_K_T)) and \
             W.numel() < weight_bytes(qtype, N, K):
         raise ValueError("W is smaller than N x K blocks")
     if A.numel() < M * (K // 32) * 36:
@@ -394,9 +395,9 @@ def repack(qtype, W, n_rows, K, out=None, stream=None):
 
 
 def repack_tiled(qtype, W, n_rows, K, out=None, stream=None):
-    """Tiled copy of raw Q4_K / Q6_K rows (ifx_repack_tiled): returns
+    """Tiled copy of raw Q4_K / Q6_K / Q8_0 rows (ifx_repack_tiled): returns
     (tiled type, device tensor).  For the MFMA batch GEMVs, M <= 32."""
-    tt = {Q4_K: Q4_K_T, Q6_K: Q6_K_T}[qtype]
+    tt = {Q4_K: Q4_K_T, Q6_K: Q6_K_T, Q8_0: Q8_0_T}[qtype]
     nbytes = int(_lib.load().ifx_tiled_bytes(qtype, n_rows, K))
     if out is None:
         out = torch.empty(nbytes, dtype=torch.uint8, device=W.device)

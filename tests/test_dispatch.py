@@ -125,4 +125,9 @@ def test_tiled_routing():
     assert L.ifx_kernel_family(ops.Q6_K_T, 17, 64, 256) == 5
     assert L.ifx_kernel_family(ops.Q6_K_T, 33, 64, 256) == 0
     assert L.ifx_tiled_bytes(ops.Q4_K, 33, 512) == 64 * 2 * 144
-    assert L.ifx_tiled_bytes(ops.Q8_0, 32, 512) == 0
+    assert L.ifx_tiled_bytes(ops.Q8_0, 33, 512) == 64 * 2 * 272
+    assert L.ifx_tiled_bytes(ops.Q5_K, 32, 512) == 0
+    rc, k = dry_dispatch("gemv", ops.Q8_0_T, 8, (151936,), 2048)
+    assert rc == 0 and k == ["k_gemv_slot<8,8,1,0,0,0,1>"]
+    rc, k = dry_dispatch("gemv", ops.Q8_0_T, 32, (151936,), 2048)
+    assert rc == 0 and k[-1] == "k_gemv_dq<8,0,1,1>"

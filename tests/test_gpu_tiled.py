@@ -10,8 +10,8 @@ from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, up
 
 pytestmark = pytest.mark.gpu
 
-Q4_K, Q6_K = 12, 14
-Q4_K_T, Q6_K_T = 212, 214
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0_T, Q4_K_T, Q6_K_T = 208, 212, 214
 
 
 @pytest.fixture(scope="module")
@@ -26,13 +26,18 @@ def tile_rows(qtype, w, N, K):
     """numpy restatement of the tiled layouts (include/ifx_qgemm.h): per
     group of 32 rows and super-block, the rows' 16-byte pieces in lane
     order (piece j of row c at 512 j + 16 c for the K-half-major pieces)."""
-    nb = 144 if qtype == Q4_K else 210
+    nb = {Q4_K: 144, Q6_K: 210, Q8_0: 272}[qtype]  # bytes per row and 256 values
     nsb = K // 256
     G = (N + 31) // 32
     b = np.zeros((G * 32, nsb, nb), np.uint8)
     b[:N] = w.reshape(N, nsb, nb)
     b = b.reshape(G, 32, nsb, nb).transpose(0, 2, 1, 3)  # [group][sb][row][bytes]
-    if qtype == Q4_K:
+    if qtype == Q8_0:
+        blk = b.reshape(G, nsb, 32, 8, 34)
+        codes = blk[..., 2:].reshape(G, nsb, 32, 8, 2, 16).transpose(0, 1, 3, 4, 2, 5)  # [j][h][row]
+        d = blk[..., :2].reshape(G, nsb, 32 * 16)
+        tile = np.concatenate([codes.reshape(G, nsb, 8192), d], axis=2)
+    elif qtype == Q4_K:
         hdr = b[:, :, :, :16].reshape(G, nsb, 512)
         qs = b[:, :, :, 16:].reshape(G, nsb, 32, 8, 16).transpose(0, 1, 3, 2, 4)  # [p*2+h][row]
         tile = np.concatenate([hdr, qs.reshape(G, nsb, 4096)], axis=2)
@@ -62,7 +67,7 @@ def atomic(name):
 
 
 @pytest.mark.parametrize("qtype,N,K", [(Q4_K, 64, 512), (Q4_K, 100, 2048), (Q6_K, 33, 256),
-                                       (Q6_K, 2048, 1024)])
+                                       (Q6_K, 2048, 1024), (Q8_0, 70, 512)])
 def test_tiled_layout(dev, qtype, N, K):
     from inferflux_amd import ops, synth
     note(f"tiled layout type={qtype} N={N} K={K}")
@@ -77,6 +82,7 @@ def test_tiled_layout(dev, qtype, N, K):
 CASES = [(Q4_K, M, 1000, 2048) for M in (1, 2, 3, 5, 8, 9, 16, 17, 32)]
 CASES += [(Q6_K, M, 1000, 2048) for M in (1, 4, 8, 12, 32)]
 CASES += [(Q4_K, 8, 100, 5120), (Q6_K, 5, 77, 11008), (Q6_K, 32, 2048, 5120), (Q4_K, 24, 31, 256)]
+CASES += [(Q8_0, M, 1000, 2048) for M in (1, 4, 8, 12, 24, 32)] + [(Q8_0, 8, 40, 11008)]
 
 
 @pytest.mark.parametrize("qtype,M,N,K", CASES)
@@ -156,7 +162,7 @@ def test_gate_up_silu_tiled(orc, dev, qtype, M):
 def test_tiled_not_handled(dev):
     """Tiled weights above M = 32, on the prefill, fused-RMSNorm and
     dequantize entries, or tiling a type without a tiled layout: not
-    handled, nothing launched."""
+    handled, nothing launched (Q5_K has no tiled layout)."""
     import torch
     from inferflux_amd import ops
     w = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
@@ -169,7 +175,7 @@ def test_tiled_not_handled(dev):
                    lambda: ops.qgemm_prefill_kernel(Q4_K_T, w, a, 64, 64, 256, ops.PREFILL_F16),
                    lambda: ops.qgemv_grouped_rmsnorm(Q4_K_T, [w], x[:1], nw, 1, [64], 256),
                    lambda: ops.dequantize(Q4_K_T, w, 64, 256),
-                   lambda: ops.repack_tiled(8, w, 4, 256)):
+                   lambda: ops.repack_tiled(13, w, 4, 256)):
             with pytest.raises((ops.NotHandled, KeyError)):
                 fn()
     assert lg.kernels == []
