@@ -25,8 +25,16 @@ def dry_dispatch(entry, qt, M, Ns, K):
     Y = (_P * n)(*[_fake(4 + i) for i in range(n)])
     NN = (ctypes.c_int * n)(*Ns)
     A, X, NW, B = _fake(8), _fake(9), _fake(10), _fake(11)
+    WS = _fake(12)  # a workspace "large enough" (1 GB) for the _ws entries
     with ops.launch_log(dry=True) as lg:
-        if entry in ("gemv", "gemv_accum"):
+        if entry in ("gemv_ws", "gemv_accum_ws"):
+            rc = L.ifx_qgemv_ws(qt, W[0], A, Y[0], ops.OUT_F32,
+                                ops.ACCUM if entry == "gemv_accum_ws" else ops.STORE, None, M,
+                                Ns[0], K, WS, 1 << 30, None)
+        elif entry == "grouped_ws":
+            rc = L.ifx_qgemv_grouped_ws(qt, n, W, Y, NN, A, ops.OUT_F32, ops.STORE, M, K, WS,
+                                        1 << 30, None)
+        elif entry in ("gemv", "gemv_accum"):
             rc = L.ifx_qgemv(qt, W[0], A, Y[0], ops.OUT_F32,
                              ops.ACCUM if entry == "gemv_accum" else ops.STORE, None, M, Ns[0], K,
                              None)

@@ -31,11 +31,23 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     from inferflux_amd import ops, synth
     note(f"launch {lid}: {entry} type={qt} M={M} N={Ns} K={K} -> {want}")
     seed = sum(Ns) + K + M
-    raw_qt = {108: 8, 114: 14}.get(qt, qt)  # row-split types: repack raw blocks on the GPU
+    # row-split / tiled types: repack raw blocks on the GPU
+    raw_qt = qt % 100 if qt > 100 else qt
+
+    def to_dev(w, n):
+        if qt > 200:
+            return ops.repack_tiled(raw_qt, up(w, dev), n, K)[1]
+        if qt > 100:
+            return ops.repack(raw_qt, up(w, dev), n, K)[1]
+        return up(w, dev)
     ws = [synth.blocks(raw_qt, n, K, seed=seed + i) for i, n in enumerate(Ns)]
-    W = [up(w, dev) for w in ws]
-    if raw_qt != qt:
-        W = [ops.repack(raw_qt, w, n, K)[1] for w, n in zip(W, Ns)]
+    W = [to_dev(w, n) for w, n in zip(ws, Ns)]
+    # the _ws entries: a zeroed workspace of the size the launch asks for
+    wsp = None
+    if entry.endswith("_ws"):
+        entry = entry[:-3]
+        nb = ops.qgemv_workspace_bytes(qt, list(Ns), M, K)
+        wsp = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
     rng = np.random.default_rng(seed)
     outl = 0.01 if entry.startswith("prefill") else 0.0
     x = synth.activations(M, K, seed=seed + 7, outlier_frac=outl)
@@ -52,28 +64,28 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         A = up(a, dev)
         X = up(x, dev)
 
+    if entry.startswith("gate_up_silu"):
+        wu = synth.blocks(raw_qt, Ns[0], K, seed=seed + 11)
+        Wu = to_dev(wu, Ns[0])
     with ops.launch_log() as lg:
         if entry == "gemv":
-            outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K)]
+            outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, workspace=wsp)]
         elif entry in ("gemv_accum", "quantize_accum"):
             y0 = up(base[:, :Ns[0]], dev)
             if entry == "gemv_accum":
-                ops.qgemv(qt, W[0], A, M, Ns[0], K, out=y0, mode=ops.ACCUM)
+                ops.qgemv(qt, W[0], A, M, Ns[0], K, out=y0, mode=ops.ACCUM, workspace=wsp)
             else:
                 ops.qgemv_grouped_rmsnorm(qt, W, X, None, M, list(Ns), K, outs=[y0],
                                           mode=ops.ACCUM)
             outs = [y0]
         elif entry == "grouped":
-            outs = ops.qgemv_grouped(qt, W, A, M, list(Ns), K)
+            outs = ops.qgemv_grouped(qt, W, A, M, list(Ns), K, workspace=wsp)
         elif entry == "grouped_rmsnorm":
             outs = ops.qgemv_grouped_rmsnorm(qt, W, X, NW, M, list(Ns), K, eps=1e-6)
         elif entry == "gate_up_silu_rmsnorm":
-            wu = synth.blocks(qt, Ns[0], K, seed=seed + 11)
-            h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], up(wu, dev), X, NW, M, Ns[0], K,
-                                                  eps=1e-6)
+            h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], Wu, X, NW, M, Ns[0], K, eps=1e-6)
         elif entry == "gate_up_silu":
-            wu = synth.blocks(qt, Ns[0], K, seed=seed + 11)
-            h, q = ops.qgemv_gate_up_silu(qt, W[0], up(wu, dev), A, M, Ns[0], K)
+            h, q = ops.qgemv_gate_up_silu(qt, W[0], Wu, A, M, Ns[0], K)
         elif entry == "prefill":
             outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, prefill=True)]
         elif entry == "prefill_int8":
@@ -87,8 +99,8 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         N = Ns[0]
         blocks = np.random.default_rng(seed).choice(N // 32, 16, replace=False)
         idx = (blocks[:, None] * 32 + np.arange(32)[None, :]).ravel()
-        g = orc.gemv_exact(qt, ws[0][idx], a, M, len(idx), K)
-        u = orc.gemv_exact(qt, wu[idx], a, M, len(idx), K)
+        g = orc.gemv_exact(raw_qt, ws[0][idx], a, M, len(idx), K)
+        u = orc.gemv_exact(raw_qt, wu[idx], a, M, len(idx), K)
         with np.errstate(over="ignore"):
             h_ref = g / (1.0 + np.exp(-g)) * u
         check_rows(down(h)[:, idx], h_ref)
@@ -97,7 +109,7 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         # the chain it replaces: grouped GEMV + SiLU producer, bit for bit
         # where the grouped launch forms the sums in the same order
         with ops.launch_log() as lg2:
-            g2, u2 = ops.qgemv_grouped(qt, [W[0], up(wu, dev)], A, M, [N, N], K)
+            g2, u2 = ops.qgemv_grouped(qt, [W[0], Wu], A, M, [N, N], K)
         if entry == "gate_up_silu_rmsnorm" or same_slot_waves(lg2.kernels[-1], want[0]):
             assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
         return
