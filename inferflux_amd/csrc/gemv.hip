@@ -604,14 +604,15 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu(const uint8_t *__restrict_
 }
 
 // Q4_K with K <= 2048 and M <= 2: the same fusion on the wide slices of the
-// grouped GEMV.  A row's K/64 <= 32 slices take half a wave, so a wave
-// computes 4 rows (2 per half) of one tensor: waves 0-7 the 32 gate rows of
-// the block, waves 8-15 the 32 up rows (the tensor is wave-uniform).  Lanes
-// 31 and 63 put the row totals in LDS; after one barrier 8 lanes per batch
-// column form h = silu(g) * u and quantize the block.  NORM = 1 / 2: the
-// Q8_1 activations are produced in the kernel from an fp32 / fp16 residual
-// (RMSNorm then Q8_1 by the first 256 threads, the standalone producer's
-// arithmetic) into LDS, their loads issued before the weight prefetch.
+// grouped GEMV.  A row's K/64 <= 32 slices take half a wave, so a wave of a
+// workgroup of NW waves computes 64 / NW rows (32 / NW per half) of one
+// tensor: waves [0, NW/2) the 32 gate rows of the block, the others the 32
+// up rows (the tensor is wave-uniform).  Lanes 31 and 63 put the row totals
+// in LDS; after one barrier 8 lanes per batch column form h = silu(g) * u
+// and quantize the block.  NORM = 1 / 2: the Q8_1 activations are produced
+// in the kernel from an fp32 / fp16 residual (RMSNorm then Q8_1 by the first
+// 256 threads, the standalone producer's arithmetic) into LDS, their loads
+// issued before the weight prefetch.
 struct SwigluArgs {
   const uint8_t *Wg, *Wu, *A;
   const void *x;
@@ -624,18 +625,20 @@ struct SwigluArgs {
 
 constexpr int kSwigluWideMaxK = 2048;
 
-template <int MC, bool F16H, int NORM>
-__global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args) {
-  constexpr int R = 2;
+template <int MC, bool F16H, int NORM, int NW = 16>
+__global__ __launch_bounds__(64 * NW) void k_gemv_swiglu_wide(const SwigluArgs args) {
+  static_assert(NW == 4 || NW == 8 || NW == 16, "waves per workgroup");
+  constexpr int kGW = NW / 2;   // waves per tensor
+  constexpr int R = 32 / NW;    // rows per half-wave
   __shared__ float gu[2][MC][32];  // [gate/up][column][output]
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[NORM ? MC * split_row_bytes(kSwigluWideMaxK) : 1];
   __shared__ float npart[4 * MC];
   const int M = args.M, N = args.N, K = args.K;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool is_up = wave >= 8;
+  const bool is_up = wave >= kGW;
   const int half = lane >> 5, lt = lane & 31;
-  const int orow0 = ((wave & 7) * 2 + half) * R;  // first output of this half-wave in the block
+  const int orow0 = ((wave % kGW) * 2 + half) * R;  // first output of this half-wave in the block
   const int col0 = blockIdx.y * MC;
   const int mvalid = min(MC, M - col0);
   const int nslice = K >> 6;
@@ -727,11 +730,27 @@ __global__ __launch_bounds__(1024) void k_gemv_swiglu_wide(const SwigluArgs args
 // One workgroup per batch column (MC = 1 at M = 2 as well): the MC = 2 kernel
 // needs 96 VGPRs, which leaves room for only one 16-wave workgroup per CU;
 // the second column's weight reads mostly hit the cache.
+template <int NORM, int NW>
+static void launch_swiglu_wide_nw(const SwigluArgs &a, bool f16h, hipStream_t s) {
+  const dim3 grid(a.N / 32, a.M);
+  if (f16h) IFX_LAUNCH(k_gemv_swiglu_wide, (1, true, NORM, NW), grid, dim3(64 * NW), 0, s, a);
+  else IFX_LAUNCH(k_gemv_swiglu_wide, (1, false, NORM, NW), grid, dim3(64 * NW), 0, s, a);
+}
+// Waves per workgroup, measured on MI355X (3B gate/up 11008 x 2048, cold
+// weights, NW = 16 / 8 / 4): with the RMSNorm fused in 8 (M = 1: 8.4 / 8.1 /
+// 8.7 us; M = 2: 10.8 / 10.2 / 10.5), from Q8_1 activations 16 (7.1 / 9.4 /
+// 9.9 us).  IFX_SWIGLU_NW in {4, 8, 16} overrides (tuning; read once).
 template <int NORM>
 static void launch_swiglu_wide(const SwigluArgs &a, bool f16h, hipStream_t s) {
-  const dim3 grid(a.N / 32, a.M);
-  if (f16h) IFX_LAUNCH(k_gemv_swiglu_wide, (1, true, NORM), grid, dim3(1024), 0, s, a);
-  else IFX_LAUNCH(k_gemv_swiglu_wide, (1, false, NORM), grid, dim3(1024), 0, s, a);
+  static const int env = [] {
+    const char *e = getenv("IFX_SWIGLU_NW");
+    const int v = e ? atoi(e) : 0;
+    return (v == 4 || v == 8 || v == 16) ? v : 0;
+  }();
+  const int nw = env ? env : NORM ? 8 : 16;
+  if (nw == 4) launch_swiglu_wide_nw<NORM, 4>(a, f16h, s);
+  else if (nw == 8) launch_swiglu_wide_nw<NORM, 8>(a, f16h, s);
+  else launch_swiglu_wide_nw<NORM, 16>(a, f16h, s);
 }
 
 static bool swiglu_wide_env() {

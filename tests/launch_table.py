@@ -55,7 +55,7 @@ LAUNCHES = [
     ("c2f_qkv_m1", "grouped_rmsnorm", Q4_K, 1, QKV3, 2048, ["k_gemv<12,1,2,1,4,0,2,1>"]),
     ("c2f_o_m1", "quantize_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2,3>"]),
     ("c2f_gate_up_m1", "gate_up_silu_rmsnorm", Q4_K, 1, (11008,), 2048,
-     ["k_gemv_swiglu_wide<1,0,1>"]),
+     ["k_gemv_swiglu_wide<1,0,1,8>"]),
     # config 3: LM head 151936 x 2048
     ("c3_q8_0_m1", "gemv", Q8_0, 1, (151936,), 2048, ["k_gemv<8,1,4,1,4,0,1>"]),
     ("c3_q8_0_m8", "gemv", Q8_0, 8, (151936,), 2048, ["k_mmvq<8,1,1,0>"]),
