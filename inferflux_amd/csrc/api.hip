@@ -190,10 +190,10 @@ bool use_lds(int qtype, int M, int K, int n_total) {
 // 3 <= M <= 8 on long-K launches with fp32 outputs (K >= 8192: the down
 // projection, 2048 x 11008 Q6_K at M = 3 / 4: 12.7 / 12.9 us against 13.9 /
 // 14.5 on mmvq.hip), which it splits over several workgroups, and
-// 4 <= M <= 8 on launches of at most 8 super-blocks per row (3B Q/K/V and
-// O, K = 2048, one super-block per wave: O at M = 4 / 8 4.8 / 5.0 us against
-// 5.1 / 5.2 on mmvq.hip).  IFX_SLOT=0|1 forces it off / on for every M it
-// fits (1..8; tuning; read once).
+// 4 <= M <= 8 on launches of at most 24 super-blocks per row (Q/K/V and O,
+// 8 waves, no split: 3B O at M = 4 / 8 4.8 / 5.0 us against 5.1 / 5.2 on
+// mmvq.hip; 14B O 5120 x 5120 at M = 8 7.2 against 8.9).  IFX_SLOT=0|1
+// forces it off / on for every M it fits (1..8; tuning; read once).
 bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
   static const int v = [] {
     const char *e = getenv("IFX_SLOT");
@@ -201,7 +201,7 @@ bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
   }();
   if (!ifx::gemv_slot_fits(qtype, M, K) || v == 0) return false;
   if (v == 1) return true;
-  return (M >= 5 && n_total >= 8192) || (M >= 3 && K >= 8192 && !f16) || (M >= 4 && K <= 2048);
+  return (M >= 5 && n_total >= 8192) || (M >= 3 && K >= 8192 && !f16) || (M >= 4 && K <= 6144);
 }
 
 // Decode batches 17 <= M <= 32 on the fp16-dequant MFMA GEMV (gemv_dq.hip),

@@ -526,8 +526,10 @@ namespace {
 // gridDim.y, fp32 outputs only), measured on MI355X:
 //  * wide launches (>= 256 row groups): no split, the fewest waves per
 //    workgroup (1..8) that give 4096 waves (an LM head: 1; N = 11008: 8);
-//  * few row groups and a long K (>= 32 super-blocks, e.g. a down
-//    projection with N = 2048): 4 waves, 8 splits.
+//  * few row groups and K up to 24 super-blocks (Q/K/V, O): 8 waves, no
+//    split;
+//  * few row groups and a longer K (e.g. a down projection with N = 2048):
+//    4 waves, 8 splits.
 // IFX_SLOT_KW in {1, 2, 4, 8} and IFX_SLOT_SPLIT >= 1 override (tuning;
 // read once); IFX_SLOT_SPLIT=1 gives bitwise reproducible results.
 void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
@@ -543,14 +545,14 @@ void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
   const bool wide = blocks >= 256;
   kw = env_kw;
   if (!kw) {
-    // short K (at most 8 super-blocks): one super-block per wave, no split
-    // (3B O 2048 x 2048 at M = 8, tiled: 4.4 us with 8 waves against 5.8
-    // with 4 waves and 2 ordered splits)
-    kw = wide ? 1 : nsb <= 8 ? 8 : 4;
+    // K up to 24 super-blocks: 8 waves, no split (3B O 2048 x 2048 at M = 8,
+    // tiled: 4.4 us against 5.8 with 4 waves and 2 ordered splits; 14B Q/K/V
+    // 7168 x 5120 at M = 16: 9.8 us against 12.3 with 4 waves and 5 splits)
+    kw = wide ? 1 : nsb <= 24 ? 8 : 4;
     while (wide && kw < 8 && blocks * kw < 4096) kw *= 2;
   }
   while (kw > 1 && kw > nsb) kw /= 2;
-  ks = env_ks > 0 ? env_ks : (wide ? 1 : 8);
+  ks = env_ks > 0 ? env_ks : (wide || (!env_kw && nsb <= 24)) ? 1 : 8;
   ks = f16 ? 1 : max(1, min(ks, nsb / kw));
 }
 

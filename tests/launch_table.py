@@ -76,8 +76,8 @@ LAUNCHES = [
     ("c4_qkv_m1", "grouped", Q4_K, 1, QKV14, 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
     ("c4_o_m1", "gemv_accum", Q4_K, 1, (5120,), 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
     ("c4_gate_up_m1", "grouped", Q4_K, 1, (13824, 13824), 5120, ["k_gemv<12,1,2,1,4,0,4>"]),
-    ("c4_qkv_m8", "grouped", Q4_K, 8, QKV14, 5120, ["k_mmvq<12,1,8,0>"]),
-    ("c4_o_m8", "gemv_accum", Q4_K, 8, (5120,), 5120, ["k_mmvq<12,1,8,0>"]),
+    ("c4_qkv_m8", "grouped", Q4_K, 8, QKV14, 5120, ["k_gemv_slot<12,8,8,0,0>"]),
+    ("c4_o_m8", "gemv_accum", Q4_K, 8, (5120,), 5120, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c4_gate_up_m8", "grouped", Q4_K, 8, (13824, 13824), 5120, ["k_gemv_slot<12,8,8,0,0>"]),
     # the benchmark's tiled forms: config 1 at M = 8, the 3B layer at M = 4 / 8
     # and the 14B layer at M = 16 / 32 with ordered K splits, the LM head at M = 8
@@ -94,8 +94,8 @@ LAUNCHES = [
     ("c2t_down_m8", "gemv_accum_ws", Q6_K_T, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
     ("c3_q8_0_t_m8", "gemv", Q8_0_T, 8, (151936,), 2048, ["k_gemv_slot<8,8,1,0,0,0,1>"]),
     ("c3_q6_k_t_m8", "gemv", Q6_K_T, 8, (151936,), 2048, ["k_gemv_slot<14,8,1,0,0,0,1>"]),
-    ("c4t_qkv_m16", "grouped_ws", Q4_K_T, 16, QKV14, 5120, ["k_gemv_slot<12,16,4,0,2,0,1>"]),
-    ("c4t_o_m16", "gemv_accum_ws", Q4_K_T, 16, (5120,), 5120, ["k_gemv_slot<12,16,4,0,2,0,1>"]),
+    ("c4t_qkv_m16", "grouped_ws", Q4_K_T, 16, QKV14, 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
+    ("c4t_o_m16", "gemv_accum_ws", Q4_K_T, 16, (5120,), 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
     ("c4t_gate_up_m16", "grouped_ws", Q4_K_T, 16, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_down_m16", "gemv_accum_ws", Q6_K_T, 16, (5120,), 13824,
      ["k_gemv_slot<14,16,4,0,2,0,1>"]),

@@ -119,7 +119,7 @@ def test_tiled_routing():
     rc, k = dry_dispatch("gemv", ops.Q6_K_T, 8, (2048,), 11008)  # few row groups: K split
     assert rc == 0 and k == ["k_fill_zero", "k_gemv_slot<14,8,4,0,1,0,1>"]
     rc, k = dry_dispatch("grouped", ops.Q4_K_T, 16, (5120, 1024, 1024), 5120)
-    assert rc == 0 and k == ["k_fill_zero", "k_gemv_slot<12,16,4,0,1,0,1>"]
+    assert rc == 0 and k == ["k_gemv_slot<12,16,8,0,0,0,1>"]  # short K: 8 waves, no split
     rc, k = dry_dispatch("grouped", ops.Q4_K_T, 32, (5120, 1024, 1024), 5120)
     assert rc == 0 and k[-1] == "k_gemv_dq<12,0,1,1>"
     for M in (1, 4, 8):
