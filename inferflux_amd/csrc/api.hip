@@ -210,12 +210,16 @@ bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
 // 30.3 us (53.3); 3B gate 11008 x 2048: 12.5 us (15.8).  Its VALU work per
 // weight does not grow with M; below M = 17 the integer kernels are faster.
 // IFX_DQ=0|1 forces it off / on for every M it fits (1..32; tuning; read
-// once).
-bool use_dq(int qtype, int M, int K, bool f16) {
+// once); IFX_DQ=0 also keeps tiled launches up to M = 16 on the slot kernel.
+int dq_env() {
   static const int v = [] {
     const char *e = getenv("IFX_DQ");
     return e ? (e[0] == '1' ? 1 : 0) : -1;
   }();
+  return v;
+}
+bool use_dq(int qtype, int M, int K, bool f16) {
+  const int v = dq_env();
   if (!ifx::gemv_dq_fits(qtype, M, K) || (f16 && !ifx::gemv_dq_fits_f16(M, K)) || v == 0)
     return false;
   return v == 1 || M > 16;
@@ -279,7 +283,8 @@ Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
     // GEMV against 29.5); the fp16-dequant GEMV above M = 16 (Q6_K down
     // 5120 x 13824 M = 16: 19.0 us on the slot GEMV, 20.9 on fp16-dequant)
     if (M <= kMaxSlotM) return Route::Slot;
-    if (M <= 2 * kMaxSlotM && (qt == IFX_TYPE_Q6_K_T || n_total < 8192)) return Route::Slot;
+    if (M <= 2 * kMaxSlotM && (qt == IFX_TYPE_Q6_K_T || n_total < 8192 || dq_env() == 0))
+      return Route::Slot;
     return Route::Dq;
   }
   if (!grouped && !gemv_only(qt) && M > kMaxSkinnyM && use_f16_gemm(qt, M, K)) return Route::F16Gemm;
