@@ -390,17 +390,21 @@ def main():
                               for n in ("qkv", "o", "gate_up", "down", "producers")},
                 "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_b * 1e-6), 1),
             }
-            # the same on the tiled weights, K splits reduced in order
-            runt = decode_layer_runner(layer3b, M, seed=10 + M, fused="batch_swiglu",
-                                       tiled=layer3b_t, ordered=True)
-            us_t = time_loop(runt, steps, args.warmup)
-            per_m[M]["tiled_swiglu_ordered"] = {
-                "us_per_layer": round(us_t, 2),
-                "layer_GBs": round(layer_alg_bytes[M] / us_t / 1e3, 1),
-                "kernel_us": {n: round(time_loop(lambda i, n=n: runt(i, n), steps, args.warmup), 2)
-                              for n in ("qkv", "o", "gate_up", "down", "producers")},
-                "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_t * 1e-6), 1),
-            }
+            # the same on the tiled weights: K splits added with fp32 atomics
+            # (the plain entries, as the reference), and reduced in split
+            # order through a workspace (the deterministic _ws entries)
+            for tname, ordered in (("tiled_swiglu", False), ("tiled_swiglu_ordered", True)):
+                runt = decode_layer_runner(layer3b, M, seed=10 + M, fused="batch_swiglu",
+                                           tiled=layer3b_t, ordered=ordered)
+                us_t = time_loop(runt, steps, args.warmup)
+                per_m[M][tname] = {
+                    "us_per_layer": round(us_t, 2),
+                    "layer_GBs": round(layer_alg_bytes[M] / us_t / 1e3, 1),
+                    "kernel_us": {n: round(time_loop(lambda i, n=n: runt(i, n), steps,
+                                                     args.warmup), 2)
+                                  for n in ("qkv", "o", "gate_up", "down", "producers")},
+                    "tokens_per_s_equiv": round(M / (workloads.QWEN3B_LAYERS * us_t * 1e-6), 1),
+                }
         if M == 1:
             fb = form_kernel_bytes(layer3b, M, "reference")
             forms["reference"] = (run, us_layer, {k: kern[k] for k in fb}, fb)
@@ -558,7 +562,7 @@ def main():
         for M in (16, 32):
             all_bytes = sum(launch_bytes(layer14, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
             steps = max(20, args.steps // 4)
-            for key, kw in ((f"M{M}", {}),
+            for key, kw in ((f"M{M}", {}), (f"M{M}_tiled", {"tiled": layer14_t}),
                             (f"M{M}_tiled_ordered", {"tiled": layer14_t, "ordered": True})):
                 run = decode_layer_runner(layer14, M, seed=40 + M, **kw)
                 us_layer = time_loop(run, steps, 5)

@@ -370,8 +370,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   float yv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) yv[i] = acc0[i] + acc1[i];
+  float base[16];  // SPLIT == 2, accumulate mode: Y before this launch
   if constexpr (SPLIT == 2) {
     const int ks = gridDim.y;
+    // the accumulate base, requested before the arrival so that its latency
+    // overlaps it (only the last workgroup uses it; nothing in this launch
+    // writes Y before that workgroup's epilogue)
+    const int nc = min(n, N - 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+      base[i] = (args.mode == 1 && m < M)
+                    ? static_cast<const float *>(sg.Y)[static_cast<int64_t>(m) * N + nc] : 0.0f;
+    }
     constexpr int kSlot = 64 * 16;  // floats per wave and split
     float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * kWaves * kSlot +
                   wave * kSlot + lane;
@@ -422,7 +433,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
       Yh[o] = static_cast<uint16_t>(f2h_bits(y));
     } else {
       float *Yf = static_cast<float *>(sg.Y);
-      if (args.mode == 1) y += Yf[o];
+      if (args.mode == 1) y += SPLIT == 2 ? base[i] : Yf[o];
       else if (args.mode == 2) y += static_cast<const float *>(sg.bias)[n];
       Yf[o] = y;
     }

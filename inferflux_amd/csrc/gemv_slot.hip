@@ -458,16 +458,31 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
     }
     return;
   }
+  float base[NM];  // SPLIT == 2, accumulate mode: Y before this launch
   if constexpr (SPLIT == 2) {
+    // wave 0 holds the workgroup's sums (the other waves are done); it alone
+    // stores them, counts the workgroup in, and if last reduces the slots
+    if (wave > 0) return;
     const int ks = gridDim.y;
-    float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * 64 * NM + lane;
-    if (wave == 0) {
+    // the accumulate base, requested before the arrival so that its latency
+    // overlaps it (only the last workgroup uses it; nothing in this launch
+    // writes Y before that workgroup's epilogue)
+    const int nc = min(n0 + c32, N - 1);
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi)
-        if (2 * (mi & ~3) + 4 * h + (mi & 3) < M) st_dev(mine + 64 * mi, acc[mi]);
-      wait_own_memory();
+    for (int mi = 0; mi < NM; ++mi) {
+      const int m = 2 * (mi & ~3) + 4 * h + (mi & 3);
+      base[mi] = (args.mode == 1 && m < M)
+                     ? static_cast<const float *>(sg.Y)[static_cast<int64_t>(m) * N + nc] : 0.0f;
     }
-    if (!split_arrive_last(args.ws.cnt + bx, ks) || wave > 0) return;
+    float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * 64 * NM + lane;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+      if (2 * (mi & ~3) + 4 * h + (mi & 3) < M) st_dev(mine + 64 * mi, acc[mi]);
+    wait_own_memory();
+    uint32_t prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(args.ws.cnt + bx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(prev) != static_cast<uint32_t>(ks - 1)) return;
     // all slots, this workgroup's included, in split order; eight slots'
     // loads in flight at a time
     const float *slot0 = args.ws.part + static_cast<int64_t>(bx) * ks * 64 * NM + lane;
@@ -513,7 +528,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       Yh[o] = static_cast<uint16_t>(f2h_bits(y));
     } else {
       float *Yf = static_cast<float *>(sg.Y);
-      if (mode == 1) y += Yf[o];
+      if (mode == 1) y += SPLIT == 2 ? base[mi] : Yf[o];
       else if (mode == 2) y += static_cast<const float *>(sg.bias)[n];
       Yf[o] = y;
     }
