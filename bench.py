@@ -562,18 +562,23 @@ def main():
         for M in (16, 32):
             all_bytes = sum(launch_bytes(layer14, l[0], M)[1] for l in workloads.DECODE_LAUNCHES)
             steps = max(20, args.steps // 4)
-            for key, kw in ((f"M{M}", {}), (f"M{M}_tiled", {"tiled": layer14_t}),
-                            (f"M{M}_tiled_ordered", {"tiled": layer14_t, "ordered": True})):
+            forms14 = [(f"M{M}", {}), (f"M{M}_tiled", {"tiled": layer14_t}),
+                       (f"M{M}_tiled_ordered", {"tiled": layer14_t, "ordered": True})]
+            if M <= 16:  # SiLU * up + Q8_1 in the gate/up launch (tiled, M <= 16)
+                forms14.append((f"M{M}_tiled_swiglu", {"tiled": layer14_t,
+                                                       "fused": "batch_swiglu"}))
+            for key, kw in forms14:
                 run = decode_layer_runner(layer14, M, seed=40 + M, **kw)
                 us_layer = time_loop(run, steps, 5)
                 kern = {l[0]: time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
                         for l in workloads.DECODE_LAUNCHES}
-                kern["producers_x4"] = time_loop(lambda i: run(i, "producers"), steps, 5)
+                kern["producers_x3" if kw.get("fused") else "producers_x4"] = time_loop(
+                    lambda i: run(i, "producers"), steps, 5)
                 c4[key] = {
                     "us_per_layer": round(us_layer, 2),
                     "layer_GBs": round(all_bytes / us_layer / 1e3, 1),
                     "gemv_GBs": round(all_bytes / sum(v for k, v in kern.items()
-                                                      if k != "producers_x4") / 1e3, 1),
+                                                      if not k.startswith("producers")) / 1e3, 1),
                     "kernel_us": {k: round(v, 2) for k, v in kern.items()},
                     "tokens_per_s_equiv": round(M / (workloads.QWEN14B_LAYERS * us_layer * 1e-6), 1),
                 }

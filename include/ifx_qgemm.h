@@ -172,9 +172,10 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
  * NULL) and/or quantized to Q8_1 blocks of 32 consecutive outputs in
  * q8_1_out [M][N/32] (may be NULL; not both), ready for the down
  * projection without a separate quantize launch.  Handles 1 <= M <= 2 and
- * N % 32 == 0 (every type), and 3 <= M <= 8 for Q4_K / Q6_K with K % 256
- * == 0 (the slot-packed MFMA GEMV: h and its blocks equal ifx_qgemv_grouped
- * + ifx_silu_mul_quantize_q8_1 bit for bit); other shapes return
+ * N % 32 == 0 (every type), 3 <= M <= 8 for Q4_K / Q6_K with K % 256 == 0,
+ * and M <= 16 on tiled copies (the slot-packed MFMA GEMV: h and its blocks
+ * equal ifx_qgemv_grouped + ifx_silu_mul_quantize_q8_1 bit for bit where
+ * the grouped launch runs the same geometry); other shapes return
  * IFX_BAD_GEOMETRY (not handled: use those two calls).
  * Replaces FusedQuantGemm::FusedGateUpSiluGemvQ8_1 and
  * FusedGateUpSiluGemvQ8_1WithEpilogue (fused_quant_gemm.h:281-307; kernels

@@ -589,11 +589,13 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
   if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
   // the fused kernels serve the decode batch (M <= 2: the v_dot4 GEMV;
-  // 3 <= M <= 8, Q4_K / Q6_K: the slot-packed MFMA GEMV) and whole Q8_1
-  // blocks of outputs; other shapes take the grouped GEMV + SiLU producer
+  // 3 <= M <= 8, Q4_K / Q6_K, and tiled rows up to M = 16: the slot-packed
+  // MFMA GEMV) and whole Q8_1 blocks of outputs; other shapes take the
+  // grouped GEMV + SiLU producer
   const int max_m = tiled(quant_type) ? 0
                     : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
-  const bool slot = M > max_m && M <= kMaxSlotM && ifx::gemv_slot_fits(quant_type, M, K);
+  const bool slot = M > max_m && M <= (tiled(quant_type) ? 2 * kMaxSlotM : kMaxSlotM) &&
+                    ifx::gemv_slot_fits(quant_type, M, K);
   if (M < 1 || (M > max_m && !slot) || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)

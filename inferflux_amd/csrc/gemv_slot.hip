@@ -437,8 +437,8 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       }
     }
     __syncthreads();
-    const int m = threadIdx.x >> 3, l = threadIdx.x & 7;  // wave 0: 8 lanes per batch row
-    if (threadIdx.x < 64 && m < M) {
+    const int m = threadIdx.x >> 3, l = threadIdx.x & 7;  // 8 lanes per batch row
+    if (threadIdx.x < 8 * MP && m < M) {
       const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[m * 32 + 4 * l]);
       const f32x4 u4 = *reinterpret_cast<const f32x4 *>(&gu[(MP + m) * 32 + 4 * l]);
       const f32x4 hv = silu_mul4(g4, u4);
@@ -633,16 +633,16 @@ void slot_q(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
 // against 12.4 / 12.4 / 13.1 with 8; 14B 13824 x 5120 at M = 8: 24.4 against
 // 27.1).  With fewer than 4 super-blocks per row the waves match them.
 // IFX_SLOT_KW overrides, as for the plain launch.
-template <int QT, int KW, bool TL>
+template <int QT, int MP, int KW, bool TL>
 void slot_swiglu_launch(const SlotArgs &args, bool f16h, hipStream_t s) {
-  constexpr int lds = slot_lds_bytes<QT, 8, KW, 2>();
+  constexpr int lds = slot_lds_bytes<QT, MP, KW, 2>();
   const dim3 grid(args.seg[0].N / 32);
   if constexpr (TL) {
-    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true, true), grid, dim3(128 * KW), lds, s, args);
-    else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true, true), grid, dim3(128 * KW), lds, s, args);
+    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, true, false, true, true), grid, dim3(128 * KW), lds, s, args);
+    else IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, false, false, true, true), grid, dim3(128 * KW), lds, s, args);
   } else {
-    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, true, false, true), grid, dim3(128 * KW), lds, s, args);
-    else IFX_LAUNCH(k_gemv_slot, (QT, 8, KW, false, false, true), grid, dim3(128 * KW), lds, s, args);
+    if (f16h) IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, true, false, true), grid, dim3(128 * KW), lds, s, args);
+    else IFX_LAUNCH(k_gemv_slot, (QT, MP, KW, false, false, true), grid, dim3(128 * KW), lds, s, args);
   }
 }
 
@@ -651,11 +651,21 @@ void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
   int kw = 4, ks = 1;
   if (getenv("IFX_SLOT_KW")) choose_slot_work(1 << 20, args.K >> 8, false, kw, ks);
   while (kw > 1 && kw > (args.K >> 8)) kw /= 2;
+  // tiled rows above M = 8: two 16-row slots per MFMA
+  if (TL && args.M > 8) {
+    switch (kw) {
+    case 1: slot_swiglu_launch<QT, 16, 1, TL>(args, f16h, s); break;
+    case 2: slot_swiglu_launch<QT, 16, 2, TL>(args, f16h, s); break;
+    case 4: slot_swiglu_launch<QT, 16, 4, TL>(args, f16h, s); break;
+    default: slot_swiglu_launch<QT, 16, 8, TL>(args, f16h, s); break;
+    }
+    return;
+  }
   switch (kw) {
-  case 1: slot_swiglu_launch<QT, 1, TL>(args, f16h, s); break;
-  case 2: slot_swiglu_launch<QT, 2, TL>(args, f16h, s); break;
-  case 4: slot_swiglu_launch<QT, 4, TL>(args, f16h, s); break;
-  default: slot_swiglu_launch<QT, 8, TL>(args, f16h, s); break;
+  case 1: slot_swiglu_launch<QT, 8, 1, TL>(args, f16h, s); break;
+  case 2: slot_swiglu_launch<QT, 8, 2, TL>(args, f16h, s); break;
+  case 4: slot_swiglu_launch<QT, 8, 4, TL>(args, f16h, s); break;
+  default: slot_swiglu_launch<QT, 8, 8, TL>(args, f16h, s); break;
   }
 }
 
@@ -712,13 +722,14 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
   return last_error();
 }
 
-// Fused gate/up/SiLU for 1 <= M <= 8 (Q4_K / Q6_K, K % 256 == 0, N % 32 == 0;
+// Fused gate/up/SiLU for 1 <= M <= 8, tiled rows up to M = 16 (K % 256 == 0, N % 32 == 0;
 // checked by the caller): H (fp32 / fp16 with f16h, or NULL) and / or the
 // Q8_1 blocks Q (or NULL).
 hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
                                    void *H, bool f16h, void *Q, int M, int N, int K,
                                    hipStream_t stream) {
-  if (!gemv_slot_fits(qtype, M, K) || M > 8 || N % 32 != 0) return hipErrorInvalidValue;
+  const bool t = qtype == kTypeQ4_KT || qtype == kTypeQ6_KT || qtype == kTypeQ8_0T;
+  if (!gemv_slot_fits(qtype, M, K) || M > (t ? 16 : 8) || N % 32 != 0) return hipErrorInvalidValue;
   SlotArgs args{};
   args.seg[0] = SlotSeg{static_cast<const uint8_t *>(Wg), nullptr, nullptr, N, 0};
   args.seg[1] = SlotSeg{static_cast<const uint8_t *>(Wu), nullptr, nullptr, N, 0};

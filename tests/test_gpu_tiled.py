@@ -6,7 +6,7 @@ the dispatch runs the same kernel and split on both."""
 import numpy as np
 import pytest
 
-from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, up
+from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, same_slot_waves, up
 
 pytestmark = pytest.mark.gpu
 
@@ -134,7 +134,8 @@ def test_grouped_tiled(orc, dev, M):
         check_rows(down(y), orc.gemv_exact(Q4_K, w, a, M, n, K))
 
 
-@pytest.mark.parametrize("qtype,M", [(Q4_K, 1), (Q4_K, 4), (Q4_K, 8), (Q6_K, 3)])
+@pytest.mark.parametrize("qtype,M", [(Q4_K, 1), (Q4_K, 4), (Q4_K, 8), (Q6_K, 3), (Q4_K, 12),
+                                     (Q4_K, 16), (Q6_K, 9)])
 def test_gate_up_silu_tiled(orc, dev, qtype, M):
     from inferflux_amd import ops, synth
     note(f"gate_up_silu tiled type={qtype} M={M}")
@@ -153,10 +154,16 @@ def test_gate_up_silu_tiled(orc, dev, qtype, M):
     u = orc.gemv_exact(qtype, wu, a, M, N, K)
     check_rows(down(h), g / (1.0 + np.exp(-g)) * u)
     assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
-    if M >= 3:  # the raw layout runs the same kernel: the same bits
+    if 3 <= M <= 8:  # the raw layout runs the same kernel: the same bits
         hr, qr = ops.qgemv_gate_up_silu(qtype, up(wg, dev), up(wu, dev), A, M, N, K)
         assert np.array_equal(down(h).view(np.uint32), down(hr).view(np.uint32))
         assert np.array_equal(down(q), down(qr))
+    if M > 8:  # 16-row slots: grouped GEMV + SiLU producer on the same geometry
+        assert lg.kernels[0].startswith(f"k_gemv_slot<{qtype},16,")
+        with ops.launch_log() as lg2:
+            g2, u2 = ops.qgemv_grouped(tt, [WG, WU], A, M, [N, N], K)
+        if same_slot_waves(lg2.kernels[-1], lg.kernels[0]):
+            assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
 
 
 def test_tiled_not_handled(dev):
