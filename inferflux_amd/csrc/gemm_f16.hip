@@ -145,10 +145,11 @@ __device__ __forceinline__ void fetch(Raw<QT> &r, rsrc_t Wr, rsrc_t Ar, uint32_t
 // values (0, 2) and (1, 3).  q ^ 0x80 = q + 128 as an unsigned byte, so
 // (0x6400 | byte) - 1152 = q exactly; the product is rounded once.
 __device__ __forceinline__ void i8x4_to_h(uint32_t x, h2 d, uint32_t &p02, uint32_t &p13) {
+  const uint32_t mg = vreg(kMagic);
   x ^= 0x80808080u;
   const h2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
-  const h2 a = as_h2((x & 0x00FF00FFu) | kMagic) + off;
-  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + off;
+  const h2 a = as_h2((x & 0x00FF00FFu) | mg) + off;
+  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | mg) + off;
   p02 = as_u32(a * d);
   p13 = as_u32(b * d);
 }
@@ -156,8 +157,25 @@ __device__ __forceinline__ void i8x4_to_h(uint32_t x, h2 d, uint32_t &p02, uint3
 // Unsigned byte codes v (< 1024) -> fp16 pairs of (v + bias) * d - mn.
 __device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint32_t &p02,
                                           uint32_t &p13) {
-  const h2 a = as_h2((x & 0x00FF00FFu) | kMagic) + bias;
-  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + bias;
+  const uint32_t mg = vreg(kMagic);
+  const h2 a = as_h2((x & 0x00FF00FFu) | mg) + bias;
+  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | mg) + bias;
+  p02 = as_u32(__builtin_elementwise_fma(a, d, -mn));
+  p13 = as_u32(__builtin_elementwise_fma(b, d, -mn));
+}
+
+// Nibble codes of a word of packed 4-bit codes (HI = 0: low, 1: high
+// nibbles) -> fp16 pairs q * d - mn of bytes (0, 2) and (1, 3).  Low
+// nibbles sit in mantissa bits 0..3 under the magic 1024 (ulp 1): 1024 + q;
+// high nibbles stay in bits 4..7, under the magic 64 (0x5400, ulp 1/16)
+// also exactly 64 + q, so neither needs more than the one shift by 8.
+template <int HI>
+__device__ __forceinline__ void q4x4_to_h(uint32_t x, h2 d, h2 mn, uint32_t &p02, uint32_t &p13) {
+  constexpr uint32_t msk = HI ? 0x00F000F0u : 0x000F000Fu;
+  const uint32_t mg = vreg(HI ? 0x54005400u : kMagic);
+  const h2 bias = splat(HI ? -64.0f : -1024.0f);
+  const h2 a = as_h2((x & msk) | mg) + bias;
+  const h2 b = as_h2(((x >> 8) & msk) | mg) + bias;
   p02 = as_u32(__builtin_elementwise_fma(a, d, -mn));
   p13 = as_u32(__builtin_elementwise_fma(b, d, -mn));
 }
@@ -207,13 +225,12 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     const float m1 = static_cast<float>((mw >> (sh + 8)) & 0xFFu);
     const h2 d0 = splat(d * sc0), d1 = splat(d * sc1);
     const h2 n0 = splat(dmin * m0), n1 = splat(dmin * m1);
-    const h2 b0 = splat(-1024.0f);
     uint32_t lo[8], hi[8];
     const uint32_t in[4] = {r.w1.x, r.w1.y, r.w1.z, r.w1.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      u8x4_to_h(in[j] & 0x0F0F0F0Fu, b0, d0, n0, lo[2 * j], lo[2 * j + 1]);
-      u8x4_to_h((in[j] >> 4) & 0x0F0F0F0Fu, b0, d1, n1, hi[2 * j], hi[2 * j + 1]);
+      q4x4_to_h<0>(in[j], d0, n0, lo[2 * j], lo[2 * j + 1]);
+      q4x4_to_h<1>(in[j], d1, n1, hi[2 * j], hi[2 * j + 1]);
     }
     u32x4 *dlo = reinterpret_cast<u32x4 *>(wrow + 16 * part);
     u32x4 *dhi = reinterpret_cast<u32x4 *>(wrow + 32 + 16 * part);

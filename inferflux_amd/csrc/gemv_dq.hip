@@ -74,27 +74,36 @@ __device__ __forceinline__ h2 splat(float f) {
 // Signed byte codes (four per word) times d -> fp16 pairs of values (0, 2)
 // and (1, 3): (0x6400 | (q ^ 0x80)) - 1152 = q exactly, one rounding.
 __device__ __forceinline__ void i8x4_to_h(uint32_t x, h2 d, uint32_t &p02, uint32_t &p13) {
+  const uint32_t mg = vreg(kMagic);
   x ^= 0x80808080u;
   const h2 off = splat(-1152.0f);
-  p02 = as_u32((as_h2((x & 0x00FF00FFu) | kMagic) + off) * d);
-  p13 = as_u32((as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + off) * d);
+  p02 = as_u32((as_h2((x & 0x00FF00FFu) | mg) + off) * d);
+  p13 = as_u32((as_h2(((x >> 8) & 0x00FF00FFu) | mg) + off) * d);
 }
 
 // Byte codes v (< 1024, four per word) -> fp16 pairs (v + bias) * d - mn of
 // values (0, 2) and (1, 3).
 __device__ __forceinline__ void u8x4_to_h(uint32_t x, h2 bias, h2 d, h2 mn, uint32_t &p02,
                                           uint32_t &p13) {
-  const h2 a = as_h2((x & 0x00FF00FFu) | kMagic) + bias;
-  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | kMagic) + bias;
+  const uint32_t mg = vreg(kMagic);
+  const h2 a = as_h2((x & 0x00FF00FFu) | mg) + bias;
+  const h2 b = as_h2(((x >> 8) & 0x00FF00FFu) | mg) + bias;
   p02 = as_u32(__builtin_elementwise_fma(a, d, -mn));
   p13 = as_u32(__builtin_elementwise_fma(b, d, -mn));
 }
 
-// Nibble codes (shift 0: low, 4: high) of two words of packed 4-bit codes
-// -> one 8-value operand (q + bias) * d - mn, one and-or per pair.
-__device__ __forceinline__ h8 op_q4(uint32_t x0, uint32_t x1, int sh, h2 bias, h2 d, h2 mn) {
-  const uint32_t w[4] = {((x0 >> sh) & 0x000F000Fu) | kMagic, ((x0 >> (sh + 8)) & 0x000F000Fu) | kMagic,
-                         ((x1 >> sh) & 0x000F000Fu) | kMagic, ((x1 >> (sh + 8)) & 0x000F000Fu) | kMagic};
+// Nibble codes (HI = 0: low, 1: high nibbles) of two words of packed 4-bit
+// codes -> one 8-value operand q * d - mn.  Low nibbles sit in mantissa
+// bits 0..3 under the magic 1024 (ulp 1): 1024 + q; high nibbles stay in
+// bits 4..7, under the magic 64 (0x5400, ulp 1/16) also exactly 64 + q; so
+// one shift per word serves both, and each pair is one and-or.
+template <int HI>
+__device__ __forceinline__ h8 op_q4(uint32_t x0, uint32_t x1, h2 d, h2 mn) {
+  constexpr uint32_t msk = HI ? 0x00F000F0u : 0x000F000Fu;
+  const uint32_t mg = vreg(HI ? 0x54005400u : kMagic);
+  const h2 bias = splat(HI ? -64.0f : -1024.0f);
+  const uint32_t w[4] = {(x0 & msk) | mg, ((x0 >> 8) & msk) | mg, (x1 & msk) | mg,
+                         ((x1 >> 8) & msk) | mg};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = as_u32(__builtin_elementwise_fma(as_h2(w[i]) + bias, d, -mn));
@@ -204,7 +213,6 @@ __device__ __forceinline__ void compute(const RawW<QT> &r, const _Float16 *sa, i
     const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, m_lo = S1 & 0x3F3F3F3Fu;
     const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
     const uint32_t m_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-    const h2 bias = splat(-1024.0f);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const uint32_t scw = p < 2 ? sc_lo : sc_hi, mw = p < 2 ? m_lo : m_hi;
@@ -215,10 +223,10 @@ __device__ __forceinline__ void compute(const RawW<QT> &r, const _Float16 *sa, i
       const h2 n1 = splat(dmin * static_cast<float>((mw >> (sh + 8)) & 0xFFu));
       const u32x4 q = r.qs[p];
       const int b0 = 64 * p + e0, b1 = 64 * p + 32 + e0;  // value offsets of the two sub-blocks
-      acc0 = mfma(act(sa, b0), op_q4(q.x, q.y, 0, bias, d0, n0), acc0);
-      acc1 = mfma(act(sa, b0 + 8), op_q4(q.z, q.w, 0, bias, d0, n0), acc1);
-      acc0 = mfma(act(sa, b1), op_q4(q.x, q.y, 4, bias, d1, n1), acc0);
-      acc1 = mfma(act(sa, b1 + 8), op_q4(q.z, q.w, 4, bias, d1, n1), acc1);
+      acc0 = mfma(act(sa, b0), op_q4<0>(q.x, q.y, d0, n0), acc0);
+      acc1 = mfma(act(sa, b0 + 8), op_q4<0>(q.z, q.w, d0, n0), acc1);
+      acc0 = mfma(act(sa, b1), op_q4<1>(q.x, q.y, d1, n1), acc0);
+      acc1 = mfma(act(sa, b1 + 8), op_q4<1>(q.z, q.w, d1, n1), acc1);
     }
   } else if constexpr (QT == kTypeQ6_K) {
     // dequant_q6k_element (quant_common.cuh:161-177): chunk c = (g, hf)

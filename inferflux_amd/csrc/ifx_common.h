@@ -111,6 +111,16 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// A constant in a VGPR, opaque to constant folding.  gfx950's VOP3
+// encodings take no literal, so a mask-and-insert against a literal
+// (x & mask) | magic compiles to v_and + v_or; with the magic in a register
+// it is one v_and_or_b32 (the mask goes to an SGPR).
+__device__ __forceinline__ uint32_t vreg(uint32_t c) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   _Float16 h;
   uint16_t b = static_cast<uint16_t>(bits16);
