@@ -124,6 +124,23 @@ struct GemvArgs {
   float eps;
 };
 
+// The segment of workgroup bx.  All segments' fields are read at once and
+// selected: an indexed read (args.seg[si]) waits for the index, one more
+// dependent scalar-memory round trip before the first weight load can
+// issue, in every wave of the launch.
+__device__ __forceinline__ GemvSeg pick_seg(const GemvArgs &a, int bx) {
+  const GemvSeg s0 = a.seg[0], s1 = a.seg[1], s2 = a.seg[2];
+  const bool in2 = a.nseg > 2 && bx >= s2.blk_begin;
+  const bool in1 = !in2 && a.nseg > 1 && bx >= s1.blk_begin;
+  GemvSeg g;
+  g.W = in2 ? s2.W : in1 ? s1.W : s0.W;
+  g.Y = in2 ? s2.Y : in1 ? s1.Y : s0.Y;
+  g.bias = in2 ? s2.bias : in1 ? s1.bias : s0.bias;
+  g.N = in2 ? s2.N : in1 ? s1.N : s0.N;
+  g.blk_begin = in2 ? s2.blk_begin : in1 ? s1.blk_begin : s0.blk_begin;
+  return g;
+}
+
 // Q4_K with MC <= 2 and Q6_K with MC = 1 use the wide (64-value) slices
 // (Q6_K at MC = 2 is faster with 32-value slices: fewer registers).  H = 2 (half-wave
 // mode, wide slices, K <= 2048 so that one row needs at most 32 lanes):
@@ -150,9 +167,10 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   constexpr int SV = kWide<QT, MC> ? 64 : 32;       // values per slice
   __shared__ float red[(G > 1) ? P * G * V : 1];
   const int bx = blockIdx.x;
-  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
-                 : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
-  const GemvSeg &sg = args.seg[si];
+  const GemvSeg sg = pick_seg(args, bx);
+  // the activation pointer is needed by every lane; using it here keeps its
+  // kernel-argument load in the first batch rather than behind a branch
+  asm volatile("" ::"s"(args.A));
   const uint8_t *__restrict__ W = sg.W;
   const int N = sg.N, M = args.M, K = args.K, mode = args.mode;
   const int lane = threadIdx.x & 63;
