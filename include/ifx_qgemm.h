@@ -94,6 +94,34 @@ int ifx_rmsnorm_quantize_q8_1(const void *residual, int residual_dtype,
 int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void *q8_1, int M,
                                int K, void *stream);
 
+/* Per-row symmetric int8 activations, the input format of ifx_qgemv_packed:
+ * per row, scale = max|x| / 127 (0 for a zero row), codes =
+ * clamp(rint(x / scale), -127, 127) evaluated as x * (1 / scale) in fp32.
+ * x [M][K] fp32, fp16 or bf16 (dtype IFX_OUT_F32, IFX_OUT_F16, IFX_IN_BF16);
+ * codes [M][K] int8, row_scales [M] fp32.  Replaces
+ * cuda_kernel::QuantizeRowsSymmetric (cuda_kernels.cu:309-369). */
+#define IFX_IN_BF16 2
+int ifx_quantize_rows_symmetric(const void *x, int dtype, int8_t *codes, float *row_scales, int M,
+                                int K, void *stream);
+
+/* Same of y = gate / (1 + exp(-gate)) * up.  Replaces
+ * cuda_kernel::SiluMulQuantizeRowsSymmetric (cuda_kernels.cu:371-437). */
+int ifx_silu_mul_quantize_rows_symmetric(const void *gate, const void *up, int dtype,
+                                         int8_t *codes, float *row_scales, int M, int K,
+                                         void *stream);
+
+/* GEMV on packed (per-row symmetric int8) activations, fp16 outputs:
+ * Y[i][m][n] = fp16(row_scales[m] * sum_k W[i][n][k] * codes[m][k]) for
+ * count = 1..3 projections of one quant type (Q4_K, Q6_K, Q8_K: K % 256 == 0;
+ * Q8_0: K % 32 == 0), any M >= 0.  Replaces FusedQuantGemm::GemvPacked,
+ * GemvPackedPair and GemvPackedTriple (fused_quant_gemm.h:79-107, .cu
+ * 1131-1231; kernels fused_dequant_gemv.cuh:80-580).  The reference applies
+ * the row scale inside every block; here once per output (results differ by
+ * fp32 rounding). */
+int ifx_qgemv_packed(int quant_type, int count, const void *const *W, void *const *Y,
+                     const int *N, const int8_t *codes, const float *row_scales, int M, int K,
+                     void *stream);
+
 /* Quantized GEMV/GEMM y[m][n] (op)= sum_k W[n][k] * a[m][k] for any M >= 1.
  * Replaces FusedQuantGemm::GemvQ8_1 / GemvQ8_1Accum / GemvQ8_1AccumF32 /
  * GemvQ8_1WithBias (fused_quant_gemm.h:171-173, 190-193, 202-205; .cu

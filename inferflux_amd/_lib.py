@@ -17,6 +17,9 @@ SIGNATURES = {
     "ifx_q8_1_quantize_f16": ([_vp, _vp, _i32, _i32, _vp], _i32),
     "ifx_rmsnorm_quantize_q8_1": ([_vp, _i32, _vp, _vp, _i32, _i32, ctypes.c_float, _vp], _i32),
     "ifx_silu_mul_quantize_q8_1": ([_vp, _vp, _i32, _vp, _i32, _i32, _vp], _i32),
+    "ifx_quantize_rows_symmetric": ([_vp, _i32, _vp, _vp, _i32, _i32, _vp], _i32),
+    "ifx_silu_mul_quantize_rows_symmetric": ([_vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp], _i32),
+    "ifx_qgemv_packed": ([_i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp], _i32),
     "ifx_qgemv": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemv_grouped": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemv_grouped_rmsnorm": ([_i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, ctypes.c_float, _i32, _i32, _i32, _i32, _vp], _i32),

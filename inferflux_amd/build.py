@@ -22,7 +22,7 @@ COMMON = [
 ]
 # Bit-exact kernels: no fp contraction anywhere in these translation units.
 EXACT = {"quantize.hip", "dequant.hip"}
-SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "mmvq.hip", "gemm_mfma.hip", "gemv_lds.hip", "gemv_slot.hip", "gemm_f16.hip", "gemv_dq.hip", "layer.hip",
+SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "mmvq.hip", "gemm_mfma.hip", "gemv_lds.hip", "gemv_slot.hip", "gemm_f16.hip", "gemv_dq.hip", "layer.hip", "packed.hip",
            "../host/fused_quant_gemm.cpp", "../host/gguf.cpp", "../host/gguf_model.cpp"]
 
 

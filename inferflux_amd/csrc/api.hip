@@ -77,6 +77,12 @@ hipError_t launch_gemv_slot(int qtype, int count, const void *const *W, void *co
                             const int *N, const void *bias, const void *A, bool f16, int M, int K,
                             int mode, hipStream_t stream, void *ws = nullptr);
 int64_t gemv_slot_workspace_bytes(int count, const int *N, bool f16, int M, int K);
+hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int8_t *codes,
+                                    float *scales, int M, int K, hipStream_t stream);
+bool gemv_packed_fits(int qtype, int K);
+hipError_t launch_gemv_packed(int qtype, int count, const void *const *W, void *const *Y,
+                              const int *N, const int8_t *X, const float *scales, int M, int K,
+                              hipStream_t stream);
 }  // namespace ifx
 
 // ---------------------------------------------------------------- launch log
@@ -509,6 +515,45 @@ int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void
   if (M < 0 || K < 0 || K % 32) return IFX_BAD_GEOMETRY;
   return status_of(ifx::launch_silu_mul_quantize_q8_1(gate, up, dtype == IFX_OUT_F16, q8_1, M, K,
                                                       static_cast<hipStream_t>(stream)));
+}
+
+int ifx_quantize_rows_symmetric(const void *x, int dtype, int8_t *codes, float *row_scales, int M,
+                                int K, void *stream) {
+  if (!x || !codes || !row_scales) return IFX_NULL_POINTER;
+  if (dtype != IFX_OUT_F32 && dtype != IFX_OUT_F16 && dtype != IFX_IN_BF16) return IFX_BAD_GEOMETRY;
+  if (M < 0 || K <= 0) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_quantize_rows_sym(x, nullptr, dtype, codes, row_scales, M, K,
+                                                 static_cast<hipStream_t>(stream)));
+}
+
+int ifx_silu_mul_quantize_rows_symmetric(const void *gate, const void *up, int dtype,
+                                         int8_t *codes, float *row_scales, int M, int K,
+                                         void *stream) {
+  if (!gate || !up || !codes || !row_scales) return IFX_NULL_POINTER;
+  if (dtype != IFX_OUT_F32 && dtype != IFX_OUT_F16 && dtype != IFX_IN_BF16) return IFX_BAD_GEOMETRY;
+  if (M < 0 || K <= 0) return IFX_BAD_GEOMETRY;
+  return status_of(ifx::launch_quantize_rows_sym(gate, up, dtype, codes, row_scales, M, K,
+                                                 static_cast<hipStream_t>(stream)));
+}
+
+int ifx_qgemv_packed(int quant_type, int count, const void *const *W, void *const *Y,
+                     const int *N, const int8_t *codes, const float *row_scales, int M, int K,
+                     void *stream) {
+  if (quant_type != IFX_TYPE_Q4_K && quant_type != IFX_TYPE_Q6_K && quant_type != IFX_TYPE_Q8_0 &&
+      quant_type != IFX_TYPE_Q8_K)
+    return IFX_UNSUPPORTED_TYPE;
+  if (!W || !Y || !N || !codes || !row_scales) return IFX_NULL_POINTER;
+  if (count < 1 || count > 3 || M < 0 || !ifx::gemv_packed_fits(quant_type, K))
+    return IFX_BAD_GEOMETRY;
+  // 32-bit buffer ranges: each weight tensor and the activation rows
+  if (static_cast<int64_t>(M) * K >= (int64_t{1} << 32)) return IFX_BAD_GEOMETRY;
+  for (int i = 0; i < count; ++i) {
+    if (!W[i] || !Y[i]) return IFX_NULL_POINTER;
+    if (N[i] <= 0 || static_cast<int64_t>(N[i]) * ifx::row_bytes(quant_type, K) >= (int64_t{1} << 32))
+      return IFX_BAD_GEOMETRY;
+  }
+  return status_of(ifx::launch_gemv_packed(quant_type, count, W, Y, N, codes, row_scales, M, K,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,

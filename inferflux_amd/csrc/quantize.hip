@@ -93,6 +93,71 @@ __global__ __launch_bounds__(256) void k_silu_mul_quantize_q8_1(const void *__re
   quantize4_store(y.x, y.y, y.z, y.w, out + blk * kQ8_1Bytes, l);
 }
 
+// ---------------------------------------------------------------------------
+// Per-row symmetric int8 activations (the reference's packed-activation
+// producers, cuda_kernels.cu:309-437): per row, amax = max |y|,
+// scale = amax / 127 (0 for a zero row), inv = 1 / scale (0 likewise),
+// q = clamp(rint(y * inv), -127, 127), with y = x (QuantizeRowsSymmetric) or
+// y = (g / (1 + exp(-g))) * u (SiluMulQuantizeRowsSymmetric).  Inputs fp32,
+// fp16 or bf16 (DT 0 / 1 / 2).  One workgroup of 256 threads per row: amax
+// is order-independent, so codes and scale are bit-exact with a CPU
+// restatement for y = x (the SiLU form differs where exp differs by an ulp).
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float load_dt(const void *p, int64_t i) {
+  if constexpr (DT == 0) return static_cast<const float *>(p)[i];
+  else if constexpr (DT == 1) return h2f(static_cast<const uint16_t *>(p)[i]);
+  else return __builtin_bit_cast(float, static_cast<uint32_t>(static_cast<const uint16_t *>(p)[i]) << 16);
+}
+
+template <int DT, bool SILU>
+__device__ __forceinline__ float row_value(const void *a, const void *b, int64_t i) {
+  if constexpr (SILU) return silu_mul1(load_dt<DT>(a, i), load_dt<DT>(b, i));
+  else return load_dt<DT>(a, i);
+}
+
+template <int DT, bool SILU>
+__global__ __launch_bounds__(256) void k_quantize_rows_sym(const void *__restrict__ a,
+                                                           const void *__restrict__ b,
+                                                           int8_t *__restrict__ codes,
+                                                           float *__restrict__ scales, int K) {
+  __shared__ float wmax[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * K;
+  const int tid = threadIdx.x;
+  float mx = 0.0f;
+  for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(row_value<DT, SILU>(a, b, base + i)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float scale = amax > 0.0f ? amax / 127.0f : 0.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  if (tid == 0) scales[blockIdx.x] = scale;
+  for (int i = tid; i < K; i += 256) {
+    const float q = rintf(row_value<DT, SILU>(a, b, base + i) * inv);
+    codes[base + i] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(q, -127.0f), 127.0f)));
+  }
+}
+
+hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int8_t *codes,
+                                    float *scales, int M, int K, hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const dim3 grid(M), block(256);
+#define IFX_QRS(DT)                                                                         \
+  do {                                                                                      \
+    if (b) IFX_LAUNCH(k_quantize_rows_sym, (DT, true), grid, block, 0, stream, a, b, codes, \
+                      scales, K);                                                           \
+    else IFX_LAUNCH(k_quantize_rows_sym, (DT, false), grid, block, 0, stream, a, b, codes,  \
+                    scales, K);                                                             \
+  } while (0)
+  if (dtype == 0) IFX_QRS(0);
+  else if (dtype == 1) IFX_QRS(1);
+  else IFX_QRS(2);
+#undef IFX_QRS
+  return last_error();
+}
+
 hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t *w, void *out,
                                         int M, int K, float eps, hipStream_t stream) {
   if (M == 0) return hipSuccess;

@@ -114,6 +114,68 @@ def silu_mul_quantize_q8_1(gate, up, out=None, stream=None):
     return out
 
 
+IN_BF16 = 2  # the row-symmetric quantizers also take bf16 input
+
+
+def _rows_dtype(t):
+    return {torch.float32: OUT_F32, torch.float16: OUT_F16, torch.bfloat16: IN_BF16}[t.dtype]
+
+
+def quantize_rows_symmetric(x, codes=None, scales=None, stream=None):
+    """Per-row symmetric int8 codes and fp32 row scales of x [M, K]
+    (fp32 / fp16 / bf16): the packed-activation format of qgemv_packed."""
+    M, K = x.shape
+    if codes is None:
+        codes = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if scales is None:
+        scales = torch.empty(M, dtype=torch.float32, device=x.device)
+    rc = _lib.load().ifx_quantize_rows_symmetric(_dev(x, "x"), _rows_dtype(x), _dev(codes, "codes"),
+                                                 _dev(scales, "scales"), M, K, _stream(stream))
+    _check(rc, "ifx_quantize_rows_symmetric")
+    return codes, scales
+
+
+def silu_mul_quantize_rows_symmetric(gate, up, codes=None, scales=None, stream=None):
+    """quantize_rows_symmetric of SiLU(gate) * up."""
+    M, K = gate.shape
+    if up.shape != gate.shape or up.dtype != gate.dtype:
+        raise ValueError("gate and up must match")
+    if codes is None:
+        codes = torch.empty((M, K), dtype=torch.int8, device=gate.device)
+    if scales is None:
+        scales = torch.empty(M, dtype=torch.float32, device=gate.device)
+    rc = _lib.load().ifx_silu_mul_quantize_rows_symmetric(
+        _dev(gate, "gate"), _dev(up, "up"), _rows_dtype(gate), _dev(codes, "codes"),
+        _dev(scales, "scales"), M, K, _stream(stream))
+    _check(rc, "ifx_silu_mul_quantize_rows_symmetric")
+    return codes, scales
+
+
+def qgemv_packed(qtype, Ws, codes, scales, M, Ns, K, outs=None, stream=None):
+    """fp16 [M, N_i] = row_scale * (W_i . codes) for 1..3 projections of raw
+    GGUF weights over packed (per-row symmetric int8) activations."""
+    import ctypes
+    count = len(Ws)
+    if not 1 <= count <= 3 or len(Ns) != count:
+        raise ValueError("1..3 projections with one N each")
+    if outs is None:
+        outs = [torch.empty((M, n), dtype=torch.float16, device=codes.device) for n in Ns]
+    for W, n, out in zip(Ws, Ns, outs):
+        if W.numel() < weight_bytes(qtype, n, K):
+            raise ValueError("W is smaller than N x K blocks")
+        if out.numel() < M * n or out.dtype != torch.float16:
+            raise ValueError("bad output tensor")
+    if codes.numel() < M * K or codes.dtype != torch.int8 or scales.numel() < M:
+        raise ValueError("codes / scales smaller than M x K / M")
+    wp = (ctypes.c_void_p * count)(*[_dev(w, "W") for w in Ws])
+    yp = (ctypes.c_void_p * count)(*[_dev(y, "out") for y in outs])
+    nn = (ctypes.c_int * count)(*Ns)
+    rc = _lib.load().ifx_qgemv_packed(qtype, count, wp, yp, nn, _dev(codes, "codes"),
+                                      _dev(scales, "scales"), M, K, _stream(stream))
+    _check(rc, "ifx_qgemv_packed")
+    return outs
+
+
 def qgemv(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE, bias=None,
           stream=None, prefill=False, workspace=None):
     """y [M, N] (op)= W . a with raw GGUF W and Q8_1 A (all device tensors).

@@ -25,6 +25,12 @@
  *   gemv_exact (fp64)      brute-force numpy dot over the dequantized
  *                          matrix; linearity; zero inputs
  *   gemv_q8_1 (fp32)       against gemv_exact within 1e-3*||y_row||
+ *   quantize_rows_symmetric KATs (ties to even, clamp, zero row, amax code
+ *                          127), the round-trip bound |x - q*scale| <=
+ *                          scale/2, sign symmetry
+ *   gemv_packed_exact      equal to gemv_exact on the same values written
+ *                          as Q8_1 blocks (power-of-two row scales make both
+ *                          formats exact); closed form for constant rows
  *   ggml_cpu_gemv          against gemv_exact within 1e-2*||y_row|| (its
  *                          activation format is Q8_K/Q8_0, not Q8_1).  The
  *                          ggml source is absent from the reference snapshot
@@ -463,6 +469,93 @@ int orc_gemv_exact(int qtype, const void *W, const void *A, double *y, int M, in
   if (check_geom(qtype, M, N, K)) return 1;
   orc_job job = {qtype, M, N, K, 0, 1, (const uint8_t *)W, (const uint8_t *)A, y, NULL};
   run_jobs(&job, threads, gemv_exact_worker);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Packed (per-row symmetric int8) activations.                               */
+/* Quantizer: native/cuda_kernels.cu:309-369 (QuantizeRowsSymmetricKernel):   */
+/*   amax = max|x| over the row; scale = amax > 0 ? amax / 127 : 0;           */
+/*   inv = scale > 0 ? 1 / scale : 0; q = clamp(rint(x * inv), -127, 127),    */
+/*   all in fp32; SiLU form (:371-437) on y = silu(g) * u as                  */
+/*   orc_silu_mul_values computes it.                                         */
+/* GEMV: native/kernels/fused_dequant_gemv.cuh:80-580 (the *_dp4a_packed      */
+/*   kernels): y[m][n] = scale[m] * sum_k w[n][k] * q[m][k], here in fp64     */
+/*   from the exact dequantized row (dequant_row_f64) and the exact codes.    */
+/* ------------------------------------------------------------------------ */
+static void quantize_row_sym(const float *y, int8_t *codes, float *scale, int64_t K) {
+  float amax = 0.0f;
+  for (int64_t i = 0; i < K; ++i) amax = fmaxf(amax, fabsf(y[i]));
+  const float sc = amax > 0.0f ? amax / 127.0f : 0.0f;
+  const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+  *scale = sc;
+  for (int64_t i = 0; i < K; ++i) {
+    const float t = y[i] * inv;
+    float q = rintf(t);
+    if (q > 127.0f) q = 127.0f;
+    if (q < -127.0f) q = -127.0f;
+    codes[i] = (int8_t)q;
+  }
+}
+
+int orc_quantize_rows_symmetric(const float *x, int8_t *codes, float *scales, int64_t M, int64_t K) {
+  if (M < 0 || K <= 0) return 1;
+  for (int64_t m = 0; m < M; ++m) quantize_row_sym(x + m * K, codes + m * K, scales + m, K);
+  return 0;
+}
+
+int orc_silu_mul_quantize_rows_symmetric(const float *g, const float *u, int8_t *codes,
+                                         float *scales, int64_t M, int64_t K) {
+  if (M < 0 || K <= 0) return 1;
+  float *y = (float *)malloc(sizeof(float) * (size_t)K);
+  if (!y) return 2;
+  for (int64_t m = 0; m < M; ++m) {
+    orc_silu_mul_values(g + m * K, u + m * K, y, K);
+    quantize_row_sym(y, codes + m * K, scales + m, K);
+  }
+  free(y);
+  return 0;
+}
+
+typedef struct {
+  int qtype, M, N, K, t, nt;
+  const uint8_t *W;
+  const int8_t *X;
+  const float *scales;
+  double *y;
+} orc_packed_job;
+
+static void *gemv_packed_worker(void *arg) {
+  orc_packed_job *j = (orc_packed_job *)arg;
+  const int64_t row_bytes = (int64_t)j->K / orc_block_elems(j->qtype) * orc_block_bytes(j->qtype);
+  double *w = (double *)malloc(sizeof(double) * j->K);
+  for (int n = j->t; n < j->N; n += j->nt) {
+    dequant_row_f64(j->qtype, j->W + n * row_bytes, w, j->K);
+    for (int m = 0; m < j->M; ++m) {
+      const int8_t *xm = j->X + (int64_t)m * j->K;
+      double s = 0.0;
+      for (int k = 0; k < j->K; ++k) s += w[k] * xm[k];
+      j->y[(int64_t)m * j->N + n] = s * (double)j->scales[m];
+    }
+  }
+  free(w);
+  return NULL;
+}
+
+/* y is [M][N] fp64; codes [M][K] int8; scales [M] fp32. */
+int orc_gemv_packed_exact(int qtype, const void *W, const int8_t *codes, const float *scales,
+                          double *y, int M, int N, int K, int threads) {
+  if (check_geom(qtype, M, N, K)) return 1;
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  pthread_t th[256];
+  orc_packed_job jobs[256];
+  for (int t = 0; t < threads; ++t) {
+    orc_packed_job jb = {qtype, M, N, K, t, threads, (const uint8_t *)W, codes, scales, y};
+    jobs[t] = jb;
+    pthread_create(&th[t], NULL, gemv_packed_worker, &jobs[t]);
+  }
+  for (int t = 0; t < threads; ++t) pthread_join(th[t], NULL);
   return 0;
 }
 

@@ -51,6 +51,9 @@ def lib():
         L.orc_gemv_exact.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
         L.orc_gemv_q8_1.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
         L.orc_ggml_cpu_gemv.argtypes = [i32, vp, vp, vp, i32, i32, i32, i32]
+        L.orc_quantize_rows_symmetric.argtypes = [vp, vp, vp, i64, i64]
+        L.orc_silu_mul_quantize_rows_symmetric.argtypes = [vp, vp, vp, vp, i64, i64]
+        L.orc_gemv_packed_exact.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32]
         _lib = L
     return _lib
 
@@ -185,6 +188,38 @@ def ggml_cpu_gemv(qtype, w_bytes, x, N, threads=0):
     M, K = x.shape
     y = np.empty((M, N), np.float32)
     if lib().orc_ggml_cpu_gemv(qtype, _p(w), _p(x), _p(y), M, N, K, _threads(threads)):
+        raise ValueError("unsupported geometry")
+    return y
+
+
+def quantize_rows_symmetric(x):
+    """(int8 codes [M][K], fp32 scales [M]) of fp32 x [M][K]."""
+    x = _f32(x)
+    M, K = x.shape
+    codes = np.empty((M, K), np.int8)
+    scales = np.empty(M, np.float32)
+    if lib().orc_quantize_rows_symmetric(_p(x), _p(codes), _p(scales), M, K):
+        raise ValueError("bad shape")
+    return codes, scales
+
+
+def silu_mul_quantize_rows_symmetric(g, u):
+    g, u = _f32(g), _f32(u)
+    M, K = g.shape
+    codes = np.empty((M, K), np.int8)
+    scales = np.empty(M, np.float32)
+    if lib().orc_silu_mul_quantize_rows_symmetric(_p(g), _p(u), _p(codes), _p(scales), M, K):
+        raise ValueError("bad shape")
+    return codes, scales
+
+
+def gemv_packed_exact(qtype, w_bytes, codes, scales, M, N, K, threads=0):
+    """fp64 y[M][N] = scale[m] * (exact dequantized W . int8 codes)."""
+    w = np.ascontiguousarray(w_bytes, dtype=np.uint8)
+    c = np.ascontiguousarray(codes, dtype=np.int8)
+    s = np.ascontiguousarray(scales, dtype=np.float32)
+    y = np.empty((M, N), np.float64)
+    if lib().orc_gemv_packed_exact(qtype, _p(w), _p(c), _p(s), _p(y), M, N, K, _threads(threads)):
         raise ValueError("unsupported geometry")
     return y
 

@@ -97,6 +97,34 @@ def test_validation_without_launch(lib):
     assert lib.ifx_status_string(3) == b"null pointer"
 
 
+def test_packed_validation_without_launch(lib):
+    """The packed-activation entries reject bad calls before any HIP call:
+    types outside Q4_K / Q6_K / Q8_0 / Q8_K, K off the block size, 0 or 4
+    projections, NULL pointers, unknown input dtypes."""
+    fake = ctypes.c_void_p(0x1000)
+    W = (ctypes.c_void_p * 3)(fake, fake, fake)
+    Y = (ctypes.c_void_p * 3)(fake, fake, fake)
+    N = (ctypes.c_int * 3)(16, 16, 16)
+    packed = lib.ifx_qgemv_packed
+    assert packed(13, 1, W, Y, N, fake, fake, 1, 256, None) == 1  # Q5_K: no packed kernel
+    assert packed(9, 1, W, Y, N, fake, fake, 1, 256, None) == 1
+    assert packed(12, 1, W, Y, N, fake, fake, 1, 250, None) == 2
+    assert packed(8, 1, W, Y, N, fake, fake, 1, 48, None) == 2
+    assert packed(12, 0, W, Y, N, fake, fake, 1, 256, None) == 2
+    assert packed(12, 4, W, Y, N, fake, fake, 1, 256, None) == 2
+    assert packed(12, 1, W, Y, N, None, fake, 1, 256, None) == 3
+    assert packed(12, 1, W, Y, N, fake, None, 1, 256, None) == 3
+    Wn = (ctypes.c_void_p * 3)(fake, None, fake)
+    assert packed(12, 2, Wn, Y, N, fake, fake, 1, 256, None) == 3
+    Nz = (ctypes.c_int * 3)(16, 0, 16)
+    assert packed(12, 2, W, Y, Nz, fake, fake, 1, 256, None) == 2
+    assert packed(12, 1, W, Y, N, fake, fake, -1, 256, None) == 2
+    assert lib.ifx_quantize_rows_symmetric(None, 0, fake, fake, 1, 8, None) == 3
+    assert lib.ifx_quantize_rows_symmetric(fake, 3, fake, fake, 1, 8, None) == 2
+    assert lib.ifx_quantize_rows_symmetric(fake, 0, fake, fake, 1, 0, None) == 2
+    assert lib.ifx_silu_mul_quantize_rows_symmetric(fake, None, 1, fake, fake, 1, 8, None) == 3
+
+
 def test_product_fails_loudly_without_library(monkeypatch):
     from inferflux_amd import _lib
     monkeypatch.setattr(_lib, "_lib", None)

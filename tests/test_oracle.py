@@ -384,3 +384,86 @@ def test_silu_mul_values_vs_fp64(orc):
     # silu(0) = 0; silu(g) = g in fp32 once exp(-g) < 2^-24
     z = orc.silu_mul_values(np.array([0.0, 20.0, 30.0], np.float32), np.array([5.0, 3.0, -2.0], np.float32))
     assert np.array_equal(z, np.array([0.0, 60.0, -60.0], np.float32))
+
+
+# ------------------------------------------- packed (row-symmetric) activations
+def test_quantize_rows_symmetric_reference_kat(orc):
+    """The reference's contract test (tests/unit/test_native_forward.cpp:
+    7181-7238): two rows of four, scales 4/127 and 3/127, -2 and 1.5 land on
+    the tie 63.5 and round to even."""
+    x = np.array([[-4.0, -2.0, 0.0, 4.0], [0.0, 1.5, -1.5, 3.0]], np.float32)
+    codes, scales = orc.quantize_rows_symmetric(x)
+    assert codes.tolist() == [[-127, -64, 0, 127], [0, 64, -64, 127]]
+    assert scales[0] == np.float32(4.0) / np.float32(127.0)
+    assert scales[1] == np.float32(3.0) / np.float32(127.0)
+
+
+def test_quantize_rows_symmetric_ties_zero_and_clamp(orc):
+    # amax 127 -> scale 1 exactly: codes are rint(x), ties to even
+    x = np.array([[127.0, 63.5, 62.5, -0.5, 0.49, -126.5, 1.5, 2.5]], np.float32)
+    codes, scales = orc.quantize_rows_symmetric(x)
+    assert scales[0] == 1.0
+    assert codes.tolist() == [[127, 64, 62, 0, 0, -126, 2, 2]]
+    codes, scales = orc.quantize_rows_symmetric(np.zeros((2, 64), np.float32))
+    assert scales.tolist() == [0.0, 0.0] and not codes.any()
+
+
+def test_quantize_rows_symmetric_properties(orc):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((16, 1000)) * rng.uniform(1e-3, 1e3, (16, 1))).astype(np.float32)
+    codes, scales = orc.quantize_rows_symmetric(x)
+    amax = np.abs(x).max(axis=1)
+    assert np.array_equal(scales, (amax / np.float32(127)).astype(np.float32))
+    # the largest magnitude maps to +-127; every code is within half a step
+    idx = np.abs(x).argmax(axis=1)
+    assert np.array_equal(np.abs(codes[np.arange(16), idx]), np.full(16, 127))
+    err = np.abs(x.astype(np.float64) - codes * scales[:, None].astype(np.float64))
+    assert np.all(err <= 0.5 * scales[:, None] * (1 + 1e-6))
+    # sign symmetry
+    c2, s2 = orc.quantize_rows_symmetric(-x)
+    assert np.array_equal(c2, -codes) and np.array_equal(s2, scales)
+
+
+def test_silu_mul_quantize_rows_symmetric_reference_kat(orc):
+    """The reference's SwiGLU quantization test (test_native_forward.cpp:
+    7634-7700): codes lrint(y / scale) with scale = max|y| / 127."""
+    g = np.array([[-1.0, 0.0, 1.0, 2.0, -2.0, 0.5, -0.5, 3.0]], np.float32)
+    u = np.array([[1.0, 1.0, 1.0, 1.0, 0.5, 2.0, 4.0, 1.0]], np.float32)
+    codes, scales = orc.silu_mul_quantize_rows_symmetric(g, u)
+    assert codes.tolist() == [[-12, 0, 32, 78, -5, 28, -34, 127]]
+    y = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert abs(scales[0] - np.abs(y).max() / 127) <= 1e-7
+
+
+@pytest.mark.parametrize("qtype,K", [(Q4_K, 512), (Q6_K, 768), (Q8_0, 160), (Q8_K, 512)])
+def test_gemv_packed_equals_q8_1_gemv(orc, qtype, K):
+    """With a power-of-two row scale both activation formats hold the same
+    values exactly (Q8_1 blocks with d = scale and the same codes), so the
+    packed GEMV equals the pinned Q8_1 GEMV up to fp64 summation order."""
+    from inferflux_amd import synth
+    M, N = 3, 40
+    rng = np.random.default_rng(K)
+    codes = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    scales = np.array([2.0**-4, 2.0**-7, 1.0], np.float32)
+    a = np.zeros((M, K // 32, 36), np.uint8)
+    a[:, :, 0:2] = np.frombuffer(np.repeat(scales.astype(np.float16), K // 32).tobytes(),
+                                 np.uint8).reshape(M, K // 32, 2)
+    a[:, :, 4:36] = codes.reshape(M, K // 32, 32).view(np.uint8)
+    w = synth.blocks(qtype, N, K, seed=K + 1)
+    y_packed = orc.gemv_packed_exact(qtype, w, codes, scales, M, N, K)
+    y_q8_1 = orc.gemv_exact(qtype, w, a.reshape(M, -1), M, N, K)
+    assert np.allclose(y_packed, y_q8_1, rtol=1e-12, atol=1e-12 * np.abs(y_q8_1).max())
+
+
+def test_gemv_packed_closed_form(orc):
+    """Q8_0 rows of code 1 with d = 1: y = scale * sum(codes)."""
+    M, N, K = 2, 3, 64
+    w = np.zeros((N * K // 32, 34), np.uint8)
+    w[:, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    w[:, 2:34] = 1
+    rng = np.random.default_rng(3)
+    codes = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    scales = np.array([0.5, 3.0], np.float32)
+    y = orc.gemv_packed_exact(Q8_0, w, codes, scales, M, N, K)
+    want = scales[:, None] * codes.sum(axis=1, dtype=np.int64)[:, None]
+    assert np.array_equal(y, np.repeat(want, N, axis=1).astype(np.float64))
