@@ -31,6 +31,13 @@ struct QuantizedWeightInfo {
   int64_t num_elements{0};
 };
 
+// Packed activations (fused_quant_gemm.h:16-19): per-row symmetric int8
+// codes [M][K] and one fp32 scale per row (QuantizeRowsSymmetric).
+struct PackedActivationInfo {
+  const int8_t *data{nullptr};
+  const float *row_scales{nullptr};
+};
+
 // One output of a grouped launch (fused_quant_gemm.h:22-26); `output` is fp16.
 struct PackedProjectionSpec {
   QuantizedWeightInfo weight;
@@ -141,6 +148,29 @@ class FusedQuantGemm {
                                                   const void *act_q8_1, uint16_t *output,
                                                   void *act_q8_1_out, int M, int N, int K,
                                                   hipStream_t stream);
+
+  // fused_quant_gemm.h:72-107: the GEMV on packed (per-row symmetric int8)
+  // activations, fp16 out; Q4_K, Q6_K, Q8_0, Q8_K (SupportsPackedActivations).
+  // False (nothing launched) for other types, bad geometry or a disabled
+  // policy, as the reference.
+  static bool GemvPacked(const QuantizedWeightInfo &weight, const PackedActivationInfo &activation,
+                         uint16_t *output, int M, int N, int K, hipStream_t stream,
+                         const NativeExecutionPolicy *policy = nullptr);
+  static bool GemvPackedPair(const std::array<PackedProjectionSpec, 2> &projections,
+                             const PackedActivationInfo &activation, int M, int K,
+                             hipStream_t stream);
+  static bool GemvPackedTriple(const std::array<PackedProjectionSpec, 3> &projections,
+                               const PackedActivationInfo &activation, int M, int K,
+                               hipStream_t stream);
+  // fused_quant_gemm.cu:925-928: the types with a packed-activation kernel.
+  static bool SupportsPackedActivations(int quant_type);
+  // cuda_kernel::QuantizeRowsSymmetric / SiluMulQuantizeRowsSymmetric
+  // (cuda_kernels.cu:309-437), fp16 input: the packed activations.
+  static bool QuantizeRowsSymmetric(const uint16_t *input, int8_t *output, float *row_scales,
+                                    int rows, int cols, hipStream_t stream);
+  static bool SiluMulQuantizeRowsSymmetric(const uint16_t *gate, const uint16_t *up,
+                                           int8_t *output, float *row_scales, int rows, int cols,
+                                           hipStream_t stream);
 
   // fused_quant_gemm.h:333: Q4_K, Q6_K, Q8_0 and Q8_K as the reference,
   // and Q5_K, for which the reference has no fused kernel.

@@ -189,6 +189,71 @@ bool FusedQuantGemm::FusedGateUpSiluGemvQ8_1WithEpilogue(const QuantizedWeightIn
                                 IFX_OUT_F16, act_q8_1_out, M, N, K, stream) == IFX_OK;
 }
 
+namespace {
+
+template <size_t C>
+bool LaunchPacked(const std::array<PackedProjectionSpec, C> &p, const PackedActivationInfo &act,
+                  int M, int K, hipStream_t stream, const NativeExecutionPolicy *policy) {
+  if (!act.data || !act.row_scales || M <= 0 || Resolve(policy).disable_fused_gemv) return false;
+  if (!FusedQuantGemm::SupportsPackedActivations(p[0].weight.quant_type)) return false;
+  const void *W[C];
+  void *Y[C];
+  int N[C];
+  for (size_t i = 0; i < C; ++i) {
+    if (!Usable(p[i].weight, act.data, p[i].output) || p[i].output_cols <= 0) return false;
+    if (p[i].weight.quant_type != p[0].weight.quant_type) return false;
+    if (!ViewCovers(p[i].weight, p[i].output_cols, K)) return false;
+    W[i] = p[i].weight.data;
+    Y[i] = p[i].output;
+    N[i] = p[i].output_cols;
+  }
+  return ifx_qgemv_packed(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act.data,
+                          act.row_scales, M, K, stream) == IFX_OK;
+}
+
+}  // namespace
+
+bool FusedQuantGemm::GemvPacked(const QuantizedWeightInfo &weight,
+                                const PackedActivationInfo &activation, uint16_t *output, int M,
+                                int N, int K, hipStream_t stream,
+                                const NativeExecutionPolicy *policy) {
+  const std::array<PackedProjectionSpec, 1> p{PackedProjectionSpec{weight, output, N}};
+  return LaunchPacked(p, activation, M, K, stream, policy);
+}
+
+bool FusedQuantGemm::GemvPackedPair(const std::array<PackedProjectionSpec, 2> &projections,
+                                    const PackedActivationInfo &activation, int M, int K,
+                                    hipStream_t stream) {
+  return LaunchPacked(projections, activation, M, K, stream, nullptr);
+}
+
+bool FusedQuantGemm::GemvPackedTriple(const std::array<PackedProjectionSpec, 3> &projections,
+                                      const PackedActivationInfo &activation, int M, int K,
+                                      hipStream_t stream) {
+  return LaunchPacked(projections, activation, M, K, stream, nullptr);
+}
+
+bool FusedQuantGemm::SupportsPackedActivations(int quant_type) {
+  return quant_type == static_cast<int>(TensorType::Q4_K) ||
+         quant_type == static_cast<int>(TensorType::Q6_K) ||
+         quant_type == static_cast<int>(TensorType::Q8_0) ||
+         quant_type == static_cast<int>(TensorType::Q8_K);
+}
+
+bool FusedQuantGemm::QuantizeRowsSymmetric(const uint16_t *input, int8_t *output,
+                                           float *row_scales, int rows, int cols,
+                                           hipStream_t stream) {
+  return ifx_quantize_rows_symmetric(input, IFX_OUT_F16, output, row_scales, rows, cols,
+                                     stream) == IFX_OK;
+}
+
+bool FusedQuantGemm::SiluMulQuantizeRowsSymmetric(const uint16_t *gate, const uint16_t *up,
+                                                  int8_t *output, float *row_scales, int rows,
+                                                  int cols, hipStream_t stream) {
+  return ifx_silu_mul_quantize_rows_symmetric(gate, up, IFX_OUT_F16, output, row_scales, rows,
+                                              cols, stream) == IFX_OK;
+}
+
 bool FusedQuantGemm::SupportsQ8_1Activations(int quant_type) {
   return quant_type == static_cast<int>(TensorType::Q4_K) ||
          quant_type == static_cast<int>(TensorType::Q5_K) ||

@@ -32,12 +32,16 @@ int orc_rmsnorm_quantize_q8_1(const float *x, const uint16_t *w, void *out, int6
 int orc_silu_mul_quantize_q8_1(const float *g, const float *u, void *out, int64_t M, int64_t K);
 int orc_gemv_exact(int qtype, const void *W, const void *A, double *y, int M, int N, int K,
                    int threads);
+int orc_quantize_rows_symmetric(const float *x, int8_t *codes, float *scales, int64_t M, int64_t K);
+int orc_gemv_packed_exact(int qtype, const void *W, const int8_t *codes, const float *scales,
+                          double *y, int M, int N, int K, int threads);
 }
 
 using inferflux::rocm::FusedDispatchGeometry;
 using inferflux::rocm::FusedQuantGemm;
 using inferflux::rocm::KernelFamily;
 using inferflux::rocm::NativeExecutionPolicy;
+using inferflux::rocm::PackedActivationInfo;
 using inferflux::rocm::PackedProjectionSpec;
 using inferflux::rocm::QuantizedWeightInfo;
 
@@ -245,6 +249,23 @@ void TestPolicy() {
   mixed[1].weight.quant_type = Q4_K;
   mixed[1].output = nullptr;
   EXPECT(!FusedQuantGemm::GemvQ8_1Pair(mixed, dummy, 1, 256, nullptr));
+  // packed activations: the reference's types only; a missing scale
+  // vector, a disabled policy or mixed types are not handled
+  EXPECT(FusedQuantGemm::SupportsPackedActivations(Q4_K));
+  EXPECT(FusedQuantGemm::SupportsPackedActivations(Q8_0));
+  EXPECT(!FusedQuantGemm::SupportsPackedActivations(13));
+  const auto *codes = reinterpret_cast<const int8_t *>(dummy);
+  const auto *scales = reinterpret_cast<const float *>(dummy);
+  const PackedActivationInfo pa{codes, scales};
+  EXPECT(!FusedQuantGemm::GemvPacked(QuantizedWeightInfo{dummy, 13, 256}, pa, dummy_out, 1, 1,
+                                     256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvPacked(w, PackedActivationInfo{codes, nullptr}, dummy_out, 1, 1,
+                                     256, nullptr));
+  EXPECT(!FusedQuantGemm::GemvPacked(w, pa, dummy_out, 1, 1, 100, nullptr));
+  EXPECT(!FusedQuantGemm::GemvPacked(w, pa, dummy_out, 1, 1, 256, nullptr, &off));
+  mixed[1].output = dummy_out;
+  mixed[1].weight.quant_type = Q6_K;
+  EXPECT(!FusedQuantGemm::GemvPackedPair(mixed, pa, 1, 256, nullptr));
 }
 
 // ------------------------------------------------------------------- gpu
@@ -393,6 +414,59 @@ void TestGrouped(int qtype, int M, int K, const std::array<int, C> &Ns) {
   }
 }
 
+// Packed activations: QuantizeRowsSymmetric on fp16 rows (bit-exact with
+// the oracle) feeding GemvPacked / Pair / Triple (fp16 out, oracle fp64).
+template <size_t C>
+void TestPacked(int qtype, int M, int K, const std::array<int, C> &Ns) {
+  std::printf("[gpu packed x%zu] qtype=%d M=%d K=%d\n", C, qtype, M, K);
+  std::fflush(stdout);
+  Rng r(7 + M + K);
+  std::vector<uint16_t> xh(static_cast<size_t>(M) * K);
+  std::vector<float> xf(xh.size());
+  for (size_t i = 0; i < xh.size(); ++i) {
+    xh[i] = orc_f32_to_f16(r.normal());
+    xf[i] = orc_f16_to_f32(xh[i]);
+  }
+  Dev dx(xh.size() * 2), dc(xh.size()), ds(static_cast<size_t>(M) * 4);
+  HIP_OK(hipMemcpy(dx.p, xh.data(), xh.size() * 2, hipMemcpyHostToDevice));
+  EXPECT(FusedQuantGemm::QuantizeRowsSymmetric(dx.as<uint16_t>(), dc.as<int8_t>(), ds.as<float>(),
+                                               M, K, nullptr));
+  HIP_OK(hipDeviceSynchronize());
+  std::vector<int8_t> c(xh.size()), ce(xh.size());
+  std::vector<float> sc(M), se(M);
+  HIP_OK(hipMemcpy(c.data(), dc.p, c.size(), hipMemcpyDeviceToHost));
+  HIP_OK(hipMemcpy(sc.data(), ds.p, sc.size() * 4, hipMemcpyDeviceToHost));
+  orc_quantize_rows_symmetric(xf.data(), ce.data(), se.data(), M, K);
+  EXPECT(c == ce);
+  EXPECT(std::memcmp(sc.data(), se.data(), sc.size() * 4) == 0);
+  std::vector<std::vector<uint8_t>> ws;
+  std::vector<std::unique_ptr<Dev>> dws, dys;
+  std::array<PackedProjectionSpec, C> spec{};
+  for (size_t i = 0; i < C; ++i) {
+    ws.push_back(MakeBlocks(qtype, Ns[i], K, 300 + i));
+    dws.emplace_back(new Dev(ws[i].size()));
+    dys.emplace_back(new Dev(static_cast<size_t>(M) * Ns[i] * 2));
+    HIP_OK(hipMemcpy(dws[i]->p, ws[i].data(), ws[i].size(), hipMemcpyHostToDevice));
+    spec[i] = PackedProjectionSpec{QuantizedWeightInfo{dws[i]->p, qtype, int64_t{Ns[i]} * K},
+                                   dys[i]->template as<uint16_t>(), Ns[i]};
+  }
+  const PackedActivationInfo act{dc.as<int8_t>(), ds.as<float>()};
+  bool ok;
+  if constexpr (C == 1)
+    ok = FusedQuantGemm::GemvPacked(spec[0].weight, act, spec[0].output, M, Ns[0], K, nullptr);
+  else if constexpr (C == 2) ok = FusedQuantGemm::GemvPackedPair(spec, act, M, K, nullptr);
+  else ok = FusedQuantGemm::GemvPackedTriple(spec, act, M, K, nullptr);
+  EXPECT(ok);
+  HIP_OK(hipDeviceSynchronize());
+  for (size_t i = 0; i < C; ++i) {
+    std::vector<double> ye(static_cast<size_t>(M) * Ns[i]);
+    orc_gemv_packed_exact(qtype, ws[i].data(), c.data(), sc.data(), ye.data(), M, Ns[i], K, 8);
+    std::vector<uint16_t> h(ye.size());
+    HIP_OK(hipMemcpy(h.data(), dys[i]->p, h.size() * 2, hipMemcpyDeviceToHost));
+    EXPECT(RowsClose(HalfToFloat(h), ye, M, Ns[i], 1e-3, true));
+  }
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -415,6 +489,11 @@ int main(int argc, char **argv) {
     TestGrouped<3>(Q4_K, 2, 1024, {128, 64, 65});
     TestGrouped<3>(Q6_K, 1, 512, {33, 1, 250});
     TestGrouped<2>(Q8_0, 4, 256, {70, 90});
+    TestPacked<1>(Q4_K, 1, 2048, {300});
+    TestPacked<2>(Q6_K, 2, 256, {8, 6});
+    TestPacked<3>(Q4_K, 2, 256, {8, 6, 4});
+    TestPacked<2>(Q8_0, 3, 1056, {70, 33});
+    TestPacked<1>(15, 2, 1024, {100});  // Q8_K
   } else {
     std::printf("usage: %s policy|gpu\n", argv[0]);
     return 2;
