@@ -197,8 +197,8 @@ __device__ __forceinline__ void packed_slice(rsrc_t Wr, uint32_t row_off, rsrc_t
 
 }  // namespace
 
-// H = 2: two rows per wave (32 lanes each, rows of at most 32 slices);
-// H = 1: one row per wave.
+// H = 2 / 4: two / four rows per wave (32 / 16 lanes each); H = 1: one row
+// per wave.
 template <int QT, int MC, int H>
 __global__ __launch_bounds__(64 * kWaves) void k_gemv_packed(const PackedArgs args) {
   constexpr int LPR = 64 / H;  // lanes per row
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_packed(const PackedArgs ar
   const bool in1 = !in2 && args.nseg > 1 && bx >= args.seg[1].blk_begin;
   const PackedSeg sg = in2 ? args.seg[2] : in1 ? args.seg[1] : args.seg[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int half = H == 2 ? lane >> 5 : 0, lt = lane & (LPR - 1);
+  const int half = lane / LPR, lt = lane & (LPR - 1);  // row of the wave, lane in it
   const int n = ((bx - sg.blk_begin) * kWaves + wave) * H + half;
   const int N = sg.N, M = args.M, K = args.K;
   const int col0 = blockIdx.y * MC;
@@ -227,7 +227,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_packed(const PackedArgs ar
 
   float tot[MC];
 #pragma unroll
-  for (int c = 0; c < MC; ++c) tot[c] = H == 2 ? halfwave_sum_to31(acc[c]) : wave_sum_to63(acc[c]);
+  for (int c = 0; c < MC; ++c)
+    tot[c] = H == 4 ? quarterwave_sum(acc[c]) : H == 2 ? halfwave_sum_to31(acc[c]) : wave_sum_to63(acc[c]);
   if (lt != LPR - 1 || n >= N) return;
 #pragma unroll
   for (int c = 0; c < MC; ++c)
@@ -240,32 +241,38 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_packed(const PackedArgs ar
 
 namespace {
 
+// Rows per wave: half-wave rows for at most 32 slices; quarter-wave rows
+// when 16 lanes leave none idle and a full wave would (K = 5120: 80 slices,
+// 5 per lane); else full-wave rows.
+int rows_per_wave(int nslice) {
+  if (nslice <= 32) return 2;
+  if (nslice % 16 == 0 && nslice % 64 != 0 && nslice <= 128) return 4;
+  return 1;
+}
+
 template <int QT, int MC>
-hipError_t launch_mc(const PackedArgs &args, int groups, hipStream_t s) {
-  const int nslice = args.K / slice_values<QT>();
-  const dim3 block(64 * kWaves);
-  if (nslice <= 32) {
-    const dim3 grid(groups, (args.M + MC - 1) / MC);
-    IFX_LAUNCH(k_gemv_packed, (QT, MC, 2), grid, block, 0, s, args);
-  } else {
-    const dim3 grid(groups, (args.M + MC - 1) / MC);
-    IFX_LAUNCH(k_gemv_packed, (QT, MC, 1), grid, block, 0, s, args);
-  }
+hipError_t launch_mc(const PackedArgs &args, int groups, int H, hipStream_t s) {
+  const dim3 block(64 * kWaves), grid(groups, (args.M + MC - 1) / MC);
+  if (H == 4) IFX_LAUNCH(k_gemv_packed, (QT, MC, 4), grid, block, 0, s, args);
+  else if (H == 2) IFX_LAUNCH(k_gemv_packed, (QT, MC, 2), grid, block, 0, s, args);
+  else IFX_LAUNCH(k_gemv_packed, (QT, MC, 1), grid, block, 0, s, args);
   return last_error();
 }
 
 template <int QT>
 hipError_t launch_qt(PackedArgs args, hipStream_t s) {
   // row groups: kWaves * H rows per workgroup
-  const int H = args.K / slice_values<QT>() <= 32 ? 2 : 1;
+  const int H = rows_per_wave(args.K / slice_values<QT>());
   int groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = groups;
     groups += (args.seg[i].N + kWaves * H - 1) / (kWaves * H);
   }
-  if (args.M >= 4) return launch_mc<QT, 4>(args, groups, s);
-  if (args.M >= 2) return launch_mc<QT, 2>(args, groups, s);
-  return launch_mc<QT, 1>(args, groups, s);
+  // batch rows per launch column: each weight byte is read ceil(M / MC) times
+  if (args.M >= 5) return launch_mc<QT, 8>(args, groups, H, s);
+  if (args.M >= 3) return launch_mc<QT, 4>(args, groups, H, s);
+  if (args.M == 2) return launch_mc<QT, 2>(args, groups, H, s);
+  return launch_mc<QT, 1>(args, groups, H, s);
 }
 
 }  // namespace

@@ -106,6 +106,10 @@ PACKED_CASES = [
     (Q8_0, 6, (333,), 1056),
     (Q8_K, 2, (500,), 1024),
     (Q8_K, 1, (64, 64, 64), 4096),
+    # quarter-wave rows (80 slices) and 8-row column groups
+    (Q4_K, 1, (13824, 13824), 5120),
+    (Q6_K, 8, (500,), 5120),
+    (Q4_K, 12, (300, 77), 2048),
 ]
 
 
