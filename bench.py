@@ -509,6 +509,23 @@ def main():
         gb = gemv_bytes(ops, qt, 8, [N], K) / us / 1e3
         c1["M8_tiled"] = {"us": round(us, 3), "GBs": round(gb, 1), "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
         del treps
+        # the packed-activation path (per-row symmetric int8 codes, fp16
+        # out) on the same weights; bytes: weights, M x K codes, M scales,
+        # fp16 outputs; and the row quantizer that produces the codes
+        for M in (1, 2):
+            x = torch.from_numpy(synth.activations(M, K, seed=0)).to(dev)
+            codes, scales = ops.quantize_rows_symmetric(x)
+            Yh = torch.empty((M, N), dtype=torch.float16, device=dev)
+            us = time_loop(lambda i: ops.qgemv_packed(qt, [reps[i % len(reps)]], codes, scales, M,
+                                                      [N], K, outs=[Yh]),
+                           max(args.steps, 200), args.warmup)
+            gb = (ops.weight_bytes(qt, N, K) + M * K + M * 4 + M * N * 2) / us / 1e3
+            c1[f"M{M}_packed"] = {"us": round(us, 3), "GBs": round(gb, 1),
+                                  "frac_hbm": round(gb / HBM_PEAK_GBS, 4)}
+            if M == 1:
+                c1["quantize_rows_symmetric_M1_us"] = round(
+                    time_loop(lambda i: ops.quantize_rows_symmetric(x, codes, scales), 200,
+                              args.warmup), 3)
         extras["config1_q4k_11008x2048"] = c1
         del reps, w
         torch.cuda.empty_cache()

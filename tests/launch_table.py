@@ -105,6 +105,12 @@ LAUNCHES = [
     ("c4t_o_m32", "gemv_accum_ws", Q4_K_T, 32, (5120,), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_gate_up_m32", "grouped_ws", Q4_K_T, 32, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_down_m32", "gemv_accum_ws", Q6_K_T, 32, (5120,), 13824, ["k_gemv_dq<14,0,2,1>"]),
+    # packed (per-row symmetric int8) activations at M = 1: config 1, the 3B
+    # QKV triple and down projection, the 14B gate/up pair
+    ("c1_packed_m1", "packed", Q4_K, 1, (11008,), 2048, ["k_gemv_packed<12,1,2>"]),
+    ("c2_qkv_packed_m1", "packed", Q4_K, 1, QKV3, 2048, ["k_gemv_packed<12,1,2>"]),
+    ("c2_down_packed_m1", "packed", Q6_K, 1, (2048,), 11008, ["k_gemv_packed<14,1,1>"]),
+    ("c4_gate_up_packed_m1", "packed", Q4_K, 1, (13824, 13824), 5120, ["k_gemv_packed<12,1,4>"]),
     # config 5: 32B prefill GEMMs at M = 512 (default dispatch, and the int8 kernel)
     ("c5_up", "prefill", Q4_K, 512, (27648,), 5120, ["k_gemm_f16<12,8,0,0,0>"]),
     ("c5_down", "prefill", Q6_K, 512, (5120,), 27648, ["k_fill_zero", "k_gemm_f16<14,8,0,1,0>"]),

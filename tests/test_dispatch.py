@@ -51,6 +51,8 @@ def dry_dispatch(entry, qt, M, Ns, K):
         elif entry == "gate_up_silu":
             rc = L.ifx_qgemv_gate_up_silu(qt, W[0], _fake(1), A, None, ops.OUT_F32, B, M, Ns[0], K,
                                           None)
+        elif entry == "packed":
+            rc = L.ifx_qgemv_packed(qt, n, W, Y, NN, A, B, M, K, None)
         elif entry == "prefill":
             rc = L.ifx_qgemm_prefill(qt, W[0], A, Y[0], ops.OUT_F32, ops.STORE, None, M, Ns[0], K,
                                      None)

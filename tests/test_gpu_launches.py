@@ -59,6 +59,11 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         A = ops.rmsnorm_quantize_q8_1(X, NW, eps=1e-6)  # the standalone producer
         a = down(A)
         check_q8_1_close(a, orc.rmsnorm_quantize_q8_1(x, nw, 1e-6), orc.rmsnorm_values(x, nw, 1e-6))
+    elif entry == "packed":
+        X = up(x, dev)
+        codes, scales = ops.quantize_rows_symmetric(X)
+        c_h, s_h = down(codes), down(scales)
+        assert np.array_equal(c_h, orc.quantize_rows_symmetric(x)[0])
     else:
         a = orc.quantize_q8_1(x)
         A = up(a, dev)
@@ -86,6 +91,8 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
             h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], Wu, X, NW, M, Ns[0], K, eps=1e-6)
         elif entry == "gate_up_silu":
             h, q = ops.qgemv_gate_up_silu(qt, W[0], Wu, A, M, Ns[0], K)
+        elif entry == "packed":
+            outs = ops.qgemv_packed(qt, W, codes, scales, M, list(Ns), K)
         elif entry == "prefill":
             outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, prefill=True)]
         elif entry == "prefill_int8":
@@ -112,6 +119,16 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
             g2, u2 = ops.qgemv_grouped(qt, [W[0], Wu], A, M, [N, N], K)
         if entry == "gate_up_silu_rmsnorm" or same_slot_waves(lg2.kernels[-1], want[0]):
             assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
+        return
+
+    if entry == "packed":
+        # fp16 outputs: the row bar plus each value's fp16 rounding
+        for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):
+            idx = _rows(n, seed + i)
+            ye = orc.gemv_packed_exact(raw_qt, w[idx], c_h, s_h, M, len(idx), K)
+            yd = down(y)[:, idx].astype(np.float64)
+            lim = 1e-3 * np.linalg.norm(ye, axis=1, keepdims=True) + np.abs(ye) * 2.0 ** -11
+            assert np.all(np.abs(yd - ye) <= lim)
         return
 
     for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):
