@@ -94,6 +94,20 @@ int ifx_rmsnorm_quantize_q8_1(const void *residual, int residual_dtype,
 int ifx_silu_mul_quantize_q8_1(const void *gate, const void *up, int dtype, void *q8_1, int M,
                                int K, void *stream);
 
+/* ifx_qgemv_gate_up_silu with a caller workspace for the fp16-dequant
+ * GEMV's K split (M up to 32): workspace_bytes >=
+ * ifx_qgemv_gate_up_silu_workspace_bytes(quant_type, M, N, K), 256-byte
+ * aligned, zeroed once before first use; every call leaves it zeroed again.
+ * Calls that share a workspace must not overlap.  Shapes that do not split
+ * ignore it.  No single-call counterpart in the reference (its fused
+ * gate/up/SiLU stops at M = 8). */
+int ifx_qgemv_gate_up_silu_ws(int quant_type, const void *W_gate, const void *W_up,
+                              const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
+                              int N, int K, void *workspace, int64_t workspace_bytes,
+                              void *stream);
+/* Workspace bytes ifx_qgemv_gate_up_silu_ws needs (0: none). */
+int64_t ifx_qgemv_gate_up_silu_workspace_bytes(int quant_type, int M, int N, int K);
+
 /* Per-row symmetric int8 activations, the input format of ifx_qgemv_packed:
  * per row, scale = max|x| / 127 (0 for a zero row), codes =
  * clamp(rint(x / scale), -127, 127) evaluated as x * (1 / scale) in fp32.
@@ -203,7 +217,11 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
  * N % 32 == 0 (every type), 3 <= M <= 8 for Q4_K / Q6_K with K % 256 == 0,
  * and M <= 16 on tiled copies (the slot-packed MFMA GEMV: h and its blocks
  * equal ifx_qgemv_grouped + ifx_silu_mul_quantize_q8_1 bit for bit where
- * the grouped launch runs the same geometry); other shapes return
+ * the grouped launch runs the same geometry); up to M = 32 (Q4_K / Q6_K /
+ * Q8_0, raw or tiled, K % 256 == 0) the fp16-dequant MFMA GEMV, whose K split
+ * needs a workspace unless it is 1 (then use ifx_qgemv_gate_up_silu_ws; h and
+ * its blocks equal ifx_qgemv_grouped_ws + ifx_silu_mul_quantize_q8_1 bit for
+ * bit where the grouped launch is the same GEMV); other shapes return
  * IFX_BAD_GEOMETRY (not handled: use those two calls).
  * Replaces FusedQuantGemm::FusedGateUpSiluGemvQ8_1 and
  * FusedGateUpSiluGemvQ8_1WithEpilogue (fused_quant_gemm.h:281-307; kernels

@@ -27,6 +27,9 @@ SIGNATURES = {
     "ifx_qgemm_prefill_ws": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _vp],
                              _i32),
     "ifx_qgemv_gate_up_silu": ([_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_qgemv_gate_up_silu_ws": ([_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64,
+                                   _vp], _i32),
+    "ifx_qgemv_gate_up_silu_workspace_bytes": ([_i32, _i32, _i32, _i32], _i64),
     "ifx_qgemv_gate_up_silu_rmsnorm": ([_i32, _vp, _vp, _vp, _i32, _vp, ctypes.c_float, _vp, _i32, _vp, _i32,
                                         _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_noalloc": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),

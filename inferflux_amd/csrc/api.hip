@@ -70,6 +70,11 @@ hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, fl
                              const void *Wd, void *workspace, int q_dim, int hidden, int ffn,
                              hipStream_t s);
 bool gemv_slot_fits(int qtype, int M, int K);
+int gemv_dq_swiglu_splits(int M, int N, int K);
+hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
+                                 void *H, bool h_f16, void *Q, int M, int N, int K, void *ws,
+                                 hipStream_t stream);
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K);
 hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
                                    void *H, bool f16h, void *Q, int M, int N, int K,
                                    hipStream_t stream);
@@ -627,34 +632,79 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
                                             static_cast<hipStream_t>(stream)));
 }
 
-int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
-                           const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
-                           int N, int K, void *stream) {
+namespace {
+
+// The fused gate/up/SiLU launches: M <= 2 the v_dot4 GEMV; 3 <= M <= 8
+// (Q4_K / Q6_K) and tiled rows up to M = 16 the slot-packed MFMA GEMV; the
+// rest up to M = 32 the fp16-dequant MFMA GEMV, whose K split needs the
+// pair's ordered-split workspace (ws) unless the split is 1.  Whole Q8_1
+// blocks of outputs only.
+int gate_up_silu_impl(int quant_type, const void *W_gate, const void *W_up, const void *A_q8_1,
+                      void *H, int h_dtype, void *q8_1_out, int M, int N, int K, void *ws,
+                      int64_t ws_bytes, void *stream) {
   if (!W_gate || !W_up || !A_q8_1 || (!H && !q8_1_out)) return IFX_NULL_POINTER;
   if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
-  // the fused kernels serve the decode batch (M <= 2: the v_dot4 GEMV;
-  // 3 <= M <= 8, Q4_K / Q6_K, and tiled rows up to M = 16: the slot-packed
-  // MFMA GEMV) and whole Q8_1 blocks of outputs; other shapes take the
-  // grouped GEMV + SiLU producer
   const int max_m = tiled(quant_type) ? 0
                     : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
   const bool slot = M > max_m && M <= (tiled(quant_type) ? 2 * kMaxSlotM : kMaxSlotM) &&
                     ifx::gemv_slot_fits(quant_type, M, K);
-  if (M < 1 || (M > max_m && !slot) || N % 32 != 0) return IFX_BAD_GEOMETRY;
+  const bool dq = M > max_m && !slot && ifx::gemv_dq_fits(quant_type, M, K);
+  if (M < 1 || (M > max_m && !slot && !dq) || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)
   void *probe_out = H ? H : q8_1_out;
   const int rc = check_gemm_args(quant_type, W_gate, A_q8_1, probe_out, IFX_OUT_F32, IFX_STORE,
                                  nullptr, M, N, K);
   if (rc != IFX_OK) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   if (slot)
     return status_of(ifx::launch_gemv_slot_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
-                                                  h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
-                                                  static_cast<hipStream_t>(stream)));
+                                                  h_dtype == IFX_OUT_F16, q8_1_out, M, N, K, s));
+  if (dq) {
+    if (ifx::gemv_dq_swiglu_splits(M, N, K) > 1) {
+      const int NN[2] = {N, N};
+      if (!ws) return IFX_BAD_GEOMETRY;  // not handled without the workspace
+      if (ws_bytes < ifx::gemv_dq_workspace_bytes(2, NN, false, M, K)) return IFX_BAD_GEOMETRY;
+    } else {
+      ws = nullptr;
+    }
+    if (ws_bytes > 0 && reinterpret_cast<uintptr_t>(ws) % 256) return IFX_BAD_GEOMETRY;
+    return status_of(ifx::launch_gemv_dq_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
+                                                h_dtype == IFX_OUT_F16, q8_1_out, M, N, K, ws, s));
+  }
   return status_of(ifx::launch_gemv_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
-                                           h_dtype == IFX_OUT_F16, q8_1_out, M, N, K,
-                                           static_cast<hipStream_t>(stream)));
+                                           h_dtype == IFX_OUT_F16, q8_1_out, M, N, K, s));
+}
+
+}  // namespace
+
+int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
+                           const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
+                           int N, int K, void *stream) {
+  return gate_up_silu_impl(quant_type, W_gate, W_up, A_q8_1, H, h_dtype, q8_1_out, M, N, K,
+                           nullptr, 0, stream);
+}
+
+int64_t ifx_qgemv_gate_up_silu_workspace_bytes(int quant_type, int M, int N, int K) {
+  if (!is_weight_type(quant_type) || row_split(quant_type) || M < 1 || N < 1 || K < 1) return 0;
+  const int max_m = tiled(quant_type) ? 0
+                    : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
+  const bool slot = M > max_m && M <= (tiled(quant_type) ? 2 * kMaxSlotM : kMaxSlotM) &&
+                    ifx::gemv_slot_fits(quant_type, M, K);
+  if (M <= max_m || slot || !ifx::gemv_dq_fits(quant_type, M, K)) return 0;
+  if (ifx::gemv_dq_swiglu_splits(M, N, K) <= 1) return 0;
+  const int NN[2] = {N, N};
+  return ifx::gemv_dq_workspace_bytes(2, NN, false, M, K);
+}
+
+int ifx_qgemv_gate_up_silu_ws(int quant_type, const void *W_gate, const void *W_up,
+                              const void *A_q8_1, void *H, int h_dtype, void *q8_1_out, int M,
+                              int N, int K, void *workspace, int64_t workspace_bytes,
+                              void *stream) {
+  if (!workspace) return IFX_NULL_POINTER;
+  return gate_up_silu_impl(quant_type, W_gate, W_up, A_q8_1, H, h_dtype, q8_1_out, M, N, K,
+                           workspace, workspace_bytes, stream);
 }
 
 int ifx_qgemv_gate_up_silu_rmsnorm(int quant_type, const void *W_gate, const void *W_up,

@@ -33,8 +33,11 @@
 // waves read; the next super-block's weight bytes are loaded while the
 // current one is computed.
 #include "ifx_common.h"
+#include "ifx_q8_1.h"
 
 #include <stdlib.h>
+
+#include <algorithm>
 
 namespace ifx {
 
@@ -62,6 +65,11 @@ struct DqArgs {
   const uint8_t *A;
   int M, K, mode, sb_per;
   SplitWs ws;  // ordered split: counters per row group, 16 KB slot per (group, split)
+  // fused gate/up/SiLU (SW): seg[0] gate, seg[1] up; h = silu(g) * u to H
+  // (fp32, or fp16 with h_f16; or none) and its Q8_1 blocks to Q (or none)
+  void *H;
+  uint8_t *Q;
+  int h_f16;
 };
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -323,11 +331,18 @@ __device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint
 // SPLIT: 0 one workgroup per row group; 1 K split, fp32 atomics into Y
 // (zeroed first in store / bias mode); 2 K split, ordered reduction through
 // args.ws (split_arrive_last).
-template <int QT, bool F16OUT, int SPLIT, bool TL = false>
+// SW: fused gate/up/SiLU.  A workgroup owns 64 outputs: waves 0-1 their
+// gate rows, waves 2-3 the same up rows, each row summed exactly as the
+// grouped launch with the same K split sums it; after the (ordered)
+// reduction the workgroup forms h = silu(g) * u and its Q8_1 blocks with the
+// SiLU producer's arithmetic (8 lanes per block), so h and the blocks equal
+// grouped GEMV + silu_mul_quantize bit for bit.
+template <int QT, bool F16OUT, int SPLIT, bool TL = false, bool SW = false>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int bx = blockIdx.x;
-  const int si = (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+  const int si = SW ? static_cast<int>(threadIdx.x >> 7)  // waves 0-1 gate, 2-3 up
+                 : (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
                  : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
   const DqSeg &sg = args.seg[si];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -343,7 +358,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
       QT == kTypeQ8_0 ? (K >> 5) * kQ8_0Bytes : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
   const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(TL ? (N + 31) & ~31 : N));
   const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
-  const int n = (bx - sg.blk_begin) * kRowsPerWg + wave * 32 + l32;
+  const int n = SW ? bx * 64 + (wave & 1) * 32 + l32
+                   : (bx - sg.blk_begin) * kRowsPerWg + wave * 32 + l32;
   // tiled: the group's first tile (group-major tiles of 32 rows x 1 super-block)
   const uint32_t row_off = TL ? static_cast<uint32_t>(n >> 5) * 32 * w_row
                               : static_cast<uint32_t>(min(n, N - 1)) * w_row;
@@ -423,6 +439,45 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) yv[i] = t[i];
     split_reset(args.ws.cnt + bx);
+  }
+  if constexpr (SW) {
+    // gate / up sums of the 64 outputs -> LDS [projection][batch row][64]
+    // (the activation stage is no longer read: every wave has passed a
+    // barrier after its last super-block)
+    if constexpr (SPLIT != 2) __syncthreads();
+    float *gu = reinterpret_cast<float *>(lds);
+    const int proj = wave >> 1, col = (wave & 1) * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+      if (m < M) gu[(proj * kMaxM + m) * 64 + col] = yv[i];
+    }
+    __syncthreads();
+    // 8 lanes per Q8_1 block (4 outputs each), two blocks per batch row;
+    // whole 8-lane groups stay active together
+    const int n0 = bx * 64;
+    for (int it = tid; it < M * 16; it += 64 * kWaves) {
+      const int blk = it >> 3, l = it & 7, m = blk >> 1, b = blk & 1;
+      const int o = n0 + 32 * b + 4 * l;
+      if (n0 + 32 * b >= N) continue;
+      const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[m * 64 + 32 * b + 4 * l]);
+      const f32x4 u4 = *reinterpret_cast<const f32x4 *>(&gu[(kMaxM + m) * 64 + 32 * b + 4 * l]);
+      const f32x4 hv = silu_mul4(g4, u4);
+      const int64_t oh = static_cast<int64_t>(m) * N + o;
+      if (args.H) {
+        if (args.h_f16) {
+          const u32x2 hh = {f2h_bits(hv.x) | (f2h_bits(hv.y) << 16),
+                            f2h_bits(hv.z) | (f2h_bits(hv.w) << 16)};
+          *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(args.H) + oh) = hh;
+        } else {
+          *reinterpret_cast<f32x4 *>(static_cast<float *>(args.H) + oh) = hv;
+        }
+      }
+      if (args.Q)
+        quantize4_store(hv.x, hv.y, hv.z, hv.w,
+                        args.Q + (static_cast<int64_t>(m) * (N >> 5) + (o >> 5)) * kQ8_1Bytes, l);
+    }
+    return;
   }
   if (n >= N) return;
 #pragma unroll
@@ -515,6 +570,78 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
 }
 
 }  // namespace
+
+namespace {
+
+template <int QT, bool TL>
+hipError_t launch_sw(const DqArgs &args, int groups, int ks, hipStream_t s) {
+  const size_t stage = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
+  const size_t shm = std::max(stage, static_cast<size_t>(2 * kMaxM * 64 * 4));  // + gate/up sums
+  const dim3 grid(groups, ks), block(64 * kWaves);
+  if (ks == 1) IFX_LAUNCH(k_gemv_dq, (QT, false, 0, TL, true), grid, block, shm, s, args);
+  else IFX_LAUNCH(k_gemv_dq, (QT, false, 2, TL, true), grid, block, shm, s, args);
+  return last_error();
+}
+
+// The pair plan (gate and up as one grouped launch of two projections):
+// row groups, K splits and sb_per as the grouped launch chooses them.
+void sw_plan(DqArgs &args, int N, int &pair_groups, int &ks) {
+  args.seg[0].N = args.seg[1].N = N;
+  args.nseg = 2;
+  dq_plan(args, false, 0, pair_groups, ks);
+}
+
+}  // namespace
+
+bool gemv_dq_fits(int qtype, int M, int K);
+
+// K splits of the fused gate/up/SiLU launch (1: no workspace needed).
+int gemv_dq_swiglu_splits(int M, int N, int K) {
+  DqArgs args{};
+  args.M = M;
+  args.K = K;
+  int pg = 0, ks = 1;
+  sw_plan(args, N, pg, ks);
+  return ks;
+}
+
+// Fused gate/up/SiLU on the fp16-dequant GEMV (k_gemv_dq, SW); N % 32 == 0.
+// ws: the pair's ordered-split workspace (gemv_dq_workspace_bytes of
+// count 2, N, N), required when the launch splits K.
+hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
+                                 void *H, bool h_f16, void *Q, int M, int N, int K, void *ws,
+                                 hipStream_t stream) {
+  if (!gemv_dq_fits(qtype, M, K) || N % 32 != 0) return hipErrorInvalidValue;
+  DqArgs args{};
+  args.seg[0] = DqSeg{static_cast<const uint8_t *>(Wg), nullptr, nullptr, N, 0};
+  args.seg[1] = DqSeg{static_cast<const uint8_t *>(Wu), nullptr, nullptr, N, 0};
+  args.A = static_cast<const uint8_t *>(A);
+  args.M = M;
+  args.K = K;
+  args.mode = 0;
+  args.H = H;
+  args.Q = static_cast<uint8_t *>(Q);
+  args.h_f16 = h_f16 ? 1 : 0;
+  int pair_groups = 0, ks = 1;
+  sw_plan(args, N, pair_groups, ks);
+  if (ks > 1) {
+    if (!ws) return hipErrorInvalidValue;
+    // the pair's workspace layout: counters for its row groups, then slots
+    args.ws.cnt = static_cast<uint32_t *>(ws);
+    args.ws.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                             (static_cast<int64_t>(pair_groups) * 4 + 255) / 256 * 256);
+  }
+  const int groups = (N + 63) / 64;
+  switch (qtype) {
+  case kTypeQ4_K: return launch_sw<kTypeQ4_K, false>(args, groups, ks, stream);
+  case kTypeQ6_K: return launch_sw<kTypeQ6_K, false>(args, groups, ks, stream);
+  case kTypeQ8_0: return launch_sw<kTypeQ8_0, false>(args, groups, ks, stream);
+  case kTypeQ4_KT: return launch_sw<kTypeQ4_K, true>(args, groups, ks, stream);
+  case kTypeQ6_KT: return launch_sw<kTypeQ6_K, true>(args, groups, ks, stream);
+  case kTypeQ8_0T: return launch_sw<kTypeQ8_0, true>(args, groups, ks, stream);
+  default: return hipErrorInvalidValue;
+  }
+}
 
 // fp16 outputs are not split: their K must fit one activation stage.
 bool gemv_dq_fits(int qtype, int M, int K) {

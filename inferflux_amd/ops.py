@@ -344,10 +344,17 @@ def qgemv_grouped_rmsnorm(qtype, Ws, x, norm_weight, M, Ns, K, eps=1e-6, outs=No
     return outs
 
 
+def gate_up_silu_workspace_bytes(qtype, M, N, K):
+    """Workspace bytes qgemv_gate_up_silu needs (0: none)."""
+    return int(_lib.load().ifx_qgemv_gate_up_silu_workspace_bytes(qtype, M, N, K))
+
+
 def qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, h_out=None, q8_1_out=None, want_h=True,
-                       want_q8_1=True, h_dtype=torch.float32, stream=None):
-    """h = silu(Wg . a) * (Wu . a) for M <= 2 in one launch; returns
-    (h [M, N] or None, Q8_1 [M, N/32*36] or None)."""
+                       want_q8_1=True, h_dtype=torch.float32, stream=None, workspace=None):
+    """h = silu(Wg . a) * (Wu . a) in one launch; returns (h [M, N] or
+    None, Q8_1 [M, N/32*36] or None).  workspace: a zeroed uint8 device
+    tensor of gate_up_silu_workspace_bytes (the fp16-dequant GEMV's K split
+    at M up to 32)."""
     if want_h and h_out is None:
         h_out = torch.empty((M, N), dtype=h_dtype, device=A.device)
     if want_q8_1 and q8_1_out is None:
@@ -361,10 +368,17 @@ def qgemv_gate_up_silu(qtype, Wg, Wu, A, M, N, K, h_out=None, q8_1_out=None, wan
     if q8_1_out is not None and q8_1_out.numel() < M * (N // 32) * 36:
         raise ValueError("bad Q8_1 output")
     hd = OUT_F16 if h_out is not None and h_out.dtype == torch.float16 else OUT_F32
-    rc = _lib.load().ifx_qgemv_gate_up_silu(
-        qtype, _dev(Wg, "Wg"), _dev(Wu, "Wu"), _dev(A, "A"),
-        _dev(h_out, "h") if h_out is not None else None, hd,
-        _dev(q8_1_out, "q8_1_out") if q8_1_out is not None else None, M, N, K, _stream(stream))
+    hp = _dev(h_out, "h") if h_out is not None else None
+    qp = _dev(q8_1_out, "q8_1_out") if q8_1_out is not None else None
+    if workspace is not None:
+        rc = _lib.load().ifx_qgemv_gate_up_silu_ws(
+            qtype, _dev(Wg, "Wg"), _dev(Wu, "Wu"), _dev(A, "A"), hp, hd, qp, M, N, K,
+            _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+            _stream(stream))
+        _check(rc, "ifx_qgemv_gate_up_silu_ws")
+        return h_out, q8_1_out
+    rc = _lib.load().ifx_qgemv_gate_up_silu(qtype, _dev(Wg, "Wg"), _dev(Wu, "Wu"), _dev(A, "A"),
+                                            hp, hd, qp, M, N, K, _stream(stream))
     _check(rc, "ifx_qgemv_gate_up_silu")
     return h_out, q8_1_out
 

@@ -779,15 +779,17 @@ def test_gate_up_silu_rmsnorm_not_handled(dev):
 
 
 def test_gate_up_silu_not_handled(dev):
-    """M > 8, M > 2 for types without the slot kernel, or N % 32 != 0: not
-    handled (positive status), nothing launched."""
+    """M > 32, M > 2 for Q5_K (no batch kernel), N % 32 != 0, or a K split
+    (fp16-dequant GEMV, M up to 32) without a workspace: not handled
+    (positive status), nothing launched."""
     import torch
     from inferflux_amd import ops
-    w = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
-    a = torch.zeros(1 << 14, dtype=torch.uint8, device=dev)
+    w = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    a = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    assert ops.gate_up_silu_workspace_bytes(Q4_K, 20, 64, 5120) > 0
     with ops.launch_log() as lg:
-        for qt, M, N, K in ((Q4_K, 9, 32, 256), (Q8_0, 3, 32, 256), (Q8_0, 1, 20, 32),
-                            (Q6_K, 4, 48, 256)):
+        for qt, M, N, K in ((Q4_K, 33, 32, 256), (Q5_K, 3, 32, 256), (Q8_0, 1, 20, 32),
+                            (Q6_K, 4, 48, 256), (Q4_K, 20, 64, 5120)):
             with pytest.raises(ops.NotHandled):
                 ops.qgemv_gate_up_silu(qt, w, w, a, M, N, K)
     assert lg.kernels == []

@@ -166,6 +166,64 @@ def test_gate_up_silu_tiled(orc, dev, qtype, M):
             assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
 
 
+def _check_h_propagated(h, g, u, tol=1e-3):
+    """h = silu(g) * u from two GEMV outputs, each held to the contract's
+    tol * ||row||_2: the bar on h is that error carried through the product,
+    |dh| <= |silu'(g) u| tol ||g_row|| + |silu(g)| tol ||u_row||.  (A row of h
+    dominated by one element can exceed tol * ||h_row|| with g and u inside
+    their own bars: the fp16-dequant GEMV rounds each weight to fp16.)"""
+    with np.errstate(over="ignore"):
+        sg = 1.0 / (1.0 + np.exp(-g))
+    dsilu = sg * (1.0 + g * (1.0 - sg))
+    eg = tol * np.linalg.norm(g, axis=1, keepdims=True)
+    eu = tol * np.linalg.norm(u, axis=1, keepdims=True)
+    bound = np.abs(dsilu * u) * eg + np.abs(g * sg) * eu + eg * eu
+    err = np.abs(np.asarray(h, np.float64) - g * sg * u)
+    assert np.all(err <= bound), f"max err / bound {(err / bound).max()}"
+
+
+@pytest.mark.parametrize("qtype,tiled,M,N,K", [(Q4_K, True, 17, 512, 1024), (Q4_K, True, 32, 1056, 5120),
+                                                (Q6_K, True, 24, 512, 2048), (Q4_K, False, 32, 512, 5120),
+                                                (Q8_0, False, 20, 256, 2048), (Q4_K, False, 12, 256, 2048)])
+def test_gate_up_silu_dq(orc, dev, qtype, tiled, M, N, K):
+    """M up to 32: the fp16-dequant GEMV with the SiLU / Q8_1 epilogue,
+    through the workspace entry when its K splits.  h against the oracle,
+    its Q8_1 blocks the exact quantization of h, and bit for bit the grouped
+    (workspace) launch + SiLU producer where that launch is the same GEMV."""
+    import torch
+    from inferflux_amd import ops, synth
+    note(f"gate_up_silu dq type={qtype} tiled={tiled} M={M} N={N} K={K}")
+    wg = synth.blocks(qtype, N, K, seed=M + 3)
+    wu = synth.blocks(qtype, N, K, seed=M + 4)
+    a = orc.quantize_q8_1(synth.activations(M, K, seed=K + M) * 0.1)
+    A = up(a, dev)
+    if tiled:
+        tt, WG = ops.repack_tiled(qtype, up(wg, dev), N, K)
+        WU = ops.repack_tiled(qtype, up(wu, dev), N, K)[1]
+    else:
+        tt, WG, WU = qtype, up(wg, dev), up(wu, dev)
+    nb = ops.gate_up_silu_workspace_bytes(tt, M, N, K)
+    ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
+    for rep in range(2):  # the second call reuses the workspace the first left zeroed
+        with ops.launch_log() as lg:
+            h, q = ops.qgemv_gate_up_silu(tt, WG, WU, A, M, N, K, workspace=ws)
+        assert len(lg.kernels) == 1 and lg.kernels[0].startswith(f"k_gemv_dq<{qtype},0,")
+        assert lg.kernels[0].endswith(f",{int(tiled)},1>")
+        g = orc.gemv_exact(qtype, wg, a, M, N, K)
+        u = orc.gemv_exact(qtype, wu, a, M, N, K)
+        _check_h_propagated(down(h), g, u)
+        assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
+    nbg = ops.qgemv_workspace_bytes(tt, [N, N], M, K)
+    wsg = torch.zeros(max(nbg, 256), dtype=torch.uint8, device=dev)
+    with ops.launch_log() as lg2:
+        g2, u2 = ops.qgemv_grouped(tt, [WG, WU], A, M, [N, N], K, workspace=wsg)
+    if lg2.kernels[-1].startswith("k_gemv_dq<"):
+        assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
+    if nb:  # without the workspace the split launch is not handled
+        with pytest.raises(ops.NotHandled):
+            ops.qgemv_gate_up_silu(tt, WG, WU, A, M, N, K)
+
+
 def test_tiled_not_handled(dev):
     """Tiled weights above M = 32, on the prefill, fused-RMSNorm and
     dequantize entries, or tiling a type without a tiled layout: not
