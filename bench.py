@@ -174,9 +174,10 @@ def main():
         fused == "ffn": QKV with the fused RMSNorm, then ifx_decode_ffn: O
         with the fused quantizer and one grid-synchronised launch for
         RMSNorm, gate/up + SiLU and down (M = 1): 3 launches.
-        fused == "batch_swiglu" (any M <= 8): the Q8_1 producers as launches of
-        their own, except SiLU * up + Q8_1, which the gate/up launch computes
-        (ifx_qgemv_gate_up_silu): 3 producers + 4 GEMVs.
+        fused == "batch_swiglu" (M <= 8; tiled copies M <= 32): the Q8_1
+        producers as launches of their own, except SiLU * up + Q8_1, which the
+        gate/up launch computes (ifx_qgemv_gate_up_silu, with the workspace
+        its ordered K split needs from M = 17): 3 producers + 4 GEMVs.
         split_down: the down projection reads a row-split copy of its Q6_K
         weights (ifx_repack, M <= 2).
         tiled: the layer's tiled copy (tiled_layer) the GEMVs read instead
@@ -212,6 +213,11 @@ def main():
                 nb = ops.qgemv_workspace_bytes(qt_, [layer[p][1] for p in l[1]], M, K_)
                 if nb:
                     wsd[l[0]] = torch.zeros(nb, dtype=torch.uint8, device=dev)
+        if fused == "batch_swiglu":
+            qt_, N_, K_, _ = layer["gate"]
+            nb = ops.gate_up_silu_workspace_bytes(qt_, M, N_, K_)
+            if nb:
+                wsd["gate_up_silu"] = torch.zeros(nb, dtype=torch.uint8, device=dev)
         ws = None
         if fused == "ffn":
             ws = torch.zeros(ops.decode_ffn_workspace_bytes(M, ffn), dtype=torch.uint8, device=dev)
@@ -272,7 +278,8 @@ def main():
                     qt, N, K, _ = layer["gate"]
                     ops.qgemv_gate_up_silu(qt, layer["gate"][3][r], layer["up"][3][r],
                                            A["ffn_in"], M, N, K, want_h=False,
-                                           q8_1_out=A["ffn_act"])
+                                           q8_1_out=A["ffn_act"],
+                                           workspace=wsd.get("gate_up_silu"))
                 if which is None or which == "down":
                     gemv("down", r)
                 return
@@ -581,9 +588,9 @@ def main():
             steps = max(20, args.steps // 4)
             forms14 = [(f"M{M}", {}), (f"M{M}_tiled", {"tiled": layer14_t}),
                        (f"M{M}_tiled_ordered", {"tiled": layer14_t, "ordered": True})]
-            if M <= 16:  # SiLU * up + Q8_1 in the gate/up launch (tiled, M <= 16)
-                forms14.append((f"M{M}_tiled_swiglu", {"tiled": layer14_t,
-                                                       "fused": "batch_swiglu"}))
+            # SiLU * up + Q8_1 in the gate/up launch (tiled; M = 32: the
+            # fp16-dequant GEMV with its ordered K split)
+            forms14.append((f"M{M}_tiled_swiglu", {"tiled": layer14_t, "fused": "batch_swiglu"}))
             for key, kw in forms14:
                 run = decode_layer_runner(layer14, M, seed=40 + M, **kw)
                 us_layer = time_loop(run, steps, 5)

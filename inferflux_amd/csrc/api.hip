@@ -635,22 +635,34 @@ int ifx_qgemv_grouped_rmsnorm(int quant_type, int count, const void *const *W, v
 namespace {
 
 // The fused gate/up/SiLU launches: M <= 2 the v_dot4 GEMV; 3 <= M <= 8
-// (Q4_K / Q6_K) and tiled rows up to M = 16 the slot-packed MFMA GEMV; the
-// rest up to M = 32 the fp16-dequant MFMA GEMV, whose K split needs the
-// pair's ordered-split workspace (ws) unless the split is 1.  Whole Q8_1
-// blocks of outputs only.
+// (Q4_K / Q6_K) the slot-packed MFMA GEMV; tiled rows up to M = 32 the GEMV
+// the grouped gate+up launch runs (route()); the rest up to M = 32 the
+// fp16-dequant MFMA GEMV, whose K split needs the pair's ordered-split
+// workspace unless the split is 1.  Whole Q8_1 blocks of outputs only.
+enum class SwKernel { None, Gemv, Slot, Dq };
+SwKernel swiglu_kernel(int qt, int M, int N, int K) {
+  const int max_m = tiled(qt) ? 0 : (qt == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
+  if (M < 1) return SwKernel::None;
+  if (M <= max_m) return SwKernel::Gemv;
+  if (tiled(qt)) {
+    if (M > 32) return SwKernel::None;
+    if (route(qt, M, K, 2 * N, false, true) == Route::Slot)
+      return ifx::gemv_slot_fits(qt, M, K) ? SwKernel::Slot : SwKernel::None;
+    return ifx::gemv_dq_fits(qt, M, K) ? SwKernel::Dq : SwKernel::None;
+  }
+  if (M <= kMaxSlotM && ifx::gemv_slot_fits(qt, M, K)) return SwKernel::Slot;
+  return ifx::gemv_dq_fits(qt, M, K) ? SwKernel::Dq : SwKernel::None;
+}
+
 int gate_up_silu_impl(int quant_type, const void *W_gate, const void *W_up, const void *A_q8_1,
                       void *H, int h_dtype, void *q8_1_out, int M, int N, int K, void *ws,
                       int64_t ws_bytes, void *stream) {
   if (!W_gate || !W_up || !A_q8_1 || (!H && !q8_1_out)) return IFX_NULL_POINTER;
   if (!is_weight_type(quant_type) || row_split(quant_type)) return IFX_UNSUPPORTED_TYPE;
   if (h_dtype != IFX_OUT_F32 && h_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
-  const int max_m = tiled(quant_type) ? 0
-                    : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
-  const bool slot = M > max_m && M <= (tiled(quant_type) ? 2 * kMaxSlotM : kMaxSlotM) &&
-                    ifx::gemv_slot_fits(quant_type, M, K);
-  const bool dq = M > max_m && !slot && ifx::gemv_dq_fits(quant_type, M, K);
-  if (M < 1 || (M > max_m && !slot && !dq) || N % 32 != 0) return IFX_BAD_GEOMETRY;
+  const SwKernel kern = swiglu_kernel(quant_type, M, N, K);
+  const bool slot = kern == SwKernel::Slot, dq = kern == SwKernel::Dq;
+  if (kern == SwKernel::None || N % 32 != 0) return IFX_BAD_GEOMETRY;
   // geometry and 32-bit range checks of the GEMV (the output pointer is
   // only checked for presence)
   void *probe_out = H ? H : q8_1_out;
@@ -688,11 +700,7 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
 
 int64_t ifx_qgemv_gate_up_silu_workspace_bytes(int quant_type, int M, int N, int K) {
   if (!is_weight_type(quant_type) || row_split(quant_type) || M < 1 || N < 1 || K < 1) return 0;
-  const int max_m = tiled(quant_type) ? 0
-                    : (quant_type == IFX_TYPE_Q4_K && K <= 2048) ? IFX_SWIGLU_MAX_M : 2;
-  const bool slot = M > max_m && M <= (tiled(quant_type) ? 2 * kMaxSlotM : kMaxSlotM) &&
-                    ifx::gemv_slot_fits(quant_type, M, K);
-  if (M <= max_m || slot || !ifx::gemv_dq_fits(quant_type, M, K)) return 0;
+  if (swiglu_kernel(quant_type, M, N, K) != SwKernel::Dq) return 0;
   if (ifx::gemv_dq_swiglu_splits(M, N, K) <= 1) return 0;
   const int NN[2] = {N, N};
   return ifx::gemv_dq_workspace_bytes(2, NN, false, M, K);

@@ -99,8 +99,10 @@ LAUNCHES = [
     ("c4t_gate_up_m16", "grouped_ws", Q4_K_T, 16, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_down_m16", "gemv_accum_ws", Q6_K_T, 16, (5120,), 13824,
      ["k_gemv_slot<14,16,4,0,2,0,1>"]),
-    ("c4t_gate_up_silu_m16", "gate_up_silu", Q4_K_T, 16, (13824,), 5120,
-     ["k_gemv_slot<12,16,4,0,0,1,1>"]),
+    ("c4t_gate_up_silu_m16", "gate_up_silu_ws", Q4_K_T, 16, (13824,), 5120,
+     ["k_gemv_dq<12,0,2,1,1>"]),
+    ("c4t_gate_up_silu_m32", "gate_up_silu_ws", Q4_K_T, 32, (13824,), 5120,
+     ["k_gemv_dq<12,0,2,1,1>"]),
     ("c4t_qkv_m32", "grouped_ws", Q4_K_T, 32, QKV14, 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_o_m32", "gemv_accum_ws", Q4_K_T, 32, (5120,), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_gate_up_m32", "grouped_ws", Q4_K_T, 32, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),

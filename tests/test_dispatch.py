@@ -48,6 +48,9 @@ def dry_dispatch(entry, qt, M, Ns, K):
         elif entry == "gate_up_silu_rmsnorm":
             rc = L.ifx_qgemv_gate_up_silu_rmsnorm(qt, W[0], _fake(1), X, ops.OUT_F32, NW, 1e-6,
                                                   None, ops.OUT_F32, B, M, Ns[0], K, None)
+        elif entry == "gate_up_silu_ws":
+            rc = L.ifx_qgemv_gate_up_silu_ws(qt, W[0], _fake(1), A, None, ops.OUT_F32, B, M, Ns[0],
+                                             K, WS, 1 << 30, None)
         elif entry == "gate_up_silu":
             rc = L.ifx_qgemv_gate_up_silu(qt, W[0], _fake(1), A, None, ops.OUT_F32, B, M, Ns[0], K,
                                           None)

@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 from tests.launch_table import IDS, LAUNCHES
-from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, same_slot_waves, up
+from tests.test_gpu_parity import (check_h_propagated, check_q8_1_close, check_rows, down, note,
+                                   same_slot_waves, up)
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +47,8 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     wsp = None
     if entry.endswith("_ws"):
         entry = entry[:-3]
-        nb = ops.qgemv_workspace_bytes(qt, list(Ns), M, K)
+        nb = (ops.gate_up_silu_workspace_bytes(qt, M, Ns[0], K) if entry == "gate_up_silu"
+              else ops.qgemv_workspace_bytes(qt, list(Ns), M, K))
         wsp = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
     rng = np.random.default_rng(seed)
     outl = 0.01 if entry.startswith("prefill") else 0.0
@@ -90,7 +92,7 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         elif entry == "gate_up_silu_rmsnorm":
             h, q = ops.qgemv_gate_up_silu_rmsnorm(qt, W[0], Wu, X, NW, M, Ns[0], K, eps=1e-6)
         elif entry == "gate_up_silu":
-            h, q = ops.qgemv_gate_up_silu(qt, W[0], Wu, A, M, Ns[0], K)
+            h, q = ops.qgemv_gate_up_silu(qt, W[0], Wu, A, M, Ns[0], K, workspace=wsp)
         elif entry == "packed":
             outs = ops.qgemv_packed(qt, W, codes, scales, M, list(Ns), K)
         elif entry == "prefill":
@@ -110,14 +112,22 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
         u = orc.gemv_exact(raw_qt, wu[idx], a, M, len(idx), K)
         with np.errstate(over="ignore"):
             h_ref = g / (1.0 + np.exp(-g)) * u
-        check_rows(down(h)[:, idx], h_ref)
+        if want[0].startswith("k_gemv_dq<"):  # fp16 weights: the GEMV bar carried through h
+            check_h_propagated(down(h)[:, idx], g, u)
+        else:
+            check_rows(down(h)[:, idx], h_ref)
         # the Q8_1 blocks are the exact quantization of the device's h
         assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
         # the chain it replaces: grouped GEMV + SiLU producer, bit for bit
         # where the grouped launch forms the sums in the same order
+        wsg = None
+        if wsp is not None:
+            nbg = ops.qgemv_workspace_bytes(qt, [N, N], M, K)
+            wsg = torch.zeros(max(nbg, 256), dtype=torch.uint8, device=dev)
         with ops.launch_log() as lg2:
-            g2, u2 = ops.qgemv_grouped(qt, [W[0], Wu], A, M, [N, N], K)
-        if entry == "gate_up_silu_rmsnorm" or same_slot_waves(lg2.kernels[-1], want[0]):
+            g2, u2 = ops.qgemv_grouped(qt, [W[0], Wu], A, M, [N, N], K, workspace=wsg)
+        same_dq = lg2.kernels[-1].startswith("k_gemv_dq<") and want[0].startswith("k_gemv_dq<")
+        if entry == "gate_up_silu_rmsnorm" or same_dq or same_slot_waves(lg2.kernels[-1], want[0]):
             assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
         return
 

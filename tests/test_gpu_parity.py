@@ -41,6 +41,22 @@ def note(msg):
     print(msg, flush=True)
 
 
+def check_h_propagated(h, g, u, tol=1e-3):
+    """h = silu(g) * u from two GEMV outputs, each held to the contract's
+    tol * ||row||_2: the bar on h is that error carried through the product,
+    |dh| <= |silu'(g) u| tol ||g_row|| + |silu(g)| tol ||u_row||.  (A row of h
+    dominated by one element can exceed tol * ||h_row|| with g and u inside
+    their own bars: the fp16-dequant GEMV rounds each weight to fp16.)"""
+    with np.errstate(over="ignore"):
+        sg = 1.0 / (1.0 + np.exp(-g))
+    dsilu = sg * (1.0 + g * (1.0 - sg))
+    eg = tol * np.linalg.norm(g, axis=1, keepdims=True)
+    eu = tol * np.linalg.norm(u, axis=1, keepdims=True)
+    bound = np.abs(dsilu * u) * eg + np.abs(g * sg) * eu + eg * eu
+    err = np.abs(np.asarray(h, np.float64) - g * sg * u)
+    assert np.all(err <= bound), f"max err / bound {(err / bound).max()}"
+
+
 def same_slot_waves(grouped, fused):
     """True when a grouped launch and the fused gate/up/SiLU launch are both
     slot-packed MFMA GEMVs with the same waves per projection (the third

@@ -6,7 +6,8 @@ the dispatch runs the same kernel and split on both."""
 import numpy as np
 import pytest
 
-from tests.test_gpu_parity import check_q8_1_close, check_rows, down, note, same_slot_waves, up
+from tests.test_gpu_parity import (check_h_propagated, check_q8_1_close, check_rows, down, note,
+                                   same_slot_waves, up)
 
 pytestmark = pytest.mark.gpu
 
@@ -166,22 +167,6 @@ def test_gate_up_silu_tiled(orc, dev, qtype, M):
             assert np.array_equal(down(q), down(ops.silu_mul_quantize_q8_1(g2, u2)))
 
 
-def _check_h_propagated(h, g, u, tol=1e-3):
-    """h = silu(g) * u from two GEMV outputs, each held to the contract's
-    tol * ||row||_2: the bar on h is that error carried through the product,
-    |dh| <= |silu'(g) u| tol ||g_row|| + |silu(g)| tol ||u_row||.  (A row of h
-    dominated by one element can exceed tol * ||h_row|| with g and u inside
-    their own bars: the fp16-dequant GEMV rounds each weight to fp16.)"""
-    with np.errstate(over="ignore"):
-        sg = 1.0 / (1.0 + np.exp(-g))
-    dsilu = sg * (1.0 + g * (1.0 - sg))
-    eg = tol * np.linalg.norm(g, axis=1, keepdims=True)
-    eu = tol * np.linalg.norm(u, axis=1, keepdims=True)
-    bound = np.abs(dsilu * u) * eg + np.abs(g * sg) * eu + eg * eu
-    err = np.abs(np.asarray(h, np.float64) - g * sg * u)
-    assert np.all(err <= bound), f"max err / bound {(err / bound).max()}"
-
-
 @pytest.mark.parametrize("qtype,tiled,M,N,K", [(Q4_K, True, 17, 512, 1024), (Q4_K, True, 32, 1056, 5120),
                                                 (Q6_K, True, 24, 512, 2048), (Q4_K, False, 32, 512, 5120),
                                                 (Q8_0, False, 20, 256, 2048), (Q4_K, False, 12, 256, 2048)])
@@ -211,7 +196,7 @@ def test_gate_up_silu_dq(orc, dev, qtype, tiled, M, N, K):
         assert lg.kernels[0].endswith(f",{int(tiled)},1>")
         g = orc.gemv_exact(qtype, wg, a, M, N, K)
         u = orc.gemv_exact(qtype, wu, a, M, N, K)
-        _check_h_propagated(down(h), g, u)
+        check_h_propagated(down(h), g, u)
         assert np.array_equal(down(q), orc.quantize_q8_1(down(h)))
     nbg = ops.qgemv_workspace_bytes(tt, [N, N], M, K)
     wsg = torch.zeros(max(nbg, 256), dtype=torch.uint8, device=dev)
