@@ -138,8 +138,10 @@ class FusedQuantGemm {
   // fused_quant_gemm.h:281-307: silu(gate . a) * (up . a) in one launch, fp16
   // out; the WithEpilogue variant also writes the Q8_1 blocks of the result
   // (act_q8_1_out, may be null) for the down projection.  N % 32 == 0 and
-  // M <= 2, or 3 <= M <= 8 for Q4_K / Q6_K with K % 256 == 0 (else false:
-  // grouped GEMV + SiluMulQuantizeQ8_1).
+  // M <= 2, 3 <= M <= 8 for Q4_K / Q6_K with K % 256 == 0, and up to M = 32
+  // (Q4_K / Q6_K / Q8_0) where the fp16-dequant GEMV needs no K split (else
+  // false: grouped GEMV + SiluMulQuantizeQ8_1, or ifx_qgemv_gate_up_silu_ws
+  // with a workspace).
   static bool FusedGateUpSiluGemvQ8_1(const QuantizedWeightInfo &gate_raw,
                                       const QuantizedWeightInfo &up_raw, const void *act_q8_1,
                                       uint16_t *output, int M, int N, int K, hipStream_t stream);
