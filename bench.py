@@ -620,6 +620,20 @@ def main():
                 us = time_loop(lambda i, n=l[0]: run(i, n), steps, 5)
                 q4[f"{l[0]}_M{M}"] = {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1),
                                       "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+            if M == 1:
+                # the gate/up pair on packed (per-row symmetric int8) activations
+                qt, N, K, greps = layer14["gate"]
+                ureps = layer14["up"][3]
+                x = torch.from_numpy(synth.activations(1, K, seed=51)).to(dev)
+                codes, scales = ops.quantize_rows_symmetric(x)
+                outs = [torch.empty((1, N), dtype=torch.float16, device=dev) for _ in range(2)]
+                us = time_loop(lambda i: ops.qgemv_packed(qt, [greps[i % len(greps)],
+                                                              ureps[i % len(ureps)]],
+                                                          codes, scales, 1, [N, N], K, outs=outs),
+                               steps, 5)
+                nb = 2 * ops.weight_bytes(qt, N, K) + K + 4 + 2 * N * 2
+                q4["gate_up_M1_packed"] = {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1),
+                                           "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
         c4["q4k_launches_M1_M8"] = q4
         extras["config4_qwen14b_layer"] = c4
         del layer14
