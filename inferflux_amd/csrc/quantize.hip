@@ -116,7 +116,31 @@ __device__ __forceinline__ float row_value(const void *a, const void *b, int64_t
   else return load_dt<DT>(a, i);
 }
 
+// Four consecutive values (element i, i % 4 == 0) with one 16- or 8-byte load.
+template <int DT>
+__device__ __forceinline__ f32x4 load4_dt(const void *p, int64_t i) {
+  if constexpr (DT == 0) return ldg<f32x4>(static_cast<const float *>(p) + i);
+  const u32x2 v = ldg<u32x2>(static_cast<const uint16_t *>(p) + i);
+  if constexpr (DT == 1)
+    return f32x4{h2f(v.x & 0xFFFFu), h2f(v.x >> 16), h2f(v.y & 0xFFFFu), h2f(v.y >> 16)};
+  else
+    return f32x4{__builtin_bit_cast(float, v.x << 16), __builtin_bit_cast(float, v.x & 0xFFFF0000u),
+                 __builtin_bit_cast(float, v.y << 16), __builtin_bit_cast(float, v.y & 0xFFFF0000u)};
+}
+
 template <int DT, bool SILU>
+__device__ __forceinline__ f32x4 row_value4(const void *a, const void *b, int64_t i) {
+  if constexpr (SILU) return silu_mul4(load4_dt<DT>(a, i), load4_dt<DT>(b, i));
+  else return load4_dt<DT>(a, i);
+}
+
+__device__ __forceinline__ int sym_code(float y, float inv) {
+  return static_cast<int>(fminf(fmaxf(rintf(y * inv), -127.0f), 127.0f));
+}
+
+// V4: K % 4 == 0, four values per thread and load (the same per-element
+// arithmetic, so the same codes and scale).
+template <int DT, bool SILU, bool V4>
 __global__ __launch_bounds__(256) void k_quantize_rows_sym(const void *__restrict__ a,
                                                            const void *__restrict__ b,
                                                            int8_t *__restrict__ codes,
@@ -125,7 +149,14 @@ __global__ __launch_bounds__(256) void k_quantize_rows_sym(const void *__restric
   const int64_t base = static_cast<int64_t>(blockIdx.x) * K;
   const int tid = threadIdx.x;
   float mx = 0.0f;
-  for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(row_value<DT, SILU>(a, b, base + i)));
+  if constexpr (V4) {
+    for (int i = 4 * tid; i < K; i += 1024) {
+      const f32x4 v = row_value4<DT, SILU>(a, b, base + i);
+      mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+    }
+  } else {
+    for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(row_value<DT, SILU>(a, b, base + i)));
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
@@ -134,9 +165,18 @@ __global__ __launch_bounds__(256) void k_quantize_rows_sym(const void *__restric
   const float scale = amax > 0.0f ? amax / 127.0f : 0.0f;
   const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
   if (tid == 0) scales[blockIdx.x] = scale;
-  for (int i = tid; i < K; i += 256) {
-    const float q = rintf(row_value<DT, SILU>(a, b, base + i) * inv);
-    codes[base + i] = static_cast<int8_t>(static_cast<int>(fminf(fmaxf(q, -127.0f), 127.0f)));
+  if constexpr (V4) {
+    for (int i = 4 * tid; i < K; i += 1024) {
+      const f32x4 v = row_value4<DT, SILU>(a, b, base + i);
+      const uint32_t w = (static_cast<uint32_t>(sym_code(v.x, inv)) & 0xFFu) |
+                         ((static_cast<uint32_t>(sym_code(v.y, inv)) & 0xFFu) << 8) |
+                         ((static_cast<uint32_t>(sym_code(v.z, inv)) & 0xFFu) << 16) |
+                         (static_cast<uint32_t>(sym_code(v.w, inv)) << 24);
+      *reinterpret_cast<uint32_t *>(codes + base + i) = w;
+    }
+  } else {
+    for (int i = tid; i < K; i += 256)
+      codes[base + i] = static_cast<int8_t>(sym_code(row_value<DT, SILU>(a, b, base + i), inv));
   }
 }
 
@@ -144,17 +184,24 @@ hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int
                                     float *scales, int M, int K, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const dim3 grid(M), block(256);
-#define IFX_QRS(DT)                                                                         \
-  do {                                                                                      \
-    if (b) IFX_LAUNCH(k_quantize_rows_sym, (DT, true), grid, block, 0, stream, a, b, codes, \
-                      scales, K);                                                           \
-    else IFX_LAUNCH(k_quantize_rows_sym, (DT, false), grid, block, 0, stream, a, b, codes,  \
-                    scales, K);                                                             \
+  const bool v4 = K % 4 == 0;
+#define IFX_QRS2(DT, V4)                                                                        \
+  do {                                                                                          \
+    if (b) IFX_LAUNCH(k_quantize_rows_sym, (DT, true, V4), grid, block, 0, stream, a, b, codes, \
+                      scales, K);                                                               \
+    else IFX_LAUNCH(k_quantize_rows_sym, (DT, false, V4), grid, block, 0, stream, a, b, codes,  \
+                    scales, K);                                                                 \
+  } while (0)
+#define IFX_QRS(DT)                 \
+  do {                              \
+    if (v4) IFX_QRS2(DT, true);     \
+    else IFX_QRS2(DT, false);       \
   } while (0)
   if (dtype == 0) IFX_QRS(0);
   else if (dtype == 1) IFX_QRS(1);
   else IFX_QRS(2);
 #undef IFX_QRS
+#undef IFX_QRS2
   return last_error();
 }
 
