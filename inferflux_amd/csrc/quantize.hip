@@ -180,11 +180,72 @@ __global__ __launch_bounds__(256) void k_quantize_rows_sym(const void *__restric
   }
 }
 
+// K % 4 == 0 and K <= 16384: 1024 threads, the row's values (SiLU products
+// included) computed once into registers, the maximum over the 16 waves in
+// LDS, the codes from the registers: one read of the inputs, one exp per
+// element.  Same per-element arithmetic as k_quantize_rows_sym.
+template <int DT, bool SILU>
+__global__ __launch_bounds__(1024) void k_quantize_rows_sym_reg(const void *__restrict__ a,
+                                                                const void *__restrict__ b,
+                                                                int8_t *__restrict__ codes,
+                                                                float *__restrict__ scales, int K) {
+  constexpr int kNit = 4;  // 4 x 4 values per thread
+  __shared__ float wmax[16];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * K;
+  const int tid = threadIdx.x;
+  f32x4 v[kNit];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kNit; ++j) {
+    const int i = 4 * tid + 4096 * j;
+    if (i < K) {
+      v[j] = row_value4<DT, SILU>(a, b, base + i);
+      mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+  float amax = wmax[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) amax = fmaxf(amax, wmax[w]);
+  const float scale = amax > 0.0f ? amax / 127.0f : 0.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  if (tid == 0) scales[blockIdx.x] = scale;
+#pragma unroll
+  for (int j = 0; j < kNit; ++j) {
+    const int i = 4 * tid + 4096 * j;
+    if (i < K) {
+      const uint32_t w = (static_cast<uint32_t>(sym_code(v[j].x, inv)) & 0xFFu) |
+                         ((static_cast<uint32_t>(sym_code(v[j].y, inv)) & 0xFFu) << 8) |
+                         ((static_cast<uint32_t>(sym_code(v[j].z, inv)) & 0xFFu) << 16) |
+                         (static_cast<uint32_t>(sym_code(v[j].w, inv)) << 24);
+      *reinterpret_cast<uint32_t *>(codes + base + i) = w;
+    }
+  }
+}
+
 hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int8_t *codes,
                                     float *scales, int M, int K, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const dim3 grid(M), block(256);
   const bool v4 = K % 4 == 0;
+  if (v4 && K <= 16384) {
+    const dim3 rblock(1024);
+#define IFX_QRSR(DT)                                                                             \
+  do {                                                                                           \
+    if (b) IFX_LAUNCH(k_quantize_rows_sym_reg, (DT, true), grid, rblock, 0, stream, a, b, codes, \
+                      scales, K);                                                                \
+    else IFX_LAUNCH(k_quantize_rows_sym_reg, (DT, false), grid, rblock, 0, stream, a, b, codes,  \
+                    scales, K);                                                                  \
+  } while (0)
+    if (dtype == 0) IFX_QRSR(0);
+    else if (dtype == 1) IFX_QRSR(1);
+    else IFX_QRSR(2);
+#undef IFX_QRSR
+    return last_error();
+  }
 #define IFX_QRS2(DT, V4)                                                                        \
   do {                                                                                          \
     if (b) IFX_LAUNCH(k_quantize_rows_sym, (DT, true, V4), grid, block, 0, stream, a, b, codes, \
