@@ -76,6 +76,65 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quantize_q8_1(const void *__res
   }
 }
 
+// The same for 2048 < K <= 16384 in one round trip: 1024 threads, each
+// holding 4 x 4 values of the row and of the norm weight in registers.  The
+// sum of squares is formed in the 256-thread kernel's order (the fused
+// RMSNorm GEMVs reproduce that kernel's bits): every thread writes its
+// 4-value terms to LDS, then thread t < 256 adds the terms of elements
+// 4t + 1024j in j order, and the wave / workgroup reductions follow as
+// there.  Bit for bit the 256-thread kernel's output.
+template <bool F16>
+__global__ __launch_bounds__(1024) void k_rmsnorm_quantize_q8_1_wide(const void *__restrict__ x,
+                                                                     const uint16_t *__restrict__ w,
+                                                                     uint8_t *__restrict__ out,
+                                                                     int K, float eps) {
+  constexpr int kNit = 4;
+  __shared__ float terms[4096];  // element group i / 4
+  __shared__ float part[4];
+  const int64_t row = blockIdx.x;
+  uint8_t *orow = out + row * (K >> 5) * kQ8_1Bytes;
+  const int tid = threadIdx.x;
+  f32x4 xr[kNit];
+  u32x2 wr[kNit];
+#pragma unroll
+  for (int j = 0; j < kNit; ++j) {
+    const int i = 4 * tid + 4096 * j;
+    if (i < K) {
+      xr[j] = load4<F16>(x, row * K + i);
+      wr[j] = ldg<u32x2>(w + i);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kNit; ++j) {
+    const int i = 4 * tid + 4096 * j;
+    if (i < K) terms[i >> 2] = xr[j].x * xr[j].x + xr[j].y * xr[j].y + xr[j].z * xr[j].z + xr[j].w * xr[j].w;
+  }
+  __syncthreads();
+  if (tid < 256) {
+    float ss = 0.0f;
+    for (int i = 4 * tid; i < K; i += 4 * 256) ss += terms[i >> 2];
+    ss = wave_sum_to63(ss);
+    if ((tid & 63) == 63) part[tid >> 6] = ss;
+  }
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rms = 1.0f / __builtin_sqrtf(total / static_cast<float>(K) + eps);
+  const int l = tid & 7;
+#pragma unroll
+  for (int j = 0; j < kNit; ++j) {
+    const int i = 4 * tid + 4096 * j;  // = 32 * block + 4 * l; whole blocks (K % 32 == 0)
+    if (i < K) {
+      const f32x4 v = xr[j];
+      const u32x2 wv = wr[j];
+      const float y0 = materialize_f32(v.x * rms) * h2f(wv.x & 0xFFFFu);
+      const float y1 = materialize_f32(v.y * rms) * h2f(wv.x >> 16);
+      const float y2 = materialize_f32(v.z * rms) * h2f(wv.y & 0xFFFFu);
+      const float y3 = materialize_f32(v.w * rms) * h2f(wv.y >> 16);
+      quantize4_store(y0, y1, y2, y3, orow + (i >> 5) * kQ8_1Bytes, l);
+    }
+  }
+}
+
 // SiLU(gate) * up then Q8_1 (fused_dequant_gemv.cuh:657-734):
 // y = (g / (1 + exp(-g))) * u, 8 lanes per Q8_1 block.
 template <bool F16>
@@ -269,6 +328,15 @@ hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int
 hipError_t launch_rmsnorm_quantize_q8_1(const void *x, bool f16, const uint16_t *w, void *out,
                                         int M, int K, float eps, hipStream_t stream) {
   if (M == 0) return hipSuccess;
+  if (K > 2048 && K <= 16384) {
+    if (f16)
+      IFX_LAUNCH(k_rmsnorm_quantize_q8_1_wide, (true), dim3(M), dim3(1024), 0, stream, x, w,
+                 static_cast<uint8_t *>(out), K, eps);
+    else
+      IFX_LAUNCH(k_rmsnorm_quantize_q8_1_wide, (false), dim3(M), dim3(1024), 0, stream, x, w,
+                 static_cast<uint8_t *>(out), K, eps);
+    return last_error();
+  }
   if (f16)
     IFX_LAUNCH(k_rmsnorm_quantize_q8_1, (true), dim3(M), dim3(256), 0, stream, x, w,
                        static_cast<uint8_t *>(out), K, eps);
