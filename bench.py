@@ -52,7 +52,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile", default=None, metavar="FORM:LAUNCH",
                    help="profiling run: eager launches of one launch of a 3B layer form "
-                        "(e.g. ffn_block:ffn, fused_norm_swiglu:gate_up), the HBM read probe "
+                        "(e.g. fused_norm_swiglu:gate_up), the HBM read probe "
                         "at its byte count and a copy of known size for counter calibration")
     p.add_argument("--profile-kernels", action="store_true",
                    help="profiling run of the batch kernels: the 32B prefill GEMMs (fp16 and "
@@ -171,9 +171,6 @@ def main():
         fused == "swiglu": in addition gate/up computes SiLU(gate)*up and
         writes its Q8_1 blocks for down itself
         (ifx_qgemv_gate_up_silu_rmsnorm): 4 launches, no producer.
-        fused == "ffn": QKV with the fused RMSNorm, then ifx_decode_ffn: O
-        with the fused quantizer and one grid-synchronised launch for
-        RMSNorm, gate/up + SiLU and down (M = 1): 3 launches.
         fused == "batch_swiglu" (M <= 8; tiled copies M <= 32): the Q8_1
         producers as launches of their own, except SiLU * up + Q8_1, which the
         gate/up launch computes (ifx_qgemv_gate_up_silu, with the workspace
@@ -184,7 +181,7 @@ def main():
         (M <= 32).  ordered: K-split launches reduce in split order through a
         workspace per launch (ifx_qgemv_ws / ifx_qgemv_grouped_ws).
         run(i, which) runs one launch kind alone ("qkv", "o", "gate_up",
-        "down", "producers"; "ffn": the FFN kernel of the "ffn" form alone)."""
+        "down", "producers")."""
         if tiled is not None:
             layer = tiled
         hidden, q_dim, ffn = layer["q"][2], layer["o"][2], layer["down"][2]
@@ -218,9 +215,6 @@ def main():
             nb = ops.gate_up_silu_workspace_bytes(qt_, M, N_, K_)
             if nb:
                 wsd["gate_up_silu"] = torch.zeros(nb, dtype=torch.uint8, device=dev)
-        ws = None
-        if fused == "ffn":
-            ws = torch.zeros(ops.decode_ffn_workspace_bytes(M, ffn), dtype=torch.uint8, device=dev)
 
         def gemv(lname, r):
             _, projs, src, accum = launches[lname]
@@ -245,23 +239,8 @@ def main():
                                       outs=[Y[p] for p in projs],
                                       mode=ops.ACCUM if accum else ops.STORE)
 
-        def ffn_block(r, with_o=True):
-            ops.decode_ffn(layer["o"][3][r] if with_o else None, attn, resid, norm_w["ffn"],
-                           layer["gate"][3][r], layer["up"][3][r], layer["down"][3][r], hidden,
-                           q_dim, ffn, ws)
-
         def run(i, which=None):
             r = i % R
-            if fused == "ffn":
-                if which is None or which == "qkv":
-                    gemv_norm("qkv", r, resid, norm_w["attn"])
-                if which is None:
-                    ffn_block(r)
-                elif which == "o":
-                    gemv_norm("o", r, attn, None)
-                elif which == "ffn":
-                    ffn_block(r, with_o=False)
-                return
             if fused == "batch_swiglu":
                 prod = which is None or which == "producers"
                 if prod:
@@ -326,19 +305,16 @@ def main():
             return {l[0]: launch_bytes(layer, l[0], M)[1] for l in workloads.DECODE_LAUNCHES}
         out = {"qkv": wb["q"] + wb["k"] + wb["v"] + M * hidden * 4 + hidden * 2 + M * qkv_n * 4,
                "o": wb["o"] + M * q_dim * 4 + M * hidden * 4}
-        if form == "ffn":
-            out["ffn"] = wb["gate"] + wb["up"] + wb["down"] + 2 * M * hidden * 4 + hidden * 2
-        else:
-            out["gate_up"] = (wb["gate"] + wb["up"] + M * hidden * 4 + hidden * 2 +
-                              (a(ffn) if form == "swiglu" else 2 * M * ffn * 4))
-            out["down"] = wb["down"] + a(ffn) + M * hidden * 4
+        out["gate_up"] = (wb["gate"] + wb["up"] + M * hidden * 4 + hidden * 2 +
+                          (a(ffn) if form == "swiglu" else 2 * M * ffn * 4))
+        out["down"] = wb["down"] + a(ffn) + M * hidden * 4
         return out
 
     if args.profile:
         # eager launches of one launch of a 3B layer form, for rocprofv3
         form, kind = args.profile.split(":")
         fused = {"reference": False, "fused_norm": True, "fused_norm_swiglu": "swiglu",
-                 "fused_norm_swiglu_split_down": "swiglu", "ffn_block": "ffn"}[form]
+                 "fused_norm_swiglu_split_down": "swiglu"}[form]
         projs3b = workloads.QWEN3B_LAYER
         R3 = n_replicas(layer_bytes(projs3b))
         layer3b = make_layer(projs3b, seed=1, replicas=R3)
@@ -346,7 +322,7 @@ def main():
                                   split_down=form.endswith("split_down"))
         profile_run(args, dev, lambda i: run(i, kind), f"{form}:{kind}",
                     form_kernel_bytes(layer3b, 1, {False: "reference", True: "norm",
-                                                   "swiglu": "swiglu", "ffn": "ffn"}[fused])[kind])
+                                                   "swiglu": "swiglu"}[fused])[kind])
         return
 
     result = {}
@@ -418,15 +394,13 @@ def main():
             for form, fused, kinds in (("fused_norm", True, ("qkv", "o", "gate_up", "down")),
                                        ("fused_norm_swiglu", "swiglu", ("qkv", "o", "gate_up", "down")),
                                        ("fused_norm_swiglu_split_down", "swiglu",
-                                        ("qkv", "o", "gate_up", "down")),
-                                       ("ffn_block", "ffn", ("qkv", "o", "ffn"))):
+                                        ("qkv", "o", "gate_up", "down"))):
                 runf = decode_layer_runner(layer3b, M, seed=10 + M, fused=fused,
                                            split_down=form.endswith("split_down"))
                 us_f = time_loop(runf, steps, args.warmup)
                 kus = {n: time_loop(lambda i, n=n: runf(i, n), steps, args.warmup) for n in kinds}
                 fb = form_kernel_bytes(layer3b, M, {"fused_norm": "norm", "fused_norm_swiglu": "swiglu",
-                                                    "fused_norm_swiglu_split_down": "swiglu",
-                                                    "ffn_block": "ffn"}[form])
+                                                    "fused_norm_swiglu_split_down": "swiglu"}[form])
                 fb = {k: fb[k] for k in kinds}
                 forms[form] = (runf, us_f, kus, fb)
                 per_m[M][form] = {
@@ -443,7 +417,6 @@ def main():
         "fused_norm_swiglu": "producers fused and SiLU*up + Q8_1 in the gate/up epilogue (4 launches)",
         "fused_norm_swiglu_split_down": "as fused_norm_swiglu, with the down projection on a "
                                         "row-split copy of its Q6_K weights (ifx_repack)",
-        "ffn_block": "QKV with the fused RMSNorm, O, and one grid-synchronised FFN launch (3 launches)",
     }
     step_form = min(forms, key=lambda f: forms[f][1])
     step_run, step_us, step_kus, step_kbytes = forms[step_form]
@@ -747,9 +720,25 @@ def profile_traffic(kernel):
     return None, "no counter summary for " + kernel + " under profiles/"
 
 
+PROBE_LIB = os.path.join(ROOT, "libbench_probe.so")
+
+
+def build_probe():
+    """Builds the benchmark's bandwidth probes (bench_probe.hip: a plain
+    streaming read and a copy of known size, for the read-rate line and the
+    counter calibration; not part of the library)."""
+    import subprocess
+    tmp = PROBE_LIB + ".tmp"
+    subprocess.run([os.environ.get("HIPCC", "/opt/rocm/bin/hipcc"), "--offload-arch=gfx950", "-O3",
+                    "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", "-o", tmp, os.path.join(ROOT, "bench_probe.hip")],
+                   check=True, capture_output=True)
+    os.replace(tmp, PROBE_LIB)
+
+
 def probe_lib():
     import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "inferflux_amd", "libifx_probe.so"))
+    lib = ctypes.CDLL(PROBE_LIB)
     for fn in (lib.ifx_probe_read, lib.ifx_probe_copy):
         fn.restype = ctypes.c_int
     lib.ifx_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,

@@ -1,4 +1,4 @@
-// probe.hip -- bandwidth probes for the benchmark harness (not part of the
+// bench_probe.hip -- bandwidth probes for the benchmark harness (not part of the
 // quantized GEMV/GEMM C ABI): a streaming read and a streaming copy with
 // 16-byte lanes, used to measure what HBM delivers at a given transfer size
 // and to calibrate the rocprofv3 FETCH_SIZE / WRITE_SIZE counters.

@@ -274,46 +274,6 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
                          int out_dtype, int mode, const void *bias, int M, int N, int K,
                          void *workspace, int64_t workspace_bytes, void *stream);
 
-/* Bytes of workspace ifx_decode_ffn needs: a 2048-byte control block, then
- * 8 copies of h = silu(gate) * up in fp32 (M x ffn values, each copy padded
- * to a multiple of 256 bytes). */
-int64_t ifx_decode_ffn_workspace_bytes(int M, int ffn);
-
-/* The post-attention half of a decode layer at M = 1 in two launches:
- *   residual += W_o . Q8_1(attn)                      (O, accumulate)
- *   a = Q8_1(RMSNorm(residual) * ffn_norm_weight)
- *   h = silu(W_gate . a) * (W_up . a), as Q8_1 blocks in the workspace
- *   residual += W_down . h                            (down, accumulate)
- * Replaces the launch sequence of transformer_forward.cu:726-817
- * (GemvQ8_1AccumF32 for O, FusedRmsNormQuantizeQ8_1,
- * FusedGateUpSiluGemvQ8_1WithEpilogue, GemvQ8_1AccumF32 for down), and
- * leaves the residual bit for bit equal to that chain's (here:
- * ifx_qgemv_grouped_rmsnorm with norm_weight NULL in IFX_ACCUM mode,
- * ifx_qgemv_gate_up_silu_rmsnorm, ifx_qgemv in IFX_ACCUM mode).
- * W_o NULL skips the O launch (attn is then not read): for callers whose
- * residual already holds the attention block's output.
- * Types: W_o, W_gate, W_up Q4_K, W_down Q6_K (the Q4_K_M mix); attn [q_dim]
- * fp32 or fp16 (attn_dtype IFX_OUT_F32 / IFX_OUT_F16); residual [hidden]
- * fp32; norm weight [hidden] fp16.  Covered shapes: M = 1, q_dim and hidden
- * multiples of 256 up to 2048, ffn a multiple of 256 up to 16384, and the
- * down rows of a workgroup within 12 waves (Qwen2.5-3B: 2048 / 11008 on 256
- * CUs); other shapes return IFX_BAD_GEOMETRY (use the chain).
- * The first launch is O (the GEMV with the fused quantizer); the second
- * does everything after it, one workgroup per compute unit, all resident
- * together, with one grid barrier in the workspace (256-byte aligned, at least
- * ifx_decode_ffn_workspace_bytes).  Its control block (bytes 0..2047) must
- * be zero before the first call; the kernel leaves it ready for the next
- * call.  Bytes 16..23 may hold an int64 wait limit in 100 MHz ticks (0: one
- * second).  A barrier that waits longer records a failure: the uint32 at
- * byte 8 becomes nonzero, the results are not valid, and the control block
- * must be zeroed again before the next call.  Calls sharing a workspace
- * must not overlap. */
-int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype, int q_dim,
-                   float *residual, const uint16_t *ffn_norm_weight, float eps, int gate_up_type,
-                   const void *W_gate, const void *W_up, int ffn, int down_type,
-                   const void *W_down, int M, int hidden, void *workspace,
-                   int64_t workspace_bytes, void *stream);
-
 /* Size of the library's static device scratch (per GPU, held until the
  * process ends) that ifx_qgemm_prefill_noalloc uses as its workspace. */
 #define IFX_NOALLOC_SCRATCH_BYTES (16 << 20)
@@ -388,6 +348,41 @@ int64_t ifx_tiled_bytes(int quant_type, int64_t n_rows, int K);
  * fused_quant_gemm.h:213-234, fused_quant_gemm.cu:573-596, 1966-2032). */
 int ifx_repack_tiled(int quant_type, const void *W, void *W_out, int64_t n_rows, int K,
                      void *stream);
+
+/* The down-projection MMQ layout: one caller-owned allocation holding
+ *   - at offset 0, the tiled copy of rows x cols Q4_K / Q6_K / Q8_0 weights
+ *     (ifx_repack_tiled);
+ *   - at ifx_mmq_layout_rows_offset (256-byte aligned), a row-major copy for
+ *     the M <= 2 GEMV: the row-split copy (ifx_repack) of Q6_K / Q8_0, the
+ *     raw rows of Q4_K;
+ *   - at ifx_mmq_layout_ws_offset, the ordered-split workspace of the tiled
+ *     launches (zeroed by ifx_mmq_layout_build; every launch leaves it zero).
+ * ifx_qgemv_mmq then runs every M in 1..32 on the faster of the two copies
+ * (measured on MI355X, 3B down 2048 x 11008 Q6_K: M = 1 6.5 against 7.0 us
+ * raw; M = 8 8.2 against 12.4 us raw).  ifx_mmq_layout_bytes: 0 for another
+ * type or cols % 256 != 0.  Replaces the copy FusedQuantGemm::
+ * BuildDownProjMmqLayout writes (fused_quant_gemm.h:222-224,
+ * fused_quant_gemm.cu:573-596, 1966-2026), whose 8-row tile is a layout of
+ * the reference's own CUDA kernel. */
+int64_t ifx_mmq_layout_bytes(int quant_type, int64_t rows, int cols);
+int64_t ifx_mmq_layout_rows_offset(int quant_type, int64_t rows, int cols);
+int64_t ifx_mmq_layout_ws_offset(int quant_type, int64_t rows, int cols);
+/* Writes the layout from raw GGUF rows W into `layout` (ifx_mmq_layout_bytes,
+ * 256-byte aligned), stream ordered.  Allocates nothing. */
+int ifx_mmq_layout_build(int quant_type, const void *W, void *layout, int64_t rows, int cols,
+                         void *stream);
+/* Y (op)= W . a on a layout of N x K weights (quant_type: the GGUF id of the
+ * raw weights), 1 <= M <= 32: M <= 2 the v_dot4 GEMV on the row-major copy,
+ * 3 <= M <= 32 the batch kernels on the tiles; mode IFX_STORE or IFX_ACCUM.
+ * Where the tiled launch splits K over workgroups, ordered != 0 adds the
+ * splits in split order through the layout's workspace (bits identical run
+ * to run, as ifx_qgemv_ws) and ordered == 0 with fp32 atomics (as
+ * ifx_qgemv); fp16 outputs always take the ordered reduction.  Launches
+ * that use the layout's workspace must not overlap (one stream, or the
+ * caller's ordering).  Replaces FusedQuantGemm::DownProjMmq
+ * (fused_quant_gemm.h:213-216, fused_quant_gemm.cu:2034-2080). */
+int ifx_qgemv_mmq(int quant_type, const void *layout, const void *A_q8_1, void *Y, int out_dtype,
+                  int mode, int M, int N, int K, int ordered, void *stream);
 
 /* Whole-tensor dequantization of n_rows x K weights to fp32 or fp16.
  * Replaces dequantize_q4_k / dequantize_q6_k / dequantize_q8_0

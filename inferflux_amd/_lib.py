@@ -33,9 +33,6 @@ SIGNATURES = {
     "ifx_qgemv_gate_up_silu_rmsnorm": ([_i32, _vp, _vp, _vp, _i32, _vp, ctypes.c_float, _vp, _i32, _vp, _i32,
                                         _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_noalloc": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
-    "ifx_decode_ffn_workspace_bytes": ([_i32, _i32], _i64),
-    "ifx_decode_ffn": ([_i32, _vp, _vp, _i32, _i32, _vp, _vp, ctypes.c_float, _i32, _vp, _vp, _i32,
-                        _i32, _vp, _i32, _i32, _vp, _i64, _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_repacked_bytes": ([_i32, _i64, _i32], _i64),
@@ -46,6 +43,11 @@ SIGNATURES = {
                               _vp], _i32),
     "ifx_qgemv_workspace_bytes": ([_i32, _i32, _vp, _i32, _i32, _i32], _i64),
     "ifx_repack_tiled": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
+    "ifx_mmq_layout_bytes": ([_i32, _i64, _i32], _i64),
+    "ifx_mmq_layout_rows_offset": ([_i32, _i64, _i32], _i64),
+    "ifx_mmq_layout_build": ([_i32, _vp, _vp, _i64, _i32, _vp], _i32),
+    "ifx_mmq_layout_ws_offset": ([_i32, _i64, _i32], _i64),
+    "ifx_qgemv_mmq": ([_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_dequantize": ([_i32, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ifx_kernel_family": ([_i32, _i32, _i32, _i32], _i32),
     "ifx_launch_log_begin": ([_i32], None),

@@ -12,7 +12,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libifx_qgemm.so")
-PROBE_LIB = os.path.join(HERE, "libifx_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = [
@@ -20,10 +19,14 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + os.path.join(HERE, "..", "include"),
 ]
+# IFX_TUNING=1 at build time compiles in the IFX_* environment overrides of
+# the dispatch and launch geometry (tuning sweeps only; see ifx_common.h).
+if os.environ.get("IFX_TUNING") == "1":
+    COMMON.append("-DIFX_TUNING")
 # Bit-exact kernels: no fp contraction anywhere in these translation units.
 EXACT = {"quantize.hip", "dequant.hip"}
-SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "mmvq.hip", "gemm_mfma.hip", "gemv_lds.hip", "gemv_slot.hip", "gemm_f16.hip", "gemv_dq.hip", "layer.hip", "packed.hip",
-           "../host/fused_quant_gemm.cpp", "../host/gguf.cpp", "../host/gguf_model.cpp"]
+SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "mmvq.hip", "gemm_mfma.hip", "gemv_lds.hip", "gemv_slot.hip", "gemm_f16.hip", "gemv_dq.hip", "packed.hip",
+           "../host/fused_quant_gemm.cpp", "../host/native_dispatch.cpp", "../host/gguf.cpp", "../host/gguf_model.cpp"]
 
 
 def _run(cmd):
@@ -59,10 +62,6 @@ def build(verbose=True):
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
     os.replace(tmp, LIB)
-    # bandwidth probes used only by the benchmark harness
-    tmp = PROBE_LIB + ".tmp"
-    _run([HIPCC] + COMMON + ["-shared", "-o", tmp, os.path.join(CSRC, "probe.hip")])
-    os.replace(tmp, PROBE_LIB)
     if verbose:
         print("built", LIB)
     return LIB

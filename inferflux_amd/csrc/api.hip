@@ -12,6 +12,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include <string>
 
 namespace ifx {
@@ -64,11 +66,6 @@ hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, in
                          hipStream_t stream);
 hipError_t launch_repack_tiled(int qtype, const void *W, void *out, int64_t n_rows, int K,
                                hipStream_t stream);
-bool decode_ffn_fits(int hidden, int ffn);
-hipError_t launch_decode_ffn(const void *Wo, const void *attn, bool attn_f16, float *resid,
-                             const uint16_t *norm_w, float eps, const void *Wg, const void *Wu,
-                             const void *Wd, void *workspace, int q_dim, int hidden, int ffn,
-                             hipStream_t s);
 bool gemv_slot_fits(int qtype, int M, int K);
 int gemv_dq_swiglu_splits(int M, int N, int K);
 hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
@@ -146,7 +143,7 @@ int min_f16_gemm_m(int qtype) {
 
 bool use_f16_gemm(int qtype, int M, int K) {
   static const int v = [] {
-    const char *e = getenv("IFX_PREFILL");
+    const char *e = ifx::tuning_env("IFX_PREFILL");
     return e ? (e[0] == 'i' ? 1 : e[0] == 'f' ? 2 : 0) : 0;
   }();
   if (!ifx::gemm_f16_fits(qtype, K) || v == 1) return false;
@@ -161,7 +158,7 @@ constexpr int kMaxGemvOnlyM = 64;
 // (tuning; read once).
 int max_gemv_m() {
   static const int v = [] {
-    const char *e = getenv("IFX_GEMV_MAX_M");
+    const char *e = ifx::tuning_env("IFX_GEMV_MAX_M");
     const int n = e ? atoi(e) : 0;
     return (n >= 0 && n <= 8 && e) ? n : kMaxGemvMDefault;
   }();
@@ -174,7 +171,7 @@ int max_gemv_m() {
 // weight byte.  IFX_DECODE=skinny|mmvq forces one (tuning; read once).
 bool use_skinny(int M) {
   static const int v = [] {
-    const char *e = getenv("IFX_DECODE");
+    const char *e = ifx::tuning_env("IFX_DECODE");
     return e ? (e[0] == 's' ? 1 : e[0] == 'm' ? 2 : 0) : 0;
   }();
   return v == 1 || (v == 0 && M > 16);
@@ -187,7 +184,7 @@ bool use_skinny(int M) {
 // IFX_LDS=0|1 forces it off / on for every shape it fits (tuning; read once).
 bool use_lds(int qtype, int M, int K, int n_total) {
   static const int v = [] {
-    const char *e = getenv("IFX_LDS");
+    const char *e = ifx::tuning_env("IFX_LDS");
     return e ? (e[0] == '1' ? 1 : 0) : -1;
   }();
   if (!ifx::gemv_lds_fits(qtype, M, K) || v == 0) return false;
@@ -207,7 +204,7 @@ bool use_lds(int qtype, int M, int K, int n_total) {
 // forces it off / on for every M it fits (1..8; tuning; read once).
 bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
   static const int v = [] {
-    const char *e = getenv("IFX_SLOT");
+    const char *e = ifx::tuning_env("IFX_SLOT");
     return e ? (e[0] == '1' ? 1 : 0) : -1;
   }();
   if (!ifx::gemv_slot_fits(qtype, M, K) || v == 0) return false;
@@ -224,7 +221,7 @@ bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
 // once); IFX_DQ=0 also keeps tiled launches up to M = 16 on the slot kernel.
 int dq_env() {
   static const int v = [] {
-    const char *e = getenv("IFX_DQ");
+    const char *e = ifx::tuning_env("IFX_DQ");
     return e ? (e[0] == '1' ? 1 : 0) : -1;
   }();
   return v;
@@ -343,9 +340,10 @@ int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int o
     return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s, w));
   }
   case Route::Dq: {
-    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;  // tiled weights
     void *w = split_ws(r, ws, ws_bytes, 1, &N, f16, M, K, wrc);
     if (wrc != IFX_OK) return wrc;
+    // tiled weights: fp16 outputs split only through the workspace
+    if (f16 && !w && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;
     return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s, w));
   }
   case Route::Skinny:
@@ -387,9 +385,9 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
                                            mode, s, w));
   }
   case Route::Dq: {
-    if (f16 && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;  // tiled weights
     void *w = split_ws(r, ws, ws_bytes, count, N, f16, M, K, wrc);
     if (wrc != IFX_OK) return wrc;
+    if (f16 && !w && !ifx::gemv_dq_fits_f16(M, K)) return IFX_BAD_GEOMETRY;  // tiled weights
     return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                          mode, 0, s, w));
   }
@@ -799,48 +797,6 @@ int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1,
                                         static_cast<hipStream_t>(stream)));
 }
 
-int64_t ifx_decode_ffn_workspace_bytes(int M, int ffn) {
-  if (M <= 0 || ffn <= 0 || ffn % 32) return 0;
-  return 2048 + 8 * ((static_cast<int64_t>(M) * ffn * 4 + 255) / 256) * 256;
-}
-
-int ifx_decode_ffn(int o_type, const void *W_o, const void *attn, int attn_dtype, int q_dim,
-                   float *residual, const uint16_t *ffn_norm_weight, float eps, int gate_up_type,
-                   const void *W_gate, const void *W_up, int ffn, int down_type,
-                   const void *W_down, int M, int hidden, void *workspace,
-                   int64_t workspace_bytes, void *stream) {
-  if ((W_o && !attn) || !residual || !ffn_norm_weight || !W_gate || !W_up || !W_down ||
-      !workspace)
-    return IFX_NULL_POINTER;
-  if ((W_o && o_type != IFX_TYPE_Q4_K) || gate_up_type != IFX_TYPE_Q4_K ||
-      down_type != IFX_TYPE_Q6_K)
-    return IFX_UNSUPPORTED_TYPE;
-  if (W_o && attn_dtype != IFX_OUT_F32 && attn_dtype != IFX_OUT_F16) return IFX_BAD_GEOMETRY;
-  if (!(eps >= 0.0f) || M != 1) return IFX_BAD_GEOMETRY;
-  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return IFX_BAD_GEOMETRY;
-  if (workspace_bytes < ifx_decode_ffn_workspace_bytes(M, ffn)) return IFX_BAD_GEOMETRY;
-  // the 32-bit range checks of the GEMVs
-  int rc = IFX_OK;
-  if (W_o) {
-    rc = check_gemm_args(o_type, W_o, attn, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M, hidden,
-                         q_dim);
-    // the O launch: the fused-quantizer GEMV's activation tile fits its LDS
-    if (rc == IFX_OK && (q_dim % 256 || ifx::split_row_bytes(q_dim) > 65536))
-      rc = IFX_BAD_GEOMETRY;
-  }
-  if (rc == IFX_OK)
-    rc = check_gemm_args(gate_up_type, W_gate, W_gate, residual, IFX_OUT_F32, IFX_STORE, nullptr,
-                         M, ffn, hidden);
-  if (rc == IFX_OK)
-    rc = check_gemm_args(down_type, W_down, W_down, residual, IFX_OUT_F32, IFX_ACCUM, nullptr, M,
-                         hidden, ffn);
-  if (rc != IFX_OK) return rc;
-  if (!ifx::decode_ffn_fits(hidden, ffn)) return IFX_BAD_GEOMETRY;
-  return status_of(ifx::launch_decode_ffn(W_o, attn, attn_dtype == IFX_OUT_F16, residual,
-                                          ffn_norm_weight, eps, W_gate, W_up, W_down, workspace,
-                                          q_dim, hidden, ffn, static_cast<hipStream_t>(stream)));
-}
-
 int ifx_qgemm_prefill_kernel(int quant_type, const void *W, const void *A_q8_1, void *Y,
                              int out_dtype, int mode, const void *bias, int M, int N, int K,
                              int kernel, int splits, void *stream) {
@@ -898,6 +854,104 @@ int ifx_repack_tiled(int quant_type, const void *W, void *W_out, int64_t n_rows,
     return IFX_BAD_GEOMETRY;  // the GEMVs address tiles with 32-bit offsets
   return status_of(ifx::launch_repack_tiled(quant_type, W, W_out, n_rows, K,
                                             static_cast<hipStream_t>(stream)));
+}
+
+namespace {
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+// The row-major section of a down-projection MMQ layout: the row-split copy
+// for Q6_K / Q8_0, the raw rows for Q4_K (already 16-byte aligned).
+int mmq_row_type(int qt) {
+  return qt == IFX_TYPE_Q4_K ? IFX_TYPE_Q4_K
+         : qt == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_R
+         : qt == IFX_TYPE_Q8_0 ? IFX_TYPE_Q8_0_R : 0;
+}
+int mmq_tiled_type(int qt) {
+  return qt == IFX_TYPE_Q4_K ? IFX_TYPE_Q4_K_T
+         : qt == IFX_TYPE_Q6_K ? IFX_TYPE_Q6_K_T
+         : qt == IFX_TYPE_Q8_0 ? IFX_TYPE_Q8_0_T : 0;
+}
+int64_t mmq_rows_bytes(int qt, int64_t rows, int cols) {
+  return qt == IFX_TYPE_Q4_K ? rows * static_cast<int64_t>(ifx::row_bytes(IFX_TYPE_Q4_K, cols))
+                             : ifx_repacked_bytes(qt, rows, cols);
+}
+// The ordered-split workspace a layout carries: the largest any tiled
+// launch of 3..32 batch rows asks for (fp32 and fp16 outputs plan alike).
+int64_t mmq_ws_bytes(int qt, int64_t rows, int cols) {
+  if (rows > (1 << 30)) return 0;
+  const int N = static_cast<int>(rows);
+  int64_t most = 0;
+  for (int M = kMaxRowSplitM + 1; M <= kMaxTiledM; ++M)
+    most = std::max(most, ifx_qgemv_workspace_bytes(mmq_tiled_type(qt), 1, &N, IFX_OUT_F32, M, cols));
+  return most;
+}
+}  // namespace
+
+int64_t ifx_mmq_layout_rows_offset(int quant_type, int64_t rows, int cols) {
+  if (!mmq_tiled_type(quant_type) || rows <= 0) return 0;
+  return align256(ifx_tiled_bytes(quant_type, rows, cols));
+}
+
+int64_t ifx_mmq_layout_ws_offset(int quant_type, int64_t rows, int cols) {
+  const int64_t off = ifx_mmq_layout_rows_offset(quant_type, rows, cols);
+  if (off == 0) return 0;
+  return align256(off + mmq_rows_bytes(quant_type, rows, cols));
+}
+
+int64_t ifx_mmq_layout_bytes(int quant_type, int64_t rows, int cols) {
+  const int64_t off = ifx_mmq_layout_ws_offset(quant_type, rows, cols);
+  if (off == 0) return 0;
+  return off + mmq_ws_bytes(quant_type, rows, cols);
+}
+
+int ifx_mmq_layout_build(int quant_type, const void *W, void *layout, int64_t rows, int cols,
+                         void *stream) {
+  if (!W || !layout) return IFX_NULL_POINTER;
+  if (!mmq_tiled_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (rows <= 0 || rows > (1 << 30) || cols <= 0 || cols % 256) return IFX_BAD_GEOMETRY;
+  if (reinterpret_cast<uintptr_t>(layout) % 256 != 0) return IFX_BAD_GEOMETRY;
+  // each section is addressed from its own base with 32-bit offsets
+  const int64_t off = ifx_mmq_layout_rows_offset(quant_type, rows, cols);
+  const int64_t raw = rows * static_cast<int64_t>(ifx::row_bytes(quant_type, cols));
+  if (off >= (int64_t{1} << 32) || mmq_rows_bytes(quant_type, rows, cols) >= (int64_t{1} << 32) ||
+      raw >= (int64_t{1} << 32))
+    return IFX_BAD_GEOMETRY;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char *base = static_cast<char *>(layout);
+  char *rows_base = base + off;
+  hipError_t e = ifx::launch_repack_tiled(quant_type, W, layout, rows, cols, s);
+  if (e != hipSuccess) return status_of(e);
+  if (quant_type == IFX_TYPE_Q4_K)
+    e = ifx::dry_run() ? hipSuccess : hipMemcpyAsync(rows_base, W, raw, hipMemcpyDeviceToDevice, s);
+  else
+    e = ifx::launch_repack(quant_type, W, rows_base, rows, cols, s);
+  if (e != hipSuccess) return status_of(e);
+  // the workspace's counters start at zero (a load-time call, never captured)
+  const int64_t ws = mmq_ws_bytes(quant_type, rows, cols);
+  if (ws > 0 && !ifx::dry_run())
+    e = hipMemsetAsync(base + ifx_mmq_layout_ws_offset(quant_type, rows, cols), 0, ws, s);
+  return status_of(e);
+}
+
+int ifx_qgemv_mmq(int quant_type, const void *layout, const void *A_q8_1, void *Y, int out_dtype,
+                  int mode, int M, int N, int K, int ordered, void *stream) {
+  if (!layout) return IFX_NULL_POINTER;
+  if (!mmq_tiled_type(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  if (mode != IFX_STORE && mode != IFX_ACCUM) return IFX_BAD_GEOMETRY;
+  if (M <= 0 || M > kMaxTiledM || N <= 0 || K <= 0 || K % 256) return IFX_BAD_GEOMETRY;
+  const char *base = static_cast<const char *>(layout);
+  if (M <= kMaxRowSplitM)
+    return qgemv_impl(mmq_row_type(quant_type), base + ifx_mmq_layout_rows_offset(quant_type, N, K),
+                      A_q8_1, Y, out_dtype, mode, nullptr, M, N, K, stream, nullptr, 0);
+  // fp16 sums are split only through the workspace; fp32 ones on request
+  void *ws = nullptr;
+  int64_t wsb = 0;
+  if (ordered || out_dtype == IFX_OUT_F16) {
+    ws = const_cast<char *>(base) + ifx_mmq_layout_ws_offset(quant_type, N, K);
+    wsb = mmq_ws_bytes(quant_type, N, K);
+    if (wsb == 0) ws = nullptr;
+  }
+  return qgemv_impl(mmq_tiled_type(quant_type), layout, A_q8_1, Y, out_dtype, mode, nullptr, M, N,
+                    K, stream, ws, wsb);
 }
 
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,

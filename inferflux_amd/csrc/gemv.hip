@@ -352,7 +352,7 @@ static void launch_t(GemvArgs args, bool f16, hipStream_t s) {
 // quarter-wave rows for the wide slices (tuning; read once).
 static int sub_rows_env() {
   static const int env = [] {
-    const char *e = getenv("IFX_GEMV_H");
+    const char *e = ifx::tuning_env("IFX_GEMV_H");
     const int v = e ? atoi(e) : 0;
     return (v == 1 || v == 2 || v == 4) ? v : 0;
   }();
@@ -416,7 +416,7 @@ static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
 // IFX_GEMV_ROWS in {1, 2, 4, 8} overrides it (tuning; read once).
 static int rows_env() {
   static const int env = [] {
-    const char *e = getenv("IFX_GEMV_ROWS");
+    const char *e = ifx::tuning_env("IFX_GEMV_ROWS");
     const int v = e ? atoi(e) : 0;
     return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
   }();
@@ -761,7 +761,7 @@ static void launch_swiglu_wide_nw(const SwigluArgs &a, bool f16h, hipStream_t s)
 template <int NORM>
 static void launch_swiglu_wide(const SwigluArgs &a, bool f16h, hipStream_t s) {
   static const int env = [] {
-    const char *e = getenv("IFX_SWIGLU_NW");
+    const char *e = ifx::tuning_env("IFX_SWIGLU_NW");
     const int v = e ? atoi(e) : 0;
     return (v == 4 || v == 8 || v == 16) ? v : 0;
   }();
@@ -773,7 +773,7 @@ static void launch_swiglu_wide(const SwigluArgs &a, bool f16h, hipStream_t s) {
 
 static bool swiglu_wide_env() {
   static const int v = [] {
-    const char *e = getenv("IFX_SWIGLU_WIDE");
+    const char *e = ifx::tuning_env("IFX_SWIGLU_WIDE");
     return e ? atoi(e) : 1;
   }();
   return v != 0;

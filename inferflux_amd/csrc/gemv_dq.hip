@@ -404,7 +404,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-      base[i] = (args.mode == 1 && m < M)
+      base[i] = (!F16OUT && args.mode == 1 && m < M)
                     ? static_cast<const float *>(sg.Y)[static_cast<int64_t>(m) * N + nc] : 0.0f;
     }
     constexpr int kSlot = 64 * 16;  // floats per wave and split
@@ -509,21 +509,21 @@ namespace {
 int dq_sb_max(int M) { return max(1, (kLdsBytes / 2 / (M + 1) - 8) / 256); }
 
 // Super-block splits: at least what the activation stage needs, and enough
-// workgroups for two per CU on 256 CUs; fp16 outputs take one split when
-// the stage allows.  IFX_DQ_WGS sets the workgroup target (tuning; read
-// once).
-int dq_splits(int groups, int nsb, int M, bool f16) {
+// workgroups for two per CU on 256 CUs; fp16 outputs without the ordered-
+// split workspace (no_split) take the fewest the stage allows.  IFX_DQ_WGS
+// sets the workgroup target (tuning; read once).
+int dq_splits(int groups, int nsb, int M, bool no_split) {
   static const int target = [] {
-    const char *e = getenv("IFX_DQ_WGS");
+    const char *e = ifx::tuning_env("IFX_DQ_WGS");
     return e && atoi(e) > 0 ? atoi(e) : 512;
   }();
   const int need = (nsb + dq_sb_max(M) - 1) / dq_sb_max(M);
-  if (f16) return need;
+  if (no_split) return need;
   return max(need, min(nsb, (target + groups - 1) / groups));
 }
 
 // Row groups and K splits of a launch (sets blk_begin and sb_per).
-void dq_plan(DqArgs &args, bool f16, int splits_req, int &groups, int &ks) {
+void dq_plan(DqArgs &args, bool no_split, int splits_req, int &groups, int &ks) {
   groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = groups;
@@ -531,8 +531,8 @@ void dq_plan(DqArgs &args, bool f16, int splits_req, int &groups, int &ks) {
   }
   const int nsb = args.K >> 8;
   const int need = (nsb + dq_sb_max(args.M) - 1) / dq_sb_max(args.M);
-  ks = (splits_req > 0 && !f16) ? max(need, min(splits_req, nsb))
-                                : dq_splits(groups, nsb, args.M, f16);
+  ks = (splits_req > 0 && !no_split) ? max(need, min(splits_req, nsb))
+                                     : dq_splits(groups, nsb, args.M, no_split);
   args.sb_per = (nsb + ks - 1) / ks;
   ks = (nsb + args.sb_per - 1) / args.sb_per;
 }
@@ -541,11 +541,15 @@ template <int QT, bool TL>
 hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   const bool ordered = args.ws.cnt != nullptr;
   int groups = 0, ks = 1;
-  dq_plan(args, f16, splits_req, groups, ks);
-  if (f16 && ks > 1) return hipErrorInvalidValue;  // fp16 outputs cannot be split
+  dq_plan(args, f16 && !ordered, splits_req, groups, ks);
+  // fp16 sums cannot be added with atomics: split only through the workspace
+  if (f16 && ks > 1 && !ordered) return hipErrorInvalidValue;
   const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
   const dim3 grid(groups, ks), block(64 * kWaves);
-  if (f16) {
+  if (f16 && ks > 1) {
+    if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, true, 2, true), grid, block, shm, s, args);
+    else IFX_LAUNCH(k_gemv_dq, (QT, true, 2), grid, block, shm, s, args);
+  } else if (f16) {
     if constexpr (TL) IFX_LAUNCH(k_gemv_dq, (QT, true, 0, true), grid, block, shm, s, args);
     else IFX_LAUNCH(k_gemv_dq, (QT, true, 0), grid, block, shm, s, args);
   } else if (ks == 1) {
@@ -663,8 +667,9 @@ int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K)
   args.M = M;
   args.K = K;
   int groups = 0, ks = 1;
-  dq_plan(args, f16, 0, groups, ks);
-  if (ks <= 1 || f16) return 0;
+  (void)f16;  // fp16 outputs split as fp32 ones when the workspace is given
+  dq_plan(args, false, 0, groups, ks);
+  if (ks <= 1) return 0;
   return (static_cast<int64_t>(groups) * 4 + 255) / 256 * 256 +
          static_cast<int64_t>(groups) * ks * kWaves * 64 * 16 * 4;
 }

@@ -471,7 +471,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       const int m = 2 * (mi & ~3) + 4 * h + (mi & 3);
-      base[mi] = (args.mode == 1 && m < M)
+      base[mi] = (!F16OUT && args.mode == 1 && m < M)
                      ? static_cast<const float *>(sg.Y)[static_cast<int64_t>(m) * N + nc] : 0.0f;
     }
     float *mine = args.ws.part + (static_cast<int64_t>(bx) * ks + blockIdx.y) * 64 * NM + lane;
@@ -546,15 +546,16 @@ namespace {
 //  * few row groups and a longer K (e.g. a down projection with N = 2048):
 //    4 waves, 8 splits.
 // IFX_SLOT_KW in {1, 2, 4, 8} and IFX_SLOT_SPLIT >= 1 override (tuning;
-// read once); IFX_SLOT_SPLIT=1 gives bitwise reproducible results.
-void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
+// read once).  no_split: fp16 outputs without the ordered-split workspace
+// (fp16 sums cannot be added with atomics), one workgroup per row group.
+void choose_slot_work(int blocks, int nsb, bool no_split, int &kw, int &ks) {
   static const int env_kw = [] {
-    const char *e = getenv("IFX_SLOT_KW");
+    const char *e = ifx::tuning_env("IFX_SLOT_KW");
     const int v = e ? atoi(e) : 0;
     return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
   }();
   static const int env_ks = [] {
-    const char *e = getenv("IFX_SLOT_SPLIT");
+    const char *e = ifx::tuning_env("IFX_SLOT_SPLIT");
     return e ? atoi(e) : 0;
   }();
   const bool wide = blocks >= 256;
@@ -568,7 +569,7 @@ void choose_slot_work(int blocks, int nsb, bool f16, int &kw, int &ks) {
   }
   while (kw > 1 && kw > nsb) kw /= 2;
   ks = env_ks > 0 ? env_ks : (wide || (!env_kw && nsb <= 24)) ? 1 : 8;
-  ks = f16 ? 1 : max(1, min(ks, nsb / kw));
+  ks = no_split ? 1 : max(1, min(ks, nsb / kw));
 }
 
 template <int QT, int MP, int KW, bool F16OUT, int SPLIT, bool TL>
@@ -584,8 +585,9 @@ void slot_launch(const SlotArgs &args, int blocks, int ks, hipStream_t s) {
 
 template <int QT, int MP, int KW, bool TL>
 void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t s) {
-  if (f16) {
-    slot_launch<QT, MP, KW, true, 0, TL>(args, blocks, 1, s);
+  if (f16) {  // a split fp16 launch is ordered (choose_slot_work)
+    if (ks > 1) slot_launch<QT, MP, KW, true, 2, TL>(args, blocks, ks, s);
+    else slot_launch<QT, MP, KW, true, 0, TL>(args, blocks, 1, s);
   } else if (ks == 1) {
     slot_launch<QT, MP, KW, false, 0, TL>(args, blocks, 1, s);
   } else if (args.ws.cnt) {
@@ -607,7 +609,7 @@ void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t 
 template <int QT, int MP, bool TL>
 void slot_kw(const SlotArgs &args, int blocks, bool f16, hipStream_t s) {
   int kw = 8, ks = 1;
-  choose_slot_work(blocks, args.K >> 8, f16, kw, ks);
+  choose_slot_work(blocks, args.K >> 8, f16 && !args.ws.cnt, kw, ks);
   switch (kw) {
   case 1: slot_split<QT, MP, 1, TL>(args, blocks, ks, f16, s); break;
   case 2: slot_split<QT, MP, 2, TL>(args, blocks, ks, f16, s); break;
@@ -649,7 +651,7 @@ void slot_swiglu_launch(const SlotArgs &args, bool f16h, hipStream_t s) {
 template <int QT, bool TL>
 void slot_swiglu_q(const SlotArgs &args, bool f16h, hipStream_t s) {
   int kw = 4, ks = 1;
-  if (getenv("IFX_SLOT_KW")) choose_slot_work(1 << 20, args.K >> 8, false, kw, ks);
+  if (ifx::tuning_env("IFX_SLOT_KW")) choose_slot_work(1 << 20, args.K >> 8, false, kw, ks);
   while (kw > 1 && kw > (args.K >> 8)) kw /= 2;
   // tiled rows above M = 8: two 16-row slots per MFMA
   if (TL && args.M > 8) {
@@ -683,8 +685,9 @@ int64_t gemv_slot_workspace_bytes(int count, const int *N, bool f16, int M, int 
   int blocks = 0;
   for (int i = 0; i < count; ++i) blocks += (N[i] + 31) / 32;
   int kw = 8, ks = 1;
-  choose_slot_work(blocks, K >> 8, f16, kw, ks);
-  if (ks <= 1 || f16) return 0;
+  (void)f16;  // fp16 outputs split as fp32 ones when the workspace is given
+  choose_slot_work(blocks, K >> 8, false, kw, ks);
+  if (ks <= 1) return 0;
   const int nm = M > 8 ? 8 : 4;  // fp32 sums per lane (MP / 2)
   return (static_cast<int64_t>(blocks) * 4 + 255) / 256 * 256 +
          static_cast<int64_t>(blocks) * ks * 64 * nm * 4;

@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <initializer_list>
 
@@ -26,6 +27,18 @@
 #endif
 
 namespace ifx {
+
+// Tuning overrides of the dispatch and launch geometry (IFX_PREFILL,
+// IFX_DQ, IFX_SLOT_KW, ...) are read only in tuning builds (-DIFX_TUNING):
+// a product build always takes the measured defaults the tests pin.
+inline const char *tuning_env(const char *name) {
+#ifdef IFX_TUNING
+  return getenv(name);
+#else
+  (void)name;
+  return nullptr;
+#endif
+}
 
 // Launch log: every kernel launch goes through IFX_LAUNCH, which records the
 // instance name ("k_gemv<12,1,2,1,4,0,2>": the kernel's template arguments as

@@ -1,11 +1,12 @@
 // ifx_slices.h -- the per-lane slice arithmetic of the weight-streaming
-// GEMV (gemv.hip) and the fused decode-layer kernel (layer.hip): a lane's
+// GEMV (gemv.hip): a lane's
 // weight bytes of one slice of a row, the matching Q8_1 activation codes
 // and scales, and the integer dot plus fp32 scaling of
 // runtime/backends/cuda/native/kernels/mmvq.cuh:62-127 (Q4_K), 424-474
 // (Q6_K), with the Q4_K min term from the Q8_1 s field (mmvq.cuh:121-125).
-// Both kernels include this one definition, so their row sums are formed by
-// the same instructions in the same order.
+// Every form of that GEMV (plain, grouped, fused producers, SiLU epilogue)
+// uses this one definition, so their row sums are formed by the same
+// instructions in the same order.
 #pragma once
 
 #include "ifx_q8_1.h"

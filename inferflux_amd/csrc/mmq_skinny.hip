@@ -417,7 +417,7 @@ namespace {
 // super-blocks per split.  IFX_SKINNY_SPLIT overrides (tuning; read once).
 int choose_splits(int row_groups, int nsb) {
   static const int env = [] {
-    const char *e = getenv("IFX_SKINNY_SPLIT");
+    const char *e = ifx::tuning_env("IFX_SKINNY_SPLIT");
     return e ? atoi(e) : 0;
   }();
   int ks = env > 0 ? env : (1024 + row_groups - 1) / row_groups;

@@ -460,7 +460,7 @@ namespace {
 // overrides (tuning; read once).
 int choose_kw(int tiles, int nsb) {
   static const int env = [] {
-    const char *e = getenv("IFX_MMVQ_KW");
+    const char *e = ifx::tuning_env("IFX_MMVQ_KW");
     const int v = e ? atoi(e) : 0;
     return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
   }();

@@ -289,7 +289,13 @@ hipError_t launch_quantize_rows_sym(const void *a, const void *b, int dtype, int
                                     float *scales, int M, int K, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const dim3 grid(M), block(256);
-  const bool v4 = K % 4 == 0;
+  // The vector forms load four values (16 bytes fp32, 8 bytes fp16 / bf16)
+  // and store four codes per access: they need K % 4 == 0 and bases aligned
+  // to those sizes (then every row is); other calls take the scalar form.
+  const uintptr_t vin = dtype == 0 ? 16 : 8;
+  const bool v4 = K % 4 == 0 && reinterpret_cast<uintptr_t>(a) % vin == 0 &&
+                  reinterpret_cast<uintptr_t>(b) % vin == 0 &&
+                  reinterpret_cast<uintptr_t>(codes) % 4 == 0;
   if (v4 && K <= 16384) {
     const dim3 rblock(1024);
 #define IFX_QRSR(DT)                                                                             \

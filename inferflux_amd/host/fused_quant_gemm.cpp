@@ -35,6 +35,17 @@ bool ParseBoolEnv(const char *name, bool fallback) {
   return fallback;
 }
 
+// string_utils.h:55-68: the fallback when unset, empty, unparseable or
+// outside [lo, hi].
+int ParseIntEnv(const char *name, int fallback, int lo, int hi) {
+  const char *v = std::getenv(name);
+  if (!v || !*v) return fallback;
+  char *end = nullptr;
+  const long n = std::strtol(v, &end, 10);
+  if (end == v || *end != '\0' || n < lo || n > hi) return fallback;
+  return static_cast<int>(n);
+}
+
 bool Usable(const QuantizedWeightInfo &w, const void *act, const void *out) {
   return w.data && w.quant_type >= 0 && act && out;
 }
@@ -53,6 +64,12 @@ bool Launch(const QuantizedWeightInfo &w, const void *act, void *out, int out_dt
   if (!ViewCovers(w, N, K)) return false;
   const FusedDispatchGeometry g{M, N, K, 1, true, false};
   if (!FusedQuantGemm::ShouldUseFusedPath(w.quant_type, g)) return false;
+  const NativeExecutionPolicy p = Resolve(policy);
+  if (p.deterministic_reductions &&
+      ifx_qgemv_workspace_bytes(w.quant_type, 1, &N, out_dtype, M, K) > 0)
+    return p.reduction_workspace &&
+           ifx_qgemv_ws(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K,
+                        p.reduction_workspace, p.reduction_workspace_bytes, stream) == IFX_OK;
   return ifx_qgemv(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K, stream) ==
          IFX_OK;
 }
@@ -74,15 +91,44 @@ bool LaunchGroup(const std::array<PackedProjectionSpec, C> &p, const void *act, 
   }
   const FusedDispatchGeometry g{M, N[0], K, static_cast<int>(C), true, false};
   if (!FusedQuantGemm::ShouldUseFusedPath(p[0].weight.quant_type, g)) return false;
+  const NativeExecutionPolicy pol = Resolve(policy);
+  if (pol.deterministic_reductions &&
+      ifx_qgemv_workspace_bytes(p[0].weight.quant_type, static_cast<int>(C), N, IFX_OUT_F16, M,
+                                K) > 0)
+    return pol.reduction_workspace &&
+           ifx_qgemv_grouped_ws(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
+                                IFX_OUT_F16, IFX_STORE, M, K, pol.reduction_workspace,
+                                pol.reduction_workspace_bytes, stream) == IFX_OK;
   return ifx_qgemv_grouped(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
                            IFX_OUT_F16, IFX_STORE, M, K, stream) == IFX_OK;
 }
 
 }  // namespace
 
+// native_execution_policy.h:61-78: the same environment names and
+// fallbacks, apart from INFERFLUX_ENABLE_DOWNPROJ_MMQ's default (the
+// struct's comment says why).
 NativeExecutionPolicy NativeExecutionPolicy::FromEnv() {
   NativeExecutionPolicy p;
+  p.force_cublas = ParseBoolEnv("INFERFLUX_FORCE_CUBLAS", false);
+  p.disable_prepacked_activations = ParseBoolEnv("INFERFLUX_DISABLE_PREPACKED_ACTIVATIONS", false);
+  p.disable_q81_activations = ParseBoolEnv("INFERFLUX_DISABLE_Q8_1_ACTIVATIONS", false);
   p.disable_fused_gemv = ParseBoolEnv("INFERFLUX_DISABLE_FUSED_GEMV", false);
+  p.enable_experimental_q81_downproj_hot_fixed =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_DOWNPROJ_HOT_FIXED", false);
+  p.enable_experimental_q81_downproj_rowpair_hot_fixed =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_DOWNPROJ_ROWPAIR_HOT_FIXED", false);
+  p.enable_experimental_q81_grouped_hot_q4k =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_GROUPED_HOT_Q4K", true);
+  p.enable_experimental_q81_grouped_rowpair_w4 =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_GROUPED_ROWPAIR_W4", true);
+  p.enable_experimental_q81_grouped_rowquad_m4 =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_GROUPED_ROWQUAD_M4", false);
+  p.enable_experimental_q81_grouped_mmq3 =
+      ParseBoolEnv("INFERFLUX_ENABLE_EXPERIMENTAL_Q8_1_GROUPED_MMQ3", true);
+  p.enable_downproj_mmq = ParseBoolEnv("INFERFLUX_ENABLE_DOWNPROJ_MMQ", true);
+  p.downproj_mmq_min_batch_override = ParseIntEnv("INFERFLUX_DOWNPROJ_MMQ_MIN_BATCH", -1, 1, 64);
+  p.enable_fused_gate_up_silu = ParseBoolEnv("INFERFLUX_ENABLE_FUSED_GATE_UP_SILU", true);
   return p;
 }
 
@@ -159,8 +205,20 @@ bool FusedQuantGemm::GemvQ8_1WithBias(const QuantizedWeightInfo &weight, const v
 
 bool FusedQuantGemm::GemvQ8_1Pair(const std::array<PackedProjectionSpec, 2> &projections,
                                   const void *act_q8_1, int M, int K, hipStream_t stream,
-                                  const NativeExecutionPolicy *policy) {
+                                  const NativeExecutionPolicy *policy,
+                                  FfnProjOperator selected_op) {
+  // Every label runs the routed grouped launch; an out-of-range value is a
+  // caller error and is not handled.
+  if (static_cast<int>(selected_op) < static_cast<int>(FfnProjOperator::kFallback) ||
+      static_cast<int>(selected_op) > static_cast<int>(FfnProjOperator::kPackedGroup))
+    return false;
   return LaunchGroup(projections, act_q8_1, M, K, stream, policy);
+}
+
+bool FusedQuantGemm::GemvQ8_1PairRowQuadCandidate(
+    const std::array<PackedProjectionSpec, 2> &projections, const void *act_q8_1, int M, int K,
+    hipStream_t stream) {
+  return LaunchGroup(projections, act_q8_1, M, K, stream, nullptr);
 }
 
 bool FusedQuantGemm::GemvQ8_1Triple(const std::array<PackedProjectionSpec, 3> &projections,
@@ -280,18 +338,19 @@ int FusedQuantGemm::GetAdaptiveThreshold(int quant_type) {
 
 // The geometry narrows it where a kernel has a hard limit (the reference
 // adjusts its threshold for packed activations, grouped outputs and K,
-// fused_quant_gemm.cu:830-923):
-//  * includes_rmsnorm: the RMSNorm + Q8_1 producer fused into the GEMV
-//    (ifx_qgemv_grouped_rmsnorm) is Q4_K only, M <= 2, with the batch's Q8_1
-//    rows (80 K / 64 + K / 8 bytes each) in 64 KiB of LDS; larger batches
-//    take the producer + GEMV;
+// fused_quant_gemm.cu:830-923; like it, includes_rmsnorm counts only when
+// the activations are not pre-quantized, packed_activation == false):
+//  * includes_rmsnorm without pre-quantized activations: the RMSNorm + Q8_1
+//    producer fused into the GEMV (ifx_qgemv_grouped_rmsnorm) is Q4_K only,
+//    M <= 2, with the batch's Q8_1 rows (80 K / 64 + K / 8 bytes each) in
+//    64 KiB of LDS; larger batches take the producer + GEMV;
 //  * K: the Q8_1 activations [M][K/32] are addressed with 32-bit offsets.
 int FusedQuantGemm::GetGeometryAwareThreshold(int quant_type,
                                               const FusedDispatchGeometry &geometry) {
   int64_t t = GetAdaptiveThreshold(quant_type);
   if (t == 0) return 0;
   const int64_t a_row = geometry.K > 0 ? static_cast<int64_t>(geometry.K / 32) * 36 : 0;
-  if (geometry.includes_rmsnorm) {
+  if (geometry.includes_rmsnorm && !geometry.packed_activation) {
     if (quant_type != static_cast<int>(TensorType::Q4_K)) return 0;
     t = std::min<int64_t>(t, 2);
     // the LDS row of the fused producer: codes in 80-byte slots per 64
@@ -333,6 +392,178 @@ const char *FusedQuantGemm::KernelFamilyName(KernelFamily family) {
   case KernelFamily::kF16DequantGemv: return "fp16 dequant MFMA GEMV";
   default: return "none";
   }
+}
+
+// ---- Down projection on the re-tiled copy ----
+
+namespace {
+
+bool DownProjLaunch(const MmqWeightInfo &w, const void *act, void *out, int out_dtype, int mode,
+                    int M, int N, int K, hipStream_t stream, const NativeExecutionPolicy *policy) {
+  const NativeExecutionPolicy p = Resolve(policy);
+  if (!p.enable_downproj_mmq || p.disable_fused_gemv) return false;
+  if (!w.data || !act || !out || M <= 0 || N <= 0 || K <= 0) return false;
+  if (N != w.rows || K != w.cols || w.tile_cols != FusedQuantGemm::kDownProjMmqTileCols)
+    return false;
+  if (!FusedQuantGemm::SupportsDownProjMmq(w.quant_type) || M > FusedQuantGemm::kDownProjMmqMaxM)
+    return false;
+  return ifx_qgemv_mmq(w.quant_type, w.data, act, out, out_dtype, mode, M, N, K,
+                       p.deterministic_reductions ? 1 : 0, stream) == IFX_OK;
+}
+
+}  // namespace
+
+bool FusedQuantGemm::DownProjMmq(const MmqWeightInfo &weight, const void *act_q8_1,
+                                 uint16_t *output, int M, int N, int K, hipStream_t stream,
+                                 const NativeExecutionPolicy *policy) {
+  return DownProjLaunch(weight, act_q8_1, output, IFX_OUT_F16, IFX_STORE, M, N, K, stream, policy);
+}
+
+bool FusedQuantGemm::DownProjMmqF32(const MmqWeightInfo &weight, const void *act_q8_1,
+                                    float *output, int M, int N, int K, hipStream_t stream,
+                                    const NativeExecutionPolicy *policy) {
+  return DownProjLaunch(weight, act_q8_1, output, IFX_OUT_F32, IFX_STORE, M, N, K, stream, policy);
+}
+
+bool FusedQuantGemm::DownProjMmqAccumF32(const MmqWeightInfo &weight, const void *act_q8_1,
+                                         float *output, int M, int N, int K, hipStream_t stream,
+                                         const NativeExecutionPolicy *policy) {
+  return DownProjLaunch(weight, act_q8_1, output, IFX_OUT_F32, IFX_ACCUM, M, N, K, stream, policy);
+}
+
+bool FusedQuantGemm::IsDownProjMmqEnabled(const NativeExecutionPolicy *policy) {
+  return Resolve(policy).enable_downproj_mmq;
+}
+
+// fused_quant_gemm.cu:1966-2026: validate, allocate, transform on the
+// stream, wait, and hand the caller the layout (freed on any failure).
+bool FusedQuantGemm::BuildDownProjMmqLayout(const QuantizedWeightInfo &weight, int rows, int cols,
+                                            MmqWeightInfo *layout, hipStream_t stream) {
+  if (!layout || !weight.data || rows <= 0 || cols <= 0 || cols % 256 != 0) return false;
+  if (!SupportsDownProjMmq(weight.quant_type)) return false;
+  if (!ViewCovers(weight, rows, cols)) return false;
+  const int64_t bytes = ifx_mmq_layout_bytes(weight.quant_type, rows, cols);
+  if (bytes <= 0) return false;
+  void *buf = nullptr;
+  if (hipMalloc(&buf, static_cast<size_t>(bytes)) != hipSuccess) return false;
+  if (ifx_mmq_layout_build(weight.quant_type, weight.data, buf, rows, cols, stream) != IFX_OK ||
+      hipStreamSynchronize(stream) != hipSuccess) {
+    (void)hipFree(buf);
+    return false;
+  }
+  *layout = MmqWeightInfo{buf, weight.quant_type, rows, cols, kDownProjMmqTileCols};
+  return true;
+}
+
+void FusedQuantGemm::DestroyDownProjMmqLayout(const MmqWeightInfo &layout) {
+  if (layout.data) (void)hipFree(const_cast<void *>(layout.data));
+}
+
+bool FusedQuantGemm::SupportsDownProjMmq(int quant_type) {
+  return quant_type == static_cast<int>(TensorType::Q4_K) ||
+         quant_type == static_cast<int>(TensorType::Q6_K);
+}
+
+int FusedQuantGemm::GetDownProjMmqThreshold(int quant_type, int m, int n, int k) {
+  (void)m;
+  (void)n;
+  (void)k;
+  (void)quant_type;
+  const int override_m = NativeExecutionPolicy::FromEnv().downproj_mmq_min_batch_override;
+  if (override_m >= 0) return override_m;
+  return 3;
+}
+
+// ---- Producers fused into their consumer ----
+
+namespace {
+
+template <size_t C>
+bool LaunchNormGroup(const std::array<PackedProjectionSpec, C> &p, const void *residual,
+                     int residual_dtype, const uint16_t *norm_weight, float eps, int M, int K,
+                     hipStream_t stream, const NativeExecutionPolicy *policy) {
+  if (!residual || Resolve(policy).disable_fused_gemv) return false;
+  const void *W[C];
+  void *Y[C];
+  int N[C];
+  for (size_t i = 0; i < C; ++i) {
+    if (!Usable(p[i].weight, residual, p[i].output)) return false;
+    if (p[i].weight.quant_type != p[0].weight.quant_type) return false;
+    if (!ViewCovers(p[i].weight, p[i].output_cols, K)) return false;
+    W[i] = p[i].weight.data;
+    Y[i] = p[i].output;
+    N[i] = p[i].output_cols;
+  }
+  const FusedDispatchGeometry g{M, N[0], K, static_cast<int>(C), false, norm_weight != nullptr};
+  if (!FusedQuantGemm::ShouldUseFusedPath(p[0].weight.quant_type, g)) return false;
+  return ifx_qgemv_grouped_rmsnorm(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, residual,
+                                   residual_dtype, norm_weight, eps, IFX_OUT_F16, IFX_STORE, M, K,
+                                   stream) == IFX_OK;
+}
+
+bool LaunchQuantizeAccum(const QuantizedWeightInfo &w, const void *input, int input_dtype,
+                         float *output, int M, int N, int K, hipStream_t stream,
+                         const NativeExecutionPolicy *policy) {
+  if (!Usable(w, input, output) || Resolve(policy).disable_fused_gemv) return false;
+  if (!ViewCovers(w, N, K)) return false;
+  const void *W[1] = {w.data};
+  void *Y[1] = {output};
+  const int NN[1] = {N};
+  return ifx_qgemv_grouped_rmsnorm(w.quant_type, 1, W, Y, NN, input, input_dtype, nullptr, 0.0f,
+                                   IFX_OUT_F32, IFX_ACCUM, M, K, stream) == IFX_OK;
+}
+
+}  // namespace
+
+bool FusedQuantGemm::FusedRmsNormGemvQ8_1Pair(const std::array<PackedProjectionSpec, 2> &projections,
+                                              const float *residual, const uint16_t *norm_weight,
+                                              int M, int K, float rms_norm_eps, hipStream_t stream,
+                                              const NativeExecutionPolicy *policy) {
+  if (!norm_weight) return false;
+  return LaunchNormGroup(projections, residual, IFX_OUT_F32, norm_weight, rms_norm_eps, M, K,
+                         stream, policy);
+}
+
+bool FusedQuantGemm::FusedRmsNormGemvQ8_1Triple(
+    const std::array<PackedProjectionSpec, 3> &projections, const float *residual,
+    const uint16_t *norm_weight, int M, int K, float rms_norm_eps, hipStream_t stream,
+    const NativeExecutionPolicy *policy) {
+  if (!norm_weight) return false;
+  return LaunchNormGroup(projections, residual, IFX_OUT_F32, norm_weight, rms_norm_eps, M, K,
+                         stream, policy);
+}
+
+bool FusedQuantGemm::QuantizeGemvQ8_1AccumF32(const QuantizedWeightInfo &weight,
+                                              const float *input, float *output, int M, int N,
+                                              int K, hipStream_t stream,
+                                              const NativeExecutionPolicy *policy) {
+  return LaunchQuantizeAccum(weight, input, IFX_OUT_F32, output, M, N, K, stream, policy);
+}
+
+bool FusedQuantGemm::QuantizeGemvQ8_1AccumF32(const QuantizedWeightInfo &weight,
+                                              const uint16_t *input, float *output, int M, int N,
+                                              int K, hipStream_t stream,
+                                              const NativeExecutionPolicy *policy) {
+  return LaunchQuantizeAccum(weight, input, IFX_OUT_F16, output, M, N, K, stream, policy);
+}
+
+bool FusedQuantGemm::FusedRmsNormGateUpSiluGemvQ8_1WithEpilogue(
+    const QuantizedWeightInfo &gate_raw, const QuantizedWeightInfo &up_raw, const float *residual,
+    const uint16_t *norm_weight, float rms_norm_eps, uint16_t *output, void *act_q8_1_out, int M,
+    int N, int K, hipStream_t stream) {
+  if (!Usable(gate_raw, residual, output) || !Usable(up_raw, residual, output) || !norm_weight)
+    return false;
+  if (gate_raw.quant_type != up_raw.quant_type) return false;
+  if (!ViewCovers(gate_raw, N, K) || !ViewCovers(up_raw, N, K)) return false;
+  return ifx_qgemv_gate_up_silu_rmsnorm(gate_raw.quant_type, gate_raw.data, up_raw.data, residual,
+                                        IFX_OUT_F32, norm_weight, rms_norm_eps, output,
+                                        IFX_OUT_F16, act_q8_1_out, M, N, K, stream) == IFX_OK;
+}
+
+int64_t FusedQuantGemm::ReductionWorkspaceBytes(int quant_type, int count, const int *N,
+                                                bool f16_out, int M, int K) {
+  return ifx_qgemv_workspace_bytes(quant_type, count, N, f16_out ? IFX_OUT_F16 : IFX_OUT_F32, M,
+                                   K);
 }
 
 }  // namespace rocm

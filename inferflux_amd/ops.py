@@ -413,44 +413,6 @@ def qgemv_gate_up_silu_rmsnorm(qtype, Wg, Wu, x, norm_weight, M, N, K, eps=1e-6,
     return h_out, q8_1_out
 
 
-def decode_ffn_workspace_bytes(M, ffn):
-    return int(_lib.load().ifx_decode_ffn_workspace_bytes(M, ffn))
-
-
-def decode_ffn(W_o, attn, resid, norm_weight, W_gate, W_up, W_down, hidden, q_dim, ffn,
-               workspace, eps=1e-6, stream=None):
-    """The post-attention half of a decode layer at M = 1 in two launches
-    (ifx_decode_ffn): resid += O . Q8_1(attn); h = silu(gate . a) * (up . a)
-    with a = Q8_1(RMSNorm(resid)); resid += down . Q8_1(h).  O, gate, up
-    Q4_K, down Q6_K; resid [1, hidden] fp32 updated in place; workspace a
-    device tensor of at least decode_ffn_workspace_bytes(1, ffn) bytes whose
-    first 2048 bytes (the control block) are zero before the first call.
-    W_o None: the O launch is skipped (the residual already holds the
-    attention block's output; attn is not read)."""
-    M = 1
-    if resid.dtype != torch.float32 or resid.numel() < hidden or (
-            W_o is not None and attn.numel() < q_dim):
-        raise ValueError("resid must be fp32 [hidden]; attn [q_dim]")
-    if norm_weight.dtype != torch.float16 or norm_weight.numel() < hidden:
-        raise ValueError("norm_weight must be fp16 [hidden]")
-    for W, n, k in ((W_o, hidden, q_dim), (W_gate, ffn, hidden), (W_up, ffn, hidden)):
-        if W is not None and W.numel() < weight_bytes(Q4_K, n, k):
-            raise ValueError("a Q4_K weight is smaller than its shape")
-    if W_down.numel() < weight_bytes(Q6_K, hidden, ffn):
-        raise ValueError("W_down is smaller than its shape")
-    ad = OUT_F16 if W_o is not None and attn.dtype == torch.float16 else OUT_F32
-    nbytes = workspace.numel() * workspace.element_size()
-    wo = _dev(W_o, "W_o") if W_o is not None else None
-    ap = _dev(attn, "attn") if W_o is not None else None
-    rc = _lib.load().ifx_decode_ffn(
-        Q4_K, wo, ap, ad, q_dim, _dev(resid, "resid"),
-        _dev(norm_weight, "norm_weight"), eps, Q4_K, _dev(W_gate, "W_gate"), _dev(W_up, "W_up"),
-        ffn, Q6_K, _dev(W_down, "W_down"), M, hidden, _dev(workspace, "workspace"), nbytes,
-        _stream(stream))
-    _check(rc, "ifx_decode_ffn")
-    return resid
-
-
 def _row_split_bytes(qtype, K):
     n = K + K // 32 * 2 if qtype == Q8_0_R else K // 2 + K // 4 + K // 16 + K // 256 * 2
     return (n + 15) // 16 * 16
@@ -483,6 +445,42 @@ def repack_tiled(qtype, W, n_rows, K, out=None, stream=None):
                                       _stream(stream))
     _check(rc, "ifx_repack_tiled")
     return tt, out
+
+
+def mmq_layout(qtype, W, n_rows, K, out=None, stream=None):
+    """Down-projection MMQ layout of raw Q4_K / Q6_K / Q8_0 rows
+    (ifx_mmq_layout_build): the tiled copy plus a row-major copy for M <= 2,
+    in one 256-byte-aligned uint8 device tensor."""
+    nbytes = int(_lib.load().ifx_mmq_layout_bytes(qtype, n_rows, K))
+    if nbytes == 0:
+        raise ValueError("no MMQ layout for this type / K")
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=W.device)
+    if W.numel() < weight_bytes(qtype, n_rows, K) or out.numel() < nbytes:
+        raise ValueError("W or out too small")
+    rc = _lib.load().ifx_mmq_layout_build(qtype, _dev(W, "W"), _dev(out, "out"), n_rows, K,
+                                          _stream(stream))
+    _check(rc, "ifx_mmq_layout_build")
+    return out
+
+
+def qgemv_mmq(qtype, layout, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE,
+              ordered=False, stream=None):
+    """y [M, N] (op)= W . a on an MMQ layout (ifx_qgemv_mmq), 1 <= M <= 32;
+    ordered: K splits added in split order through the layout's workspace."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=layout.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if out.dtype not in (torch.float16, torch.float32):
+        raise TypeError("out must be float32 or float16")
+    if layout.numel() < int(_lib.load().ifx_mmq_layout_bytes(qtype, N, K)):
+        raise ValueError("layout is smaller than N x K")
+    if A.numel() < M * (K // 32) * 36 or out.numel() < M * N:
+        raise ValueError("A or out too small")
+    rc = _lib.load().ifx_qgemv_mmq(qtype, _dev(layout, "layout"), _dev(A, "A"), _dev(out, "out"),
+                                   od, mode, M, N, K, int(bool(ordered)), _stream(stream))
+    _check(rc, "ifx_qgemv_mmq")
+    return out
 
 
 def dequantize(qtype, W, n_rows, K, out_dtype=torch.float32, stream=None, out=None):

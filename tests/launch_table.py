@@ -17,6 +17,9 @@ Entry kinds:
   quantize_accum      ifx_qgemv_grouped_rmsnorm with norm_weight NULL (Q8_1 fused in), accumulate
   gate_up_silu_rmsnorm  ifx_qgemv_gate_up_silu_rmsnorm (Q8_1 output of silu(gate)*up)
   gate_up_silu        ifx_qgemv_gate_up_silu (Q8_1 output of silu(gate)*up)
+  mmq_accum           ifx_qgemv_mmq on the down-projection MMQ layout (ifx_mmq_layout_build of
+                      the raw type named), accumulate into an fp32 residual; _ws: ordered
+                      K splits through the layout's own workspace
   prefill             ifx_qgemm_prefill
   prefill_int8        ifx_qgemm_prefill_kernel(IFX_PREFILL_INT8)
 Kernel names: include/ifx_qgemm.h, ifx_launch_log_begin.
@@ -107,6 +110,14 @@ LAUNCHES = [
     ("c4t_o_m32", "gemv_accum_ws", Q4_K_T, 32, (5120,), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_gate_up_m32", "grouped_ws", Q4_K_T, 32, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_down_m32", "gemv_accum_ws", Q6_K_T, 32, (5120,), 13824, ["k_gemv_dq<14,0,2,1>"]),
+    # the down projections on the MMQ layout (FusedQuantGemm::DownProjMmq):
+    # row-split rows at M <= 2, tiles above, ordered K splits
+    ("c2m_down_m1", "mmq_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1>"]),
+    ("c2m_down_m4", "mmq_accum_ws", Q6_K, 4, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
+    ("c2m_down_m8", "mmq_accum_ws", Q6_K, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
+    ("c4m_down_m16", "mmq_accum_ws", Q6_K, 16, (5120,), 13824,
+     ["k_gemv_slot<14,16,4,0,2,0,1>"]),
+    ("c4m_down_m32", "mmq_accum_ws", Q6_K, 32, (5120,), 13824, ["k_gemv_dq<14,0,2,1>"]),
     # packed (per-row symmetric int8) activations at M = 1: config 1, the 3B
     # QKV triple and down projection, the 14B gate/up pair
     ("c1_packed_m1", "packed", Q4_K, 1, (11008,), 2048, ["k_gemv_packed<12,1,2>"]),

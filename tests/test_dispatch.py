@@ -31,6 +31,9 @@ def dry_dispatch(entry, qt, M, Ns, K):
             rc = L.ifx_qgemv_ws(qt, W[0], A, Y[0], ops.OUT_F32,
                                 ops.ACCUM if entry == "gemv_accum_ws" else ops.STORE, None, M,
                                 Ns[0], K, WS, 1 << 30, None)
+        elif entry in ("mmq_accum", "mmq_accum_ws"):
+            rc = L.ifx_qgemv_mmq(qt, W[0], A, Y[0], ops.OUT_F32, ops.ACCUM, M, Ns[0], K,
+                                 int(entry == "mmq_accum_ws"), None)
         elif entry == "grouped_ws":
             rc = L.ifx_qgemv_grouped_ws(qt, n, W, Y, NN, A, ops.OUT_F32, ops.STORE, M, K, WS,
                                         1 << 30, None)
@@ -86,29 +89,6 @@ def test_dry_run_launches_nothing_and_log_closes():
     rc, kernels = dry_dispatch("gemv", ops.Q4_K, 1, (64,), 256)
     assert rc == 0 and len(kernels) == 1
     assert L.ifx_launch_log_end().decode() == ""
-
-
-def test_decode_ffn_routing():
-    """The single-launch FFN entry at the 3B shape: the O GEMV with the fused
-    quantizer, then the FFN kernel; shapes beyond it are not handled."""
-    from inferflux_amd import _lib, ops
-    L = _lib.load()
-    f = [_fake(i) for i in range(9)]
-    ws = ops.decode_ffn_workspace_bytes(1, 11008)
-
-    def call(hidden, ffn, M=1):
-        with ops.launch_log(dry=True) as lg:
-            rc = L.ifx_decode_ffn(ops.Q4_K, f[0], f[1], ops.OUT_F32, 2048, f[2], f[3], 1e-6,
-                                  ops.Q4_K, f[4], f[5], ffn, ops.Q6_K, f[6], M, hidden, f[7], ws,
-                                  None)
-        return rc, lg.kernels
-    assert call(2048, 11008) == (0, ["k_gemv<12,1,1,1,4,0,2,3>", "k_decode_ffn"])
-    with ops.launch_log(dry=True) as lg:  # W_o NULL: the FFN kernel alone
-        rc = L.ifx_decode_ffn(ops.Q4_K, None, None, ops.OUT_F32, 2048, f[2], f[3], 1e-6,
-                              ops.Q4_K, f[4], f[5], 11008, ops.Q6_K, f[6], 1, 2048, f[7], ws, None)
-    assert rc == 0 and lg.kernels == ["k_decode_ffn"]
-    assert call(5120, 13824)[0] == 2  # hidden beyond half-wave rows: not handled
-    assert call(2048, 11008, M=2)[0] == 2
 
 
 def test_tiled_routing():

@@ -36,6 +36,8 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     raw_qt = qt % 100 if qt > 100 else qt
 
     def to_dev(w, n):
+        if entry.startswith("mmq"):
+            return ops.mmq_layout(qt, up(w, dev), n, K)
         if qt > 200:
             return ops.repack_tiled(raw_qt, up(w, dev), n, K)[1]
         if qt > 100:
@@ -48,6 +50,7 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     if entry.endswith("_ws"):
         entry = entry[:-3]
         nb = (ops.gate_up_silu_workspace_bytes(qt, M, Ns[0], K) if entry == "gate_up_silu"
+              else 0 if entry == "mmq_accum"  # the layout's own
               else ops.qgemv_workspace_bytes(qt, list(Ns), M, K))
         wsp = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
     rng = np.random.default_rng(seed)
@@ -77,9 +80,12 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     with ops.launch_log() as lg:
         if entry == "gemv":
             outs = [ops.qgemv(qt, W[0], A, M, Ns[0], K, workspace=wsp)]
-        elif entry in ("gemv_accum", "quantize_accum"):
+        elif entry in ("gemv_accum", "quantize_accum", "mmq_accum"):
             y0 = up(base[:, :Ns[0]], dev)
-            if entry == "gemv_accum":
+            if entry == "mmq_accum":
+                ops.qgemv_mmq(qt, W[0], A, M, Ns[0], K, out=y0, mode=ops.ACCUM,
+                              ordered=wsp is not None)
+            elif entry == "gemv_accum":
                 ops.qgemv(qt, W[0], A, M, Ns[0], K, out=y0, mode=ops.ACCUM, workspace=wsp)
             else:
                 ops.qgemv_grouped_rmsnorm(qt, W, X, None, M, list(Ns), K, outs=[y0],
@@ -144,7 +150,7 @@ def test_bench_launch(orc, dev, lid, entry, qt, M, Ns, K, want):
     for i, (w, n, y) in enumerate(zip(ws, Ns, outs)):
         idx = _rows(n, seed + i)
         ye = orc.gemv_exact(raw_qt, w[idx], a, M, len(idx), K)
-        if entry in ("gemv_accum", "quantize_accum"):
+        if entry in ("gemv_accum", "quantize_accum", "mmq_accum"):
             ye = ye + base[:, idx]
         yd = down(y)
         assert np.isfinite(yd).all()

@@ -43,6 +43,31 @@ def test_quantize_rows_symmetric_bit_exact(orc, dev, dtype, M, K):
     assert np.array_equal(down(scales).view(np.uint32), s_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_quantize_rows_symmetric_offset_views(orc, dev, dtype):
+    """Inputs and codes at odd element offsets (views into larger buffers):
+    the vector loads need 16- / 8-byte and the code stores 4-byte alignment,
+    so these calls take the scalar form and still give the oracle's bits."""
+    import torch
+    from inferflux_amd import ops, synth
+    M, K = 3, 2048
+    note(f"quantize_rows_symmetric offset views {dtype}")
+    x = synth.activations(M, K, seed=5, outlier_frac=0.01)
+    big = _to_dtype(np.concatenate([np.zeros(1, np.float32), x.ravel()]), dtype, dev)
+    xv = big[1:].view(M, K)  # one element past an aligned base
+    cbig = torch.empty(M * K + 1, dtype=torch.int8, device=dev)
+    cv = cbig[1:].view(M, K)
+    codes, scales = ops.quantize_rows_symmetric(xv, codes=cv)
+    c_ref, s_ref = orc.quantize_rows_symmetric(down(xv.float()))
+    assert np.array_equal(down(codes), c_ref)
+    assert np.array_equal(down(scales).view(np.uint32), s_ref.view(np.uint32))
+    ubig = _to_dtype(np.concatenate([np.zeros(1, np.float32), x.ravel() * 0.5]), dtype, dev)
+    codes, scales = ops.silu_mul_quantize_rows_symmetric(xv, ubig[1:].view(M, K), codes=cv)
+    c2, s2 = ops.silu_mul_quantize_rows_symmetric(xv.clone(), ubig[1:].view(M, K).clone())
+    assert np.array_equal(down(codes), down(c2))  # the same codes as aligned inputs
+    assert np.array_equal(down(scales), down(s2))
+
+
 def test_quantize_rows_symmetric_reference_kat(dev):
     """cuda_kernel::QuantizeRowsSymmetric's contract test
     (tests/unit/test_native_forward.cpp:7181-7238), fp16 input."""

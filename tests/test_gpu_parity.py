@@ -615,6 +615,19 @@ def test_host_cpp_gpu():
     assert r.returncode == 0, r.stdout + r.stderr
 
 
+def test_host_cpp_down_proj_gpu():
+    """BuildDownProjMmqLayout + DownProjMmq through the C++ mirror on the 3B
+    (2048 x 11008 Q6_K, M = 1/2/4/8) and 14B (5120 x 13824 Q6_K, M = 16/32)
+    down projections and Q4_K cases, against the oracle, plus the
+    producer-fused extensions (tests/cpp/test_down_proj_mmq.cpp)."""
+    import subprocess
+    from tests.test_host_cpp import BIN_MMQ, binary
+    note("host cpp down-proj mmq gpu cases")
+    r = subprocess.run([binary(BIN_MMQ), "gpu"], capture_output=True, text=True, timeout=110)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 # ------------------------------------------------ fused Q8_1 producers
 def _q8_1_fields(a):
     b = a.reshape(a.shape[0], -1, 36)
