@@ -23,6 +23,11 @@ COMMON = [
 # the dispatch and launch geometry (tuning sweeps only; see ifx_common.h).
 if os.environ.get("IFX_TUNING") == "1":
     COMMON.append("-DIFX_TUNING")
+    if os.environ.get("IFX_STAMPS") == "1":  # wave timelines (IFX_STAMP)
+        COMMON.append("-DIFX_STAMPS")
+    # a tuning build goes to its own directory, never over the product library
+    OBJ = os.environ.get("IFX_BUILD_OUT", os.path.join(HERE, "_build_tuning"))
+    LIB = os.path.join(OBJ, "libifx_qgemm.so")
 # Bit-exact kernels: no fp contraction anywhere in these translation units.
 EXACT = {"quantize.hip", "dequant.hip"}
 SOURCES = ["api.hip", "quantize.hip", "dequant.hip", "gemv.hip", "mmq_skinny.hip", "mmvq.hip", "gemm_mfma.hip", "gemv_lds.hip", "gemv_slot.hip", "gemm_f16.hip", "gemv_dq.hip", "packed.hip",

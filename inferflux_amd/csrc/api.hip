@@ -411,7 +411,9 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
 
 }  // namespace
 
+
 extern "C" {
+
 
 int ifx_block_bytes(int quant_type) {
   switch (quant_type) {

@@ -166,6 +166,8 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
   constexpr int LPR = 64 / H;                       // lanes per row set
   constexpr int SV = kWide<QT, MC> ? 64 : 32;       // values per slice
   __shared__ float red[(G > 1) ? P * G * V : 1];
+  [[maybe_unused]] constexpr int kStampBase = NORM == 1 ? 0 : NORM == 3 ? 1 : 3;
+  IFX_STAMP(0);
   const int bx = blockIdx.x;
   const GemvSeg sg = pick_seg(args, bx);
   // the activation pointer is needed by every lane; using it here keeps its
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       if (s0 < nslice) q4k_wide_load<R>(wt, Wr, voff, soff, s0);
     }
     __syncthreads();
+    IFX_STAMP(1);
     const ALdsS as{a_lds, a_str, static_cast<uint32_t>(K / 64 * 80)};
     for (int s = s0; s < nslice; s += LPR * G) {
       if (s != s0) q4k_wide_load<R>(wt, Wr, voff, soff, s);
@@ -283,6 +286,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       q8_0_slice<MC, R>(Wrs, Ar, rows, a_row, mvalid, s, acc);
   }
 
+  IFX_STAMP(2);
   // Sum each partial over the wave (DPP adds, no LDS); lane 63 ends with
   // all V totals, then across the G waves of the row group through LDS.
   float v[V];
@@ -329,6 +333,7 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
       Yf[o_idx] = y;
     }
   }
+  IFX_STAMP(3);
 }
 
 template <int QT, int MC, int R, int G, int H = 1>
@@ -651,6 +656,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_swiglu_wide(const SwigluArgs a
   __shared__ float gu[2][MC][32];  // [gate/up][column][output]
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[NORM ? MC * split_row_bytes(kSwigluWideMaxK) : 1];
   __shared__ float npart[4 * MC];
+  [[maybe_unused]] constexpr int kStampBase = 2;
+  IFX_STAMP(0);
   const int M = args.M, N = args.N, K = args.K;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -705,6 +712,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_swiglu_wide(const SwigluArgs a
                                threadIdx.x);
     }
     __syncthreads();
+    IFX_STAMP(1);
     const ALdsS as{a_lds, static_cast<uint32_t>(split_row_bytes(K)), static_cast<uint32_t>(K / 64 * 80)};
     for (int s = lt; s < nslice; s += 32) {
       if (s != lt) q4k_wide_load<R>(wt, Wr, voff, soff, s);
@@ -717,6 +725,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_swiglu_wide(const SwigluArgs a
       q4k_wide_compute<MC, R>(wt, as, mvalid, s, acc);
     }
   }
+  IFX_STAMP(2);
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -725,6 +734,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_swiglu_wide(const SwigluArgs a
       if (lt == 31) gu[is_up][c][orow0 + r] = v;
     }
   __syncthreads();
+  IFX_STAMP(3);
   const int c = threadIdx.x >> 3, l = threadIdx.x & 7;
   if (c < MC && (c == 0 || c < mvalid)) {  // whole 8-lane groups (mvalid >= 1)
     const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[0][c][4 * l]);
@@ -901,3 +911,17 @@ hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, 
 }
 
 }  // namespace ifx
+
+#ifdef IFX_STAMPS
+// Tuning builds: copies the wave timeline records of this file's kernels (8
+// int64 per wave, see IFX_STAMP) to host memory, then clears them; returns
+// the record count.
+extern "C" int ifx_debug_stamps(long long *out, int max_waves) {
+  const int n = max_waves < ifx::kStampWaves ? max_waves : ifx::kStampWaves;
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(ifx::ifx_stamps)) != hipSuccess) return -1;
+  if (hipMemcpy(out, p, static_cast<size_t>(n) * 64, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  if (hipMemset(p, 0, static_cast<size_t>(ifx::kStampWaves) * 64) != hipSuccess) return -1;
+  return n;
+}
+#endif

@@ -31,6 +31,36 @@ namespace ifx {
 // Tuning overrides of the dispatch and launch geometry (IFX_PREFILL,
 // IFX_DQ, IFX_SLOT_KW, ...) are read only in tuning builds (-DIFX_TUNING):
 // a product build always takes the measured defaults the tests pin.
+// Wave timelines for tuning builds (-DIFX_STAMPS): IFX_STAMP(k) has the
+// lowest active lane of each wave of a launch write the constant 100 MHz clock to slot k (0..7)
+// of its record in ifx_stamps (one record of 8 int64 per wave: region
+// kStampBase (a constant the kernel defines, 0..3) of 16384 waves, then
+// blockIdx.x major, then blockIdx.y, then the wave); the host reads the
+// buffer through ifx_debug_stamps.  Product builds compile the macro to nothing.
+#ifdef IFX_STAMPS
+constexpr int kStampWaves = 1 << 16;
+// one array per translation unit (no relocatable device code): a tuning
+// build instruments the kernels of one file at a time (gemv.hip)
+static __device__ long long ifx_stamps[kStampWaves * 8];
+#define IFX_STAMP(k)                                                                              \
+  do {                                                                                            \
+    const long long t_ = static_cast<long long>(__builtin_amdgcn_s_memrealtime());                \
+    const int w_ = kStampBase * 16384 +                                                           \
+                   (static_cast<int>(blockIdx.x) * static_cast<int>(gridDim.y) +                  \
+                    static_cast<int>(blockIdx.y)) * static_cast<int>(blockDim.x >> 6) +           \
+                   static_cast<int>(threadIdx.x >> 6);                                            \
+    const unsigned long long b_ = __ballot(1);                                                    \
+    if (static_cast<unsigned long long>(threadIdx.x & 63) ==                                      \
+            static_cast<unsigned long long>(__ffsll(static_cast<long long>(b_)) - 1) &&            \
+        w_ < kStampWaves)                                                                         \
+      ifx_stamps[w_ * 8 + (k)] = t_;                                                              \
+  } while (0)
+#else
+#define IFX_STAMP(k) \
+  do {               \
+  } while (0)
+#endif
+
 inline const char *tuning_env(const char *name) {
 #ifdef IFX_TUNING
   return getenv(name);
