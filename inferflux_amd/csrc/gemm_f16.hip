@@ -57,7 +57,23 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kPitch = kBK + 8;  // halves per staged row (144 B: conflict-free b128 reads)
+// A staged row is its 64 K values as eight 16-byte groups, unpadded; group
+// g of row r sits at position g ^ swz(r).  The swizzle makes both access
+// patterns conflict-free on 64 banks (16 lanes per b128 phase) and on 32
+// banks (8 lanes): the MFMA operand reads (lane l: row l % 32, group
+// 2 ks + l / 32) and the stage writes (threads 2r, 2r + 1: both halves of
+// row r, activations groups 4 p + j, Q4_K / Q6_K weights 2 p, 2 p + 1,
+// 4 + 2 p, 5 + 2 p).  With a 72-half padded pitch and no swizzle the writes
+// were 2-way conflicted (counters: about one conflict cycle per LDS
+// instruction).  The table was found by exhaustive search over the two bank
+// models.
+constexpr int kPitch = kBK;  // halves per staged row
+__device__ __forceinline__ int swz(int r) {
+  // (r & 1) ^ g[(r >> 1) & 7] with g = {0, 6, 3, 5, 1, 7, 2, 4}
+  return (r & 1) ^ ((0x8B9AF0 >> (3 * ((r >> 1) & 7))) & 7);
+}
+// Halves offset of group g of row r in a stage buffer.
+__device__ __forceinline__ int slot(int r, int g) { return r * kPitch + 8 * (g ^ swz(r)); }
 #ifndef IFX_F16_VALU_PER_MFMA
 #define IFX_F16_VALU_PER_MFMA 5
 #endif
@@ -194,19 +210,21 @@ template <int QT, bool AH>
 __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int item) {
   const int row = item >> 1, part = item & 1;
   if constexpr (AH) {
-    u32x4 *dst = reinterpret_cast<u32x4 *>(&sm.a[buf][row * kPitch + 32 * part]);
-    dst[0] = r.a0;
-    dst[1] = r.a1;
-    dst[2] = r.a2;
-    dst[3] = r.a3;
+    _Float16 *arow = sm.a[buf];
+    *reinterpret_cast<u32x4 *>(arow + slot(row, 4 * part)) = r.a0;
+    *reinterpret_cast<u32x4 *>(arow + slot(row, 4 * part + 1)) = r.a1;
+    *reinterpret_cast<u32x4 *>(arow + slot(row, 4 * part + 2)) = r.a2;
+    *reinterpret_cast<u32x4 *>(arow + slot(row, 4 * part + 3)) = r.a3;
   } else {  // activations: 32 values of block `part` at slots 32*part ..
     uint32_t o[16];
     q8_1_block_to_h(r.ads, r.a0, r.a1, o);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(&sm.a[buf][row * kPitch + 32 * part]);
+    _Float16 *arow = sm.a[buf];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4 *>(arow + slot(row, 4 * part + j)) =
+          u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
   }
-  _Float16 *wrow = &sm.w[buf][row * kPitch];
+  _Float16 *wbuf = sm.w[buf];
   if constexpr (QT == kTypeQ4_K) {
     // 16 qs bytes: values 16*part .. +15 of sub-blocks 2p (low nibbles) and
     // 2p + 1 (high nibbles); get_scale_min_k4 (quant_common.cuh:83-94).
@@ -232,12 +250,10 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
       q4x4_to_h<0>(in[j], d0, n0, lo[2 * j], lo[2 * j + 1]);
       q4x4_to_h<1>(in[j], d1, n1, hi[2 * j], hi[2 * j + 1]);
     }
-    u32x4 *dlo = reinterpret_cast<u32x4 *>(wrow + 16 * part);
-    u32x4 *dhi = reinterpret_cast<u32x4 *>(wrow + 32 + 16 * part);
-    dlo[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-    dlo[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-    dhi[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-    dhi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 2 * part)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 2 * part + 1)) = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 4 + 2 * part)) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 5 + 2 * part)) = u32x4{hi[4], hi[5], hi[6], hi[7]};
   } else if constexpr (QT == kTypeQ6_K) {
     // ql (w0) and qh (w1) bytes of values 16*part .. +15 of sub-blocks hf
     // (low nibbles, qh bits 2hf..2hf+1) and hf + 2 (high nibbles, qh bits
@@ -259,12 +275,10 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
       u8x4_to_h(clo, b, dl, zero, lo[2 * j], lo[2 * j + 1]);
       u8x4_to_h(chi, b, dh, zero, hi[2 * j], hi[2 * j + 1]);
     }
-    u32x4 *dlo = reinterpret_cast<u32x4 *>(wrow + 16 * part);
-    u32x4 *dhi = reinterpret_cast<u32x4 *>(wrow + 32 + 16 * part);
-    dlo[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-    dlo[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-    dhi[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-    dhi[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 2 * part)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 2 * part + 1)) = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 4 + 2 * part)) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4 *>(wbuf + slot(row, 5 + 2 * part)) = u32x4{hi[4], hi[5], hi[6], hi[7]};
   } else {
     // one Q8_0 block (32 values) at slots 32*part ..; dequant_q8_0_element
     // (quant_common.cuh:185-188)
@@ -273,9 +287,10 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
     const uint32_t in[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) i8x4_to_h(in[j], d, o[2 * j], o[2 * j + 1]);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(wrow + 32 * part);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4 *>(wbuf + slot(row, 4 * part + j)) =
+          u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
   }
 }
 
@@ -381,12 +396,14 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       h8 fa[kFM], fb[4];
+      // rows arow + 32 i (brow + 32 j) share swz(arow) (swz(brow)): period 16
+      const int ga = 8 * ((2 * ks + h) ^ swz(arow)), gb = 8 * ((2 * ks + h) ^ swz(brow));
 #pragma unroll
       for (int i = 0; i < kFM; ++i)
-        fa[i] = *reinterpret_cast<const h8 *>(sa + (arow + 32 * i) * kPitch + ks * 16 + 8 * h);
+        fa[i] = *reinterpret_cast<const h8 *>(sa + (arow + 32 * i) * kPitch + ga);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const h8 *>(sw + (brow + 32 * j) * kPitch + ks * 16 + 8 * h);
+        fb[j] = *reinterpret_cast<const h8 *>(sw + (brow + 32 * j) * kPitch + gb);
 #pragma unroll
       for (int i = 0; i < kFM; ++i)
 #pragma unroll
