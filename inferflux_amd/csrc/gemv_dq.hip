@@ -288,31 +288,41 @@ __device__ __forceinline__ void compute(const RawW<QT> &r, const _Float16 *sa, i
 
 // Stage the activations of super-blocks [sb0, sb0 + cnt) as fp16: row m at
 // sa + m * pitch, values in the order (0, 2, 1, 3) of each group of four.
-// Up to 4 Q8_1 blocks per thread, all loads issued before any conversion.
-__device__ __forceinline__ void stage_a(_Float16 *sa, int pitch, rsrc_t Ar, uint32_t a_row, int M,
-                                        int sb0, int cnt, int tid) {
-  const int items = M * 8 * cnt;
+// Up to 4 Q8_1 blocks per thread.  stage_a_load issues the loads with no
+// branch around them (items past the end re-read the last one, unused), so
+// that the weight loads issued after it do not hold them up (a wave's loads
+// complete in issue order); stage_a_store converts and stores.
+struct StageA {
   uint32_t ds[4];
   u32x4 q0[4], q1[4];
+};
+
+__device__ __forceinline__ void stage_a_load(StageA &st, rsrc_t Ar, uint32_t a_row, int M, int sb0,
+                                             int cnt, int tid) {
+  const int items = M * 8 * cnt;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int it = tid + 256 * u;
-    if (it < items) {
-      const int m = it / (8 * cnt), j = it - m * 8 * cnt;
-      const uint32_t o = m * a_row + (sb0 * 8 + j) * kQ8_1Bytes;
-      ds[u] = bload<uint32_t>(Ar, o, 0);
-      q0[u] = bload<u32x4>(Ar, o + 4, 0);
-      q1[u] = bload<u32x4>(Ar, o + 20, 0);
-    }
+    const int it = min(tid + 256 * u, items - 1);
+    const int m = it / (8 * cnt), j = it - m * 8 * cnt;
+    const uint32_t o = m * a_row + (sb0 * 8 + j) * kQ8_1Bytes;
+    st.ds[u] = bload<uint32_t>(Ar, o, 0);
+    st.q0[u] = bload<u32x4>(Ar, o + 4, 0);
+    st.q1[u] = bload<u32x4>(Ar, o + 20, 0);
   }
+}
+
+__device__ __forceinline__ void stage_a_store(const StageA &st, _Float16 *sa, int pitch, int M,
+                                              int cnt, int tid) {
+  const int items = M * 8 * cnt;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int it = tid + 256 * u;
     if (it < items) {
       const int m = it / (8 * cnt), j = it - m * 8 * cnt;
-      const h2 d = splat(h2f(ds[u] & 0xFFFFu));
+      const h2 d = splat(h2f(st.ds[u] & 0xFFFFu));
       u32x4 *dst = reinterpret_cast<u32x4 *>(sa + m * pitch + 32 * j);
-      const uint32_t in[8] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y, q1[u].z, q1[u].w};
+      const uint32_t in[8] = {st.q0[u].x, st.q0[u].y, st.q0[u].z, st.q0[u].w,
+                              st.q1[u].x, st.q1[u].y, st.q1[u].z, st.q1[u].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         uint32_t o[4];
@@ -371,13 +381,18 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
 
   // Three super-blocks of weights in flight per wave (register ring), the
-  // first two issued before the activation stage is built.
+  // first two issued right after the activation stage's loads, so that the
+  // stage (small, cache-resident) completes without waiting behind them.
+  StageA st;
+  stage_a_load(st, Ar, a_row, M, sb_begin, cnt, tid);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_sched_barrier(0);
   RawW<QT> w0, w1, w2;
-  if (cnt > 0) fetch_w<QT, TL>(w0, Wr, row_off, sb_begin, h, l32);
-  if (cnt > 1) fetch_w<QT, TL>(w1, Wr, row_off, sb_begin + 1, h, l32);
+  fetch_w<QT, TL>(w0, Wr, row_off, sb_begin, h, l32);  // cnt >= 1
+  fetch_w<QT, TL>(w1, Wr, row_off, sb_begin + min(1, cnt - 1), h, l32);
   for (int i = tid; i < pitch / 8; i += 64 * kWaves)
     reinterpret_cast<u32x4 *>(lds + M * pitch)[i] = u32x4{0, 0, 0, 0};
-  stage_a(lds, pitch, Ar, a_row, M, sb_begin, cnt, tid);
+  stage_a_store(st, lds, pitch, M, cnt, tid);
   __syncthreads();
 
   auto step = [&](const RawW<QT> &cur, RawW<QT> &fut, int i) {
