@@ -91,14 +91,18 @@ struct NativeExecutionPolicy {
   // Deterministic K splits (no reference counterpart).  Where a kernel
   // splits K over workgroups, the plain launches add the splits' partial sums
   // with fp32 atomics (as the reference's accumulate kernels), so the last
-  // bits vary run to run.  With deterministic_reductions set:
+  // bits vary run to run.
+  //  * Gemv* / GemvQ8_1Pair / GemvQ8_1Triple add them in split order
+  //    through reduction_workspace (caller-owned device memory, 256-byte
+  //    aligned, zeroed once after allocation, ReductionWorkspaceBytes for
+  //    the launch) whenever it is given and large enough, so a caller that
+  //    provides scratch gets the same bits on every call; with
+  //    deterministic_reductions set a split launch without such a workspace
+  //    is not handled (false), without it the launch takes the atomics.
   //  * DownProjMmq* add them in split order through the layout's own
-  //    workspace (fp16 outputs always do);
-  //  * Gemv* / GemvQ8_1Pair / GemvQ8_1Triple do the same through
-  //    reduction_workspace (caller-owned device memory, 256-byte aligned,
-  //    zeroed once after allocation, ReductionWorkspaceBytes for the
-  //    launch); a launch that splits without a large enough workspace is not
-  //    handled (false).
+  //    workspace with deterministic_reductions set (fp16 outputs always do);
+  //    otherwise with atomics, which are faster there (14B down at M = 32:
+  //    about 20 against 25 us).
   // Calls that share a workspace (or a layout) must not overlap.
   bool deterministic_reductions{false};
   void *reduction_workspace{nullptr};

@@ -56,6 +56,21 @@ bool ViewCovers(const QuantizedWeightInfo &w, int N, int K) {
          w.num_elements >= static_cast<int64_t>(N) * static_cast<int64_t>(K);
 }
 
+// How a launch that splits K adds its splits' partial sums.  need: the
+// ordered workspace bytes of the launch (0: it does not split, so the plain
+// launch is already deterministic).  With deterministic_reductions the
+// ordered reduction is required (no large enough workspace: not handled);
+// without it, a caller-given reduction_workspace that fits (size and
+// 256-byte alignment) selects it too, and anything else takes fp32 atomics.
+enum class Reduction { kAtomic, kOrdered, kRefuse };
+Reduction SplitReduction(const NativeExecutionPolicy &p, int64_t need) {
+  if (need <= 0) return Reduction::kAtomic;
+  const bool fits = p.reduction_workspace && p.reduction_workspace_bytes >= need &&
+                    reinterpret_cast<uintptr_t>(p.reduction_workspace) % 256 == 0;
+  if (fits) return Reduction::kOrdered;
+  return p.deterministic_reductions ? Reduction::kRefuse : Reduction::kAtomic;
+}
+
 bool Launch(const QuantizedWeightInfo &w, const void *act, void *out, int out_dtype, int mode,
             const void *bias, int M, int N, int K, hipStream_t stream,
             const NativeExecutionPolicy *policy) {
@@ -65,11 +80,13 @@ bool Launch(const QuantizedWeightInfo &w, const void *act, void *out, int out_dt
   const FusedDispatchGeometry g{M, N, K, 1, true, false};
   if (!FusedQuantGemm::ShouldUseFusedPath(w.quant_type, g)) return false;
   const NativeExecutionPolicy p = Resolve(policy);
-  if (p.deterministic_reductions &&
-      ifx_qgemv_workspace_bytes(w.quant_type, 1, &N, out_dtype, M, K) > 0)
-    return p.reduction_workspace &&
-           ifx_qgemv_ws(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K,
+  switch (SplitReduction(p, ifx_qgemv_workspace_bytes(w.quant_type, 1, &N, out_dtype, M, K))) {
+  case Reduction::kRefuse: return false;
+  case Reduction::kOrdered:
+    return ifx_qgemv_ws(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K,
                         p.reduction_workspace, p.reduction_workspace_bytes, stream) == IFX_OK;
+  case Reduction::kAtomic: break;
+  }
   return ifx_qgemv(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K, stream) ==
          IFX_OK;
 }
@@ -92,13 +109,16 @@ bool LaunchGroup(const std::array<PackedProjectionSpec, C> &p, const void *act, 
   const FusedDispatchGeometry g{M, N[0], K, static_cast<int>(C), true, false};
   if (!FusedQuantGemm::ShouldUseFusedPath(p[0].weight.quant_type, g)) return false;
   const NativeExecutionPolicy pol = Resolve(policy);
-  if (pol.deterministic_reductions &&
-      ifx_qgemv_workspace_bytes(p[0].weight.quant_type, static_cast<int>(C), N, IFX_OUT_F16, M,
-                                K) > 0)
-    return pol.reduction_workspace &&
-           ifx_qgemv_grouped_ws(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
+  switch (SplitReduction(pol, ifx_qgemv_workspace_bytes(p[0].weight.quant_type,
+                                                        static_cast<int>(C), N, IFX_OUT_F16, M,
+                                                        K))) {
+  case Reduction::kRefuse: return false;
+  case Reduction::kOrdered:
+    return ifx_qgemv_grouped_ws(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
                                 IFX_OUT_F16, IFX_STORE, M, K, pol.reduction_workspace,
                                 pol.reduction_workspace_bytes, stream) == IFX_OK;
+  case Reduction::kAtomic: break;
+  }
   return ifx_qgemv_grouped(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
                            IFX_OUT_F16, IFX_STORE, M, K, stream) == IFX_OK;
 }

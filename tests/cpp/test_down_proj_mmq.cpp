@@ -350,7 +350,9 @@ void TestDownProj(int qtype, int M, int N, int K) {
 
 // deterministic_reductions on the raw-weight entries: a launch that splits
 // K needs reduction_workspace (else it is not handled); with it, two calls
-// give the same bits and pass the oracle bar.
+// give the same bits and pass the oracle bar.  Without the flag a large
+// enough workspace gives the same ordered reduction, a smaller one the
+// atomic form.
 void TestDeterministicGemv(int qtype, int M, int N, int K) {
   std::printf("[gpu deterministic gemv] qtype=%d M=%d N=%d K=%d\n", qtype, M, N, K);
   std::fflush(stdout);
@@ -378,6 +380,24 @@ void TestDeterministicGemv(int qtype, int M, int N, int K) {
   HIP_OK(hipMemcpy(b.data(), y, b.size() * 4, hipMemcpyDeviceToHost));
   EXPECT(a == b);
   EXPECT(RowsClose(a, p.ye, M, N, 1e-3, false));
+  // without the flag, the caller's workspace alone selects the ordered
+  // reduction: the same bits again
+  NativeExecutionPolicy scratch;
+  scratch.reduction_workspace = ws.p;
+  scratch.reduction_workspace_bytes = wsb;
+  EXPECT(FusedQuantGemm::GemvQ8_1F32(w, da.p, y, M, N, K, nullptr, &scratch));
+  HIP_OK(hipDeviceSynchronize());
+  HIP_OK(hipMemcpy(b.data(), y, b.size() * 4, hipMemcpyDeviceToHost));
+  EXPECT(a == b);
+  // a workspace below the launch's size without the flag: the atomic form
+  // still runs (and passes the bar)
+  if (wsb > 0) {
+    scratch.reduction_workspace_bytes = wsb - 256;
+    EXPECT(FusedQuantGemm::GemvQ8_1F32(w, da.p, y, M, N, K, nullptr, &scratch));
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(b.data(), y, b.size() * 4, hipMemcpyDeviceToHost));
+    EXPECT(RowsClose(b, p.ye, M, N, 1e-3, false));
+  }
 }
 
 // The producer-fused extensions against the oracle chain: RMSNorm + Q8_1
