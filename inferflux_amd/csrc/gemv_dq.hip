@@ -38,6 +38,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace ifx {
 
@@ -351,11 +352,12 @@ template <int QT, bool F16OUT, int SPLIT, bool TL = false, bool SW = false>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int bx = blockIdx.x;
-  const int si = SW ? static_cast<int>(threadIdx.x >> 7)  // waves 0-1 gate, 2-3 up
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar descriptors
+  const int si = SW ? wave >> 1  // waves 0-1 gate, 2-3 up
                  : (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
                  : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
   const DqSeg &sg = args.seg[si];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
   const int M = args.M, K = args.K, N = sg.N;
   const int nsb = K >> 8;
@@ -520,6 +522,236 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_gemv_dq(const DqArgs args) {
 
 namespace {
 
+// Rolling-stage form without a K split, for launches wide enough to fill
+// the chip with one workgroup per 128-row group (k_gemv_dqr): each workgroup
+// walks the whole K of its rows, so the sums need no cross-workgroup
+// reduction (no partial-sum traffic, no zero fill, the same bits every run).
+// The activations pass through two LDS stages of C super-blocks: the next
+// step's Q8_1 loads are issued right after a step's barrier, ahead of that
+// step's weight loads, and converted into the idle stage after the step's
+// units, so waiting for them waits only for weights the step itself uses
+// (a wave's loads complete in issue order).  WV = 8: two waves per row
+// slice (one per half of the SIMDs' wave slots), taking alternate
+// super-blocks; their sums meet in LDS at the end.  Each wave keeps D of
+// its super-blocks in flight across steps.
+template <int C, int NT>
+struct StageR {
+  static constexpr int kSlots = 1024 / NT;  // M * 8 * C <= 1024 Q8_1 blocks
+  uint32_t ds[kSlots];
+  u32x4 q0[kSlots], q1[kSlots];
+};
+
+// Loads of step s (super-blocks s*C .. s*C + C - 1; past the end the last
+// one is re-read: finite values that meet zero weights).
+template <int C, int NT>
+__device__ __forceinline__ void stage_r_load(StageR<C, NT> &st, rsrc_t Ar, uint32_t a_row, int M,
+                                             int step, int nsb, int tid) {
+  const int items = M * 8 * C;
+#pragma unroll
+  for (int u = 0; u < StageR<C, NT>::kSlots; ++u) {
+    const int it = min(tid + NT * u, items - 1);
+    const int m = it / (8 * C), j = it - m * (8 * C);
+    const int sb = min(step * C + (j >> 3), nsb - 1);
+    const uint32_t o = m * a_row + (sb * 8 + (j & 7)) * kQ8_1Bytes;
+    st.ds[u] = bload<uint32_t>(Ar, o, 0);
+    st.q0[u] = bload<u32x4>(Ar, o + 4, 0);
+    st.q1[u] = bload<u32x4>(Ar, o + 20, 0);
+  }
+}
+
+template <int C, int NT>
+__device__ __forceinline__ void stage_r_store(const StageR<C, NT> &st, _Float16 *sa, int pitch,
+                                              int M, int tid) {
+  const int items = M * 8 * C;
+#pragma unroll
+  for (int u = 0; u < StageR<C, NT>::kSlots; ++u) {
+    const int it = tid + NT * u;
+    if (it < items) {
+      const int m = it / (8 * C), j = it - m * (8 * C);
+      const h2 d = splat(h2f(st.ds[u] & 0xFFFFu));
+      u32x4 *dst = reinterpret_cast<u32x4 *>(sa + m * pitch + 32 * j);
+      const uint32_t in[8] = {st.q0[u].x, st.q0[u].y, st.q0[u].z, st.q0[u].w,
+                              st.q1[u].x, st.q1[u].y, st.q1[u].z, st.q1[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t o[4];
+        i8x4_to_h(in[2 * k], d, o[0], o[1]);
+        i8x4_to_h(in[2 * k + 1], d, o[2], o[3]);
+        dst[k] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// grid: one workgroup per 128-row group (all projections; SW: 64 outputs,
+// row slices 0-1 gate and 2-3 up); 64 * WV threads.  Dynamic LDS: two
+// stages of (M + 1) rows of pitch C * 256 + 8 halves (row M zero).
+template <int QT, bool F16OUT, bool TL, bool SW, int C, int D, int WV>
+__global__ __launch_bounds__(64 * WV, 1) void k_gemv_dqr(const DqArgs args) {
+  constexpr int NT = 64 * WV, kHalves = WV / 4, Cw = C / kHalves;
+  static_assert((WV == 4 || WV == 8) && C % kHalves == 0, "row slices");
+  static_assert(D == Cw || D == 2 * Cw, "ring and stage steps");
+  [[maybe_unused]] constexpr int kStampBase = 0;
+  IFX_STAMP(0);
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int bx = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar descriptors
+  const int rw = wave & 3, half = wave >> 2;  // row slice; which super-blocks (WV = 8)
+  const int si = SW ? rw >> 1
+                 : (args.nseg > 2 && bx >= args.seg[2].blk_begin) ? 2
+                 : (args.nseg > 1 && bx >= args.seg[1].blk_begin) ? 1 : 0;
+  const DqSeg &sg = args.seg[si];
+  const int l32 = lane & 31, h = lane >> 5;
+  const int M = args.M, K = args.K, N = sg.N;
+  const int nsb = K >> 8;
+  const int nsteps = (nsb + C - 1) / C;
+  constexpr int kPitch = C * 256 + 8;  // halves; 4 dwords mod 64 banks
+
+  const uint32_t a_row = static_cast<uint32_t>(K >> 5) * kQ8_1Bytes;
+  const uint32_t w_row = static_cast<uint32_t>(
+      QT == kTypeQ8_0 ? (K >> 5) * kQ8_0Bytes : (K >> 8) * (QT == kTypeQ4_K ? kQ4KBytes : kQ6KBytes));
+  const rsrc_t Wr = make_rsrc(sg.W, w_row * static_cast<uint32_t>(TL ? (N + 31) & ~31 : N));
+  const rsrc_t Ar = make_rsrc(args.A, a_row * static_cast<uint32_t>(M));
+  const int n = SW ? bx * 64 + (rw & 1) * 32 + l32
+                   : (bx - sg.blk_begin) * kRowsPerWg + rw * 32 + l32;
+  const uint32_t row_off = TL ? static_cast<uint32_t>(n >> 5) * 32 * w_row
+                              : static_cast<uint32_t>(min(n, N - 1)) * w_row;
+  const int stage_halves = (M + 1) * kPitch;
+  const int arow_off = (l32 < M ? l32 : M) * kPitch;  // batch rows past M read the zero row M
+
+  // the wave's super-block i (K order i * kHalves + half); past the end:
+  // out of range, zeros, no reads
+  auto fetch = [&](RawW<QT> &r, int i) {
+    const int t = i * kHalves + half;
+    fetch_w<QT, TL>(r, Wr, t < nsb ? row_off : 0xF0000000u, min(t, nsb - 1), h, l32);
+  };
+
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
+
+  // prologue: stage 0's loads, the ring's first D - 1 super-blocks, stage 0
+  StageR<C, NT> st;
+  stage_r_load<C, NT>(st, Ar, a_row, M, 0, nsb, tid);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_sched_barrier(0);
+  RawW<QT> w[D];
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j) fetch(w[j], j);
+  for (int i = tid; i < kPitch / 8; i += NT) {
+    reinterpret_cast<u32x4 *>(lds + M * kPitch)[i] = u32x4{0, 0, 0, 0};
+    reinterpret_cast<u32x4 *>(lds + stage_halves + M * kPitch)[i] = u32x4{0, 0, 0, 0};
+  }
+  stage_r_store<C, NT>(st, lds, kPitch, M, tid);
+  __syncthreads();
+  IFX_STAMP(1);
+
+  // one stage step; off: the ring slot of its first super-block (a constant:
+  // the loop below takes D / Cw steps per pass)
+  auto step = [&](auto off, int s) {
+    const _Float16 *sa = lds + (s & 1) * stage_halves + arow_off;
+    // the next step's activations, ahead of this step's weight loads
+    stage_r_load<C, NT>(st, Ar, a_row, M, s + 1, nsb, tid);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < Cw; ++u) {
+      fetch(w[(decltype(off)::value + u + D - 1) % D], s * Cw + u + D - 1);
+      compute<QT>(w[(decltype(off)::value + u) % D], sa + 256 * (u * kHalves + half), h, acc0, acc1);
+    }
+    if (s + 1 < nsteps) stage_r_store<C, NT>(st, lds + ((s + 1) & 1) * stage_halves, kPitch, M, tid);
+    __syncthreads();
+    if (s < 5) IFX_STAMP(2 + s);
+  };
+  for (int s = 0; s < nsteps; s += D / Cw) {
+    step(std::integral_constant<int, 0>{}, s);
+    if constexpr (D == 2 * Cw) {
+      if (s + 1 < nsteps) step(std::integral_constant<int, Cw>{}, s + 1);
+    }
+  }
+
+  // lane holds column n and batch rows 8*(i/4) + 4*h + (i%4)
+  float yv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) yv[i] = acc0[i] + acc1[i];
+  if constexpr (WV == 8) {
+    // the second half's sums -> LDS [row slice][16][64], added by the first
+    float *red = reinterpret_cast<float *>(lds) + rw * 1024 + lane;
+    if (half) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) red[64 * i] = yv[i];
+    }
+    __syncthreads();
+    if (!half) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) yv[i] += red[64 * i];
+    }
+  }
+  if constexpr (SW) {
+    // gate / up sums of the 64 outputs -> LDS [projection][batch row][64]
+    // (past the stages and the halves' sums)
+    float *gu = reinterpret_cast<float *>(lds) + (WV == 8 ? 4096 : 0);
+    const int proj = rw >> 1, col = (rw & 1) * 32 + l32;
+    if (!half) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+        if (m < M) gu[(proj * kMaxM + m) * 64 + col] = yv[i];
+      }
+    }
+    __syncthreads();
+    const int n0 = bx * 64;
+    for (int it = tid; it < M * 16; it += NT) {
+      const int blk = it >> 3, l = it & 7, m = blk >> 1, b = blk & 1;
+      const int o = n0 + 32 * b + 4 * l;
+      if (n0 + 32 * b >= N) continue;
+      const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&gu[m * 64 + 32 * b + 4 * l]);
+      const f32x4 u4 = *reinterpret_cast<const f32x4 *>(&gu[(kMaxM + m) * 64 + 32 * b + 4 * l]);
+      const f32x4 hv = silu_mul4(g4, u4);
+      const int64_t oh = static_cast<int64_t>(m) * N + o;
+      if (args.H) {
+        if (args.h_f16) {
+          const u32x2 hh = {f2h_bits(hv.x) | (f2h_bits(hv.y) << 16),
+                            f2h_bits(hv.z) | (f2h_bits(hv.w) << 16)};
+          *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(args.H) + oh) = hh;
+        } else {
+          *reinterpret_cast<f32x4 *>(static_cast<float *>(args.H) + oh) = hv;
+        }
+      }
+      if (args.Q)
+        quantize4_store(hv.x, hv.y, hv.z, hv.w,
+                        args.Q + (static_cast<int64_t>(m) * (N >> 5) + (o >> 5)) * kQ8_1Bytes, l);
+    }
+    IFX_STAMP(7);
+    return;
+  }
+  IFX_STAMP(7);
+  if (half || n >= N) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+    if (m >= M) continue;
+    const int64_t o = static_cast<int64_t>(m) * N + n;
+    float y = yv[i];
+    if constexpr (F16OUT) {
+      uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
+      if (args.mode == 1) y += h2f(Yh[o]);
+      else if (args.mode == 2) y += h2f(static_cast<const uint16_t *>(sg.bias)[n]);
+      Yh[o] = static_cast<uint16_t>(f2h_bits(y));
+    } else {
+      float *Yf = static_cast<float *>(sg.Y);
+      if (args.mode == 1) y += Yf[o];
+      else if (args.mode == 2) y += static_cast<const float *>(sg.bias)[n];
+      Yf[o] = y;
+    }
+  }
+}
+
+namespace {
+
 // Largest K range (super-blocks) whose fp16 activation stage fits kLdsBytes.
 int dq_sb_max(int M) { return max(1, (kLdsBytes / 2 / (M + 1) - 8) / 256); }
 
@@ -537,12 +769,41 @@ int dq_splits(int groups, int nsb, int M, bool no_split) {
   return max(need, min(nsb, (target + groups - 1) / groups));
 }
 
-// Row groups and K splits of a launch (sets blk_begin and sb_per).
-void dq_plan(DqArgs &args, bool no_split, int splits_req, int &groups, int &ks) {
+// Launches with at least this many row groups of 128 (three quarters of
+// the 256 CUs) take the no-split rolling-stage form, k_gemv_dqr: measured on
+// the 14B gate/up pair (216 groups), it beats the K split with its partial
+// sums.  IFX_DQR_GROUPS overrides (tuning; read once; 0 = never).
+int dqr_min_groups() {
+  static const int v = [] {
+    const char *e = ifx::tuning_env("IFX_DQR_GROUPS");
+    return e ? atoi(e) : 192;
+  }();
+  return v;
+}
+
+// Whether a launch of `groups` row groups takes k_gemv_dqr.  Q8_0 up to
+// M = 16 stays on the K split (its deeper ring leaves one wave per SIMD,
+// measured slower on the 151936-row LM head).
+bool dq_rolling(int qtype, int groups, int M, int splits_req) {
+  return dqr_min_groups() > 0 && groups >= dqr_min_groups() && splits_req == 0 &&
+         !(qtype % 100 == kTypeQ8_0 && M <= 16);
+}
+
+// Row groups and K splits of a launch (sets blk_begin and sb_per);
+// rolling: the launch takes k_gemv_dqr (ks = 1, sb_per unused).
+void dq_plan(DqArgs &args, int qtype, bool no_split, int splits_req, int &groups, int &ks,
+             bool *rolling = nullptr) {
   groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = groups;
     groups += (args.seg[i].N + kRowsPerWg - 1) / kRowsPerWg;
+  }
+  const bool roll = dq_rolling(qtype, groups, args.M, splits_req);
+  if (rolling) *rolling = roll;
+  if (roll) {
+    ks = 1;
+    args.sb_per = args.K >> 8;
+    return;
   }
   const int nsb = args.K >> 8;
   const int need = (nsb + dq_sb_max(args.M) - 1) / dq_sb_max(args.M);
@@ -552,11 +813,60 @@ void dq_plan(DqArgs &args, bool no_split, int splits_req, int &groups, int &ks) 
   ks = (nsb + args.sb_per - 1) / args.sb_per;
 }
 
+
+// The no-split rolling-stage launch (k_gemv_dqr): C super-blocks per stage
+// step (M * 8 * C <= 1024 Q8_1 blocks, two stages within 160 KB), D in
+// flight per wave.  groups: row groups of 128 (SW: pairs of 64 outputs).
+template <int QT, bool F16, bool TL, bool SW, int C, int D, int WV>
+hipError_t launch_dqr_c(const DqArgs &args, int groups, hipStream_t s) {
+  constexpr int kPitch = C * 256 + 8;
+  constexpr int kMaxMr = 1024 / (8 * C);  // the stage's batch rows
+  if (args.M > kMaxMr) return hipErrorInvalidValue;
+  const size_t shm = std::max(static_cast<size_t>(2) * (args.M + 1) * kPitch * 2,
+                              static_cast<size_t>(2 * 4096 * 4));  // halves' sums + gate/up sums
+  if (!dry_run()) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemv_dqr<QT, F16, TL, SW, C, D, WV>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        static_cast<int>(std::max(2 * (kMaxMr + 1) * kPitch * 2, 2 * 4096 * 4)));
+    if (attr != hipSuccess) return attr;
+  }
+  IFX_LAUNCH(k_gemv_dqr, (QT, F16, TL, SW, C, D, WV), dim3(groups), dim3(64 * WV), shm, s, args);
+  return last_error();
+}
+
+template <int QT, bool F16, bool TL, bool SW>
+hipError_t launch_dqr(const DqArgs &args, int groups, hipStream_t s) {
+  static const int wv = [] {
+    const char *e = ifx::tuning_env("IFX_DQR_WV");
+    return e ? atoi(e) : 8;
+  }();
+  static const int dd = [] {
+    const char *e = ifx::tuning_env("IFX_DQR_D");
+    return e ? atoi(e) : 2;
+  }();
+  if (wv == 4) {
+    if (args.M > 16) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 4>(args, groups, s);
+    return launch_dqr_c<QT, F16, TL, SW, 8, 8, 4>(args, groups, s);
+  }
+  if (args.M > 16) {
+    if (QT != kTypeQ8_0 && dd == 4) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 8>(args, groups, s);
+    return launch_dqr_c<QT, F16, TL, SW, 4, 2, 8>(args, groups, s);
+  }
+  return launch_dqr_c<QT, F16, TL, SW, 8, 4, 8>(args, groups, s);
+}
+
+
 template <int QT, bool TL>
 hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   const bool ordered = args.ws.cnt != nullptr;
   int groups = 0, ks = 1;
-  dq_plan(args, f16 && !ordered, splits_req, groups, ks);
+  bool rolling = false;
+  dq_plan(args, QT, f16 && !ordered, splits_req, groups, ks, &rolling);
+  if (rolling) {
+    if (f16) return launch_dqr<QT, true, TL, false>(args, groups, s);
+    return launch_dqr<QT, false, TL, false>(args, groups, s);
+  }
   // fp16 sums cannot be added with atomics: split only through the workspace
   if (f16 && ks > 1 && !ordered) return hipErrorInvalidValue;
   const size_t shm = static_cast<size_t>(args.M + 1) * (args.sb_per * 256 + 8) * 2;
@@ -604,10 +914,10 @@ hipError_t launch_sw(const DqArgs &args, int groups, int ks, hipStream_t s) {
 
 // The pair plan (gate and up as one grouped launch of two projections):
 // row groups, K splits and sb_per as the grouped launch chooses them.
-void sw_plan(DqArgs &args, int N, int &pair_groups, int &ks) {
+void sw_plan(DqArgs &args, int qtype, int N, int &pair_groups, int &ks, bool *rolling = nullptr) {
   args.seg[0].N = args.seg[1].N = N;
   args.nseg = 2;
-  dq_plan(args, false, 0, pair_groups, ks);
+  dq_plan(args, qtype, false, 0, pair_groups, ks, rolling);
 }
 
 }  // namespace
@@ -615,12 +925,12 @@ void sw_plan(DqArgs &args, int N, int &pair_groups, int &ks) {
 bool gemv_dq_fits(int qtype, int M, int K);
 
 // K splits of the fused gate/up/SiLU launch (1: no workspace needed).
-int gemv_dq_swiglu_splits(int M, int N, int K) {
+int gemv_dq_swiglu_splits(int qtype, int M, int N, int K) {
   DqArgs args{};
   args.M = M;
   args.K = K;
   int pg = 0, ks = 1;
-  sw_plan(args, N, pg, ks);
+  sw_plan(args, qtype, N, pg, ks);
   return ks;
 }
 
@@ -642,7 +952,20 @@ hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, cons
   args.Q = static_cast<uint8_t *>(Q);
   args.h_f16 = h_f16 ? 1 : 0;
   int pair_groups = 0, ks = 1;
-  sw_plan(args, N, pair_groups, ks);
+  bool rolling = false;
+  sw_plan(args, qtype, N, pair_groups, ks, &rolling);
+  const int groups = (N + 63) / 64;
+  if (rolling) {
+    switch (qtype) {
+    case kTypeQ4_K: return launch_dqr<kTypeQ4_K, false, false, true>(args, groups, stream);
+    case kTypeQ6_K: return launch_dqr<kTypeQ6_K, false, false, true>(args, groups, stream);
+    case kTypeQ8_0: return launch_dqr<kTypeQ8_0, false, false, true>(args, groups, stream);
+    case kTypeQ4_KT: return launch_dqr<kTypeQ4_K, false, true, true>(args, groups, stream);
+    case kTypeQ6_KT: return launch_dqr<kTypeQ6_K, false, true, true>(args, groups, stream);
+    case kTypeQ8_0T: return launch_dqr<kTypeQ8_0, false, true, true>(args, groups, stream);
+    default: return hipErrorInvalidValue;
+    }
+  }
   if (ks > 1) {
     if (!ws) return hipErrorInvalidValue;
     // the pair's workspace layout: counters for its row groups, then slots
@@ -650,7 +973,6 @@ hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, cons
     args.ws.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
                                              (static_cast<int64_t>(pair_groups) * 4 + 255) / 256 * 256);
   }
-  const int groups = (N + 63) / 64;
   switch (qtype) {
   case kTypeQ4_K: return launch_sw<kTypeQ4_K, false>(args, groups, ks, stream);
   case kTypeQ6_K: return launch_sw<kTypeQ6_K, false>(args, groups, ks, stream);
@@ -662,20 +984,28 @@ hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, cons
   }
 }
 
-// fp16 outputs are not split: their K must fit one activation stage.
+// Types and batch sizes of the fp16-dequant GEMV.
 bool gemv_dq_fits(int qtype, int M, int K) {
   return (qtype == kTypeQ4_K || qtype == kTypeQ6_K || qtype == kTypeQ8_0 || qtype == kTypeQ4_KT ||
           qtype == kTypeQ6_KT || qtype == kTypeQ8_0T) && M >= 1 &&
          M <= kMaxM && K % 256 == 0;
 }
 
+// fp16 outputs of the split form without a workspace: one activation stage
+// holds K.
 bool gemv_dq_fits_f16(int M, int K) { return M <= kMaxM && K / 256 <= dq_sb_max(M); }
+// ... or the launch (count projections of N rows) takes the no-split form.
+bool gemv_dq_f16_unsplit(int qtype, int count, const int *N, int M, int K) {
+  int groups = 0;
+  for (int i = 0; i < count; ++i) groups += (N[i] + kRowsPerWg - 1) / kRowsPerWg;
+  return M <= kMaxM && (K / 256 <= dq_sb_max(M) || dq_rolling(qtype, groups, M, 0));
+}
 
 // count projections (1..3) of one quant type share A; bias only with
 // count == 1.  splits_req: 0 = chosen from the shape.
 // Workspace bytes of the ordered split (0: the launch does not split):
 // counters (256-byte aligned) then one 16 KB slot per (row group, split).
-int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K) {
+int64_t gemv_dq_workspace_bytes(int qtype, int count, const int *N, bool f16, int M, int K) {
   DqArgs args{};
   for (int i = 0; i < count; ++i) args.seg[i].N = N[i];
   args.nseg = count;
@@ -683,7 +1013,7 @@ int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K)
   args.K = K;
   int groups = 0, ks = 1;
   (void)f16;  // fp16 outputs split as fp32 ones when the workspace is given
-  dq_plan(args, false, 0, groups, ks);
+  dq_plan(args, qtype, false, 0, groups, ks);
   if (ks <= 1) return 0;
   return (static_cast<int64_t>(groups) * 4 + 255) / 256 * 256 +
          static_cast<int64_t>(groups) * ks * kWaves * 64 * 16 * 4;
@@ -722,3 +1052,17 @@ hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *cons
 }
 
 }  // namespace ifx
+
+#ifdef IFX_STAMPS
+// Tuning builds: the wave timeline records of this file's kernels (8 int64
+// per wave, see IFX_STAMP) copied to host memory, then cleared; returns the
+// record count.
+extern "C" int ifx_debug_stamps_dq(long long *out, int max_waves) {
+  const int n = max_waves < ifx::kStampWaves ? max_waves : ifx::kStampWaves;
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(ifx::ifx_stamps)) != hipSuccess) return -1;
+  if (hipMemcpy(out, p, static_cast<size_t>(n) * 64, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  if (hipMemset(p, 0, static_cast<size_t>(ifx::kStampWaves) * 64) != hipSuccess) return -1;
+  return n;
+}
+#endif

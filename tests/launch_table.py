@@ -73,8 +73,7 @@ LAUNCHES = [
     ("c4_down_m16", "gemv_accum", Q6_K, 16, (5120,), 13824, ["k_mmvq<14,1,8,0>"]),
     ("c4_qkv_m32", "grouped", Q4_K, 32, QKV14, 5120, ["k_fill_zero", "k_gemv_dq<12,0,1>"]),
     ("c4_o_m32", "gemv_accum", Q4_K, 32, (5120,), 5120, ["k_gemv_dq<12,0,1>"]),
-    ("c4_gate_up_m32", "grouped", Q4_K, 32, (13824, 13824), 5120,
-     ["k_fill_zero", "k_gemv_dq<12,0,1>"]),
+    ("c4_gate_up_m32", "grouped", Q4_K, 32, (13824, 13824), 5120, ["k_gemv_dqr<12,0,0,0,4,2,8>"]),
     ("c4_down_m32", "gemv_accum", Q6_K, 32, (5120,), 13824, ["k_gemv_dq<14,0,1>"]),
     ("c4_qkv_m1", "grouped", Q4_K, 1, QKV14, 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
     ("c4_o_m1", "gemv_accum", Q4_K, 1, (5120,), 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
@@ -99,16 +98,18 @@ LAUNCHES = [
     ("c3_q6_k_t_m8", "gemv", Q6_K_T, 8, (151936,), 2048, ["k_gemv_slot<14,8,1,0,0,0,1>"]),
     ("c4t_qkv_m16", "grouped_ws", Q4_K_T, 16, QKV14, 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
     ("c4t_o_m16", "gemv_accum_ws", Q4_K_T, 16, (5120,), 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
-    ("c4t_gate_up_m16", "grouped_ws", Q4_K_T, 16, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
+    ("c4t_gate_up_m16", "grouped_ws", Q4_K_T, 16, (13824, 13824), 5120,
+     ["k_gemv_dqr<12,0,1,0,8,4,8>"]),
     ("c4t_down_m16", "gemv_accum_ws", Q6_K_T, 16, (5120,), 13824,
      ["k_gemv_slot<14,16,4,0,2,0,1>"]),
-    ("c4t_gate_up_silu_m16", "gate_up_silu_ws", Q4_K_T, 16, (13824,), 5120,
-     ["k_gemv_dq<12,0,2,1,1>"]),
-    ("c4t_gate_up_silu_m32", "gate_up_silu_ws", Q4_K_T, 32, (13824,), 5120,
-     ["k_gemv_dq<12,0,2,1,1>"]),
+    ("c4t_gate_up_silu_m16", "gate_up_silu", Q4_K_T, 16, (13824,), 5120,
+     ["k_gemv_dqr<12,0,1,1,8,4,8>"]),
+    ("c4t_gate_up_silu_m32", "gate_up_silu", Q4_K_T, 32, (13824,), 5120,
+     ["k_gemv_dqr<12,0,1,1,4,2,8>"]),
     ("c4t_qkv_m32", "grouped_ws", Q4_K_T, 32, QKV14, 5120, ["k_gemv_dq<12,0,2,1>"]),
     ("c4t_o_m32", "gemv_accum_ws", Q4_K_T, 32, (5120,), 5120, ["k_gemv_dq<12,0,2,1>"]),
-    ("c4t_gate_up_m32", "grouped_ws", Q4_K_T, 32, (13824, 13824), 5120, ["k_gemv_dq<12,0,2,1>"]),
+    ("c4t_gate_up_m32", "grouped_ws", Q4_K_T, 32, (13824, 13824), 5120,
+     ["k_gemv_dqr<12,0,1,0,4,2,8>"]),
     ("c4t_down_m32", "gemv_accum_ws", Q6_K_T, 32, (5120,), 13824, ["k_gemv_dq<14,0,2,1>"]),
     # the down projections on the MMQ layout (FusedQuantGemm::DownProjMmq):
     # row-split rows at M <= 2, tiles above, ordered K splits

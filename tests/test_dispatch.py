@@ -93,8 +93,8 @@ def test_dry_run_launches_nothing_and_log_closes():
 
 def test_tiled_routing():
     """Tiled weights: the slot-packed int8 MFMA GEMV for M <= 16 (wide Q4_K
-    launches: M <= 8) and the fp16-dequant MFMA GEMV above, both with the
-    layout flag; the
+    launches: M <= 8) and the fp16-dequant MFMA GEMV above (its no-split
+    form for 192 or more row groups), both with the layout flag; the
     gate/up/SiLU entry on the slot kernel from M = 1; M > 32 not handled."""
     from inferflux_amd import _lib, ops
     L = _lib.load()
@@ -122,5 +122,5 @@ def test_tiled_routing():
     assert L.ifx_tiled_bytes(ops.Q5_K, 32, 512) == 0
     rc, k = dry_dispatch("gemv", ops.Q8_0_T, 8, (151936,), 2048)
     assert rc == 0 and k == ["k_gemv_slot<8,8,1,0,0,0,1>"]
-    rc, k = dry_dispatch("gemv", ops.Q8_0_T, 32, (151936,), 2048)
-    assert rc == 0 and k[-1] == "k_gemv_dq<8,0,1,1>"
+    rc, k = dry_dispatch("gemv", ops.Q8_0_T, 32, (151936,), 2048)  # >= 192 row groups: no split
+    assert rc == 0 and k == ["k_gemv_dqr<8,0,1,0,4,2,8>"]
