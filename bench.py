@@ -805,7 +805,8 @@ def profile_kernels_run(args, dev):
     `steps` launches each of the config-5 prefill GEMMs on the fp16 kernel
     (and, where the shape uses one, with the activation workspace) and (a
     quarter as many) on the int8 kernel, of the config-4 14B grouped
-    gate+up and down launches at M = 32, and of config 1 and the 3B down
+    gate+up and down launches at M = 32 (and the fused gate/up/SiLU
+    launch on tiled rows, the bench's form), and of config 1 and the 3B down
     projection at M = 8 on raw and on tiled rows (weights rotating over
     >= 512 MB of replicas), then 20 copies of exactly 64 MiB for counter
     calibration.  Prints one JSON line of event timings."""
@@ -856,6 +857,17 @@ def profile_kernels_run(args, dev):
         Ys = [torch.empty((M, N), dtype=torch.float32, device=dev) for N in Ns]
         out[f"decode14b_{launch}_m32_us"] = timed(
             lambda i: ops.qgemv_grouped(qt, reps[i % R], A, M, Ns, K, outs=Ys), args.steps)
+        if launch == "gate_up":  # the bench's form: tiled rows, SiLU * up and Q8_1 fused in
+            treps = [[ops.repack_tiled(qt, w, N, K)[1] for w, N in zip(r, Ns)] for r in reps]
+            del reps
+            Q = torch.empty((M, Ns[0] // 32 * 36), dtype=torch.uint8, device=dev)
+            nb = ops.gate_up_silu_workspace_bytes(qt + 200, M, Ns[0], K)
+            wsd = torch.zeros(max(nb, 256), dtype=torch.uint8, device=dev)
+            out["decode14b_gate_up_silu_tiled_m32_us"] = timed(
+                lambda i: ops.qgemv_gate_up_silu(qt + 200, treps[i % R][0], treps[i % R][1], A, M,
+                                                 Ns[0], K, want_h=False, q8_1_out=Q,
+                                                 workspace=wsd if nb else None), args.steps)
+            reps = treps
         del reps, ws
         torch.cuda.empty_cache()
     # raw against tiled rows (ifx_repack_tiled) on the slot-packed GEMV: config 1
