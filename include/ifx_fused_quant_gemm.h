@@ -96,9 +96,11 @@ struct NativeExecutionPolicy {
   //    through reduction_workspace (caller-owned device memory, 256-byte
   //    aligned, zeroed once after allocation, ReductionWorkspaceBytes for
   //    the launch) whenever it is given and large enough, so a caller that
-  //    provides scratch gets the same bits on every call; with
-  //    deterministic_reductions set a split launch without such a workspace
-  //    is not handled (false), without it the launch takes the atomics.
+  //    provides scratch gets the same bits on every call (launches that need
+  //    none take the same deterministic kernels); with
+  //    deterministic_reductions set that holds without a workspace too, and
+  //    a split launch without a large enough one is not handled (false);
+  //    otherwise the launch takes the plain entry and its atomics.
   //  * DownProjMmq* add them in split order through the layout's own
   //    workspace with deterministic_reductions set (fp16 outputs always do);
   //    otherwise with atomics, which are faster there (14B down at M = 32:

@@ -172,10 +172,14 @@ int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *con
  * split stores its fp32 partial sums in the workspace and the last
  * workgroup of a tile to finish adds them in split order and writes Y: the
  * bits are the same run to run, and there is no zero-fill launch and no
- * atomic on Y.  Other launches are those of the plain entries.  workspace:
- * at least ifx_qgemv_workspace_bytes bytes, 256-byte aligned; its leading
- * counters must be zero before the first call (zero the buffer once after
- * allocating it) and every call leaves them zero.  Calls that share a
+ * atomic on Y.  Other launches are those of the plain entries, except fp32
+ * accumulate launches at 9 <= M <= 16, which the plain entries run on the
+ * fp16-dequant GEMV's atomic split and these on the integer kernels without
+ * a split.  workspace: at least ifx_qgemv_workspace_bytes bytes, 256-byte
+ * aligned; its leading counters must be zero before the first call (zero
+ * the buffer once after allocating it) and every call leaves them zero.
+ * workspace may be NULL with workspace_bytes 0: launches that need none run
+ * as above, the others return IFX_BAD_GEOMETRY.  Calls that share a
  * workspace must not overlap.  No reference counterpart (the reference's
  * split kernels add with fp32 atomics, mmvq.cuh:280-401). */
 int ifx_qgemv_ws(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,

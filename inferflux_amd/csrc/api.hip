@@ -186,7 +186,7 @@ bool use_skinny(int M) {
 bool use_lds(int qtype, int M, int K, int n_total) {
   static const int v = [] {
     const char *e = ifx::tuning_env("IFX_LDS");
-    return e ? (e[0] == '1' ? 1 : 0) : -1;
+    return e ? (e[0] == '1' ? 1 : e[0] == '2' ? 2 : 0) : -1;
   }();
   if (!ifx::gemv_lds_fits(qtype, M, K) || v == 0) return false;
   if (v == 1) return true;
@@ -206,7 +206,7 @@ bool use_lds(int qtype, int M, int K, int n_total) {
 bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
   static const int v = [] {
     const char *e = ifx::tuning_env("IFX_SLOT");
-    return e ? (e[0] == '1' ? 1 : 0) : -1;
+    return e ? (e[0] == '1' ? 1 : e[0] == '2' ? 2 : 0) : -1;
   }();
   if (!ifx::gemv_slot_fits(qtype, M, K) || v == 0) return false;
   if (v == 1) return true;
@@ -223,7 +223,7 @@ bool use_slot(int qtype, int M, int K, int n_total, bool f16) {
 int dq_env() {
   static const int v = [] {
     const char *e = ifx::tuning_env("IFX_DQ");
-    return e ? (e[0] == '1' ? 1 : 0) : -1;
+    return e ? (e[0] == '1' ? 1 : e[0] == '2' ? 2 : 0) : -1;
   }();
   return v;
 }
@@ -283,8 +283,24 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
 
 // Kernel route of ifx_qgemv (grouped = false) and ifx_qgemv_grouped
 // (grouped = true) for valid arguments; n_total = sum of the projections' N.
+// atomic_accum: a plain entry (no ordered reduction asked for) accumulating
+// into fp32 outputs.  Such Q4_K / Q6_K launches at 9 <= M <= 16 take the
+// fp16-dequant GEMV's atomic K split, which needs no zero fill in that mode
+// (measured on MI355X, 14B O / down at M = 16: 7.2 / 18.2 us against 10.3 /
+// 20.5 tiled on the slot GEMV, 7.6 / 27.1 against 10.3 / 31.2 raw on MMVQ;
+// 3B O 4.5 against 6.4) when they have 2048 rows or more; the store
+// launches and the ordered entries keep the integer kernels (the zero fill,
+// or the split's ordered reduction, costs more than it gains), and so do
+// narrow launches (integer-exact sums: a row of few outputs is no norm to
+// hide the fp16 weight rounding behind).
 enum class Route { F16Gemm, Gemv, Lds, Slot, Dq, Skinny, Mmvq, Mfma, PerProjection };
-Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
+Route route(int qt, int M, int K, int n_total, bool f16, bool grouped, bool atomic_accum = false) {
+  if (atomic_accum && !f16 && M > kMaxSlotM && M <= 2 * kMaxSlotM && n_total >= 2048 &&
+      dq_env() < 0 &&
+      (qt == IFX_TYPE_Q4_K || qt == IFX_TYPE_Q6_K || qt == IFX_TYPE_Q4_K_T ||
+       qt == IFX_TYPE_Q6_K_T) &&
+      ifx::gemv_dq_fits(qt, M, K))
+    return Route::Dq;
   if (tiled(qt)) {
     // measured on MI355X (14B / 3B shapes, cold weights): the slot-packed
     // GEMV (two 16-row slots above M = 8) up to M = 16, except wide Q4_K
@@ -292,7 +308,8 @@ Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
     // GEMV against 29.5); the fp16-dequant GEMV above M = 16 (Q6_K down
     // 5120 x 13824 M = 16: 19.0 us on the slot GEMV, 20.9 on fp16-dequant)
     if (M <= kMaxSlotM) return Route::Slot;
-    if (M <= 2 * kMaxSlotM && (qt == IFX_TYPE_Q6_K_T || n_total < 8192 || dq_env() == 0))
+    if (M <= 2 * kMaxSlotM && dq_env() != 2 &&
+        (qt == IFX_TYPE_Q6_K_T || n_total < 8192 || dq_env() == 0))
       return Route::Slot;
     return Route::Dq;
   }
@@ -309,24 +326,27 @@ Route route(int qt, int M, int K, int n_total, bool f16, bool grouped) {
 // The ordered-split workspace of a slot / dq launch: nullptr when there is
 // none (atomics) or the launch does not split; rc = IFX_BAD_GEOMETRY when
 // the caller's workspace is too small or not 256-byte aligned.
+// ordered: an ordered entry (ifx_qgemv_ws / _grouped_ws), whose launches
+// that split need the workspace (none given: IFX_BAD_GEOMETRY).
 void *split_ws(Route r, int qtype, void *ws, int64_t ws_bytes, int count, const int *N, bool f16,
-               int M, int K, int &rc) {
+               int M, int K, bool ordered, int &rc) {
   rc = IFX_OK;
-  if (!ws) return nullptr;
+  if (!ws && !ordered) return nullptr;
   const int64_t need = r == Route::Slot ? ifx::gemv_slot_workspace_bytes(count, N, f16, M, K)
                                         : ifx::gemv_dq_workspace_bytes(qtype, count, N, f16, M, K);
   if (need == 0) return nullptr;
-  if (ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) rc = IFX_BAD_GEOMETRY;
+  if (!ws || ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) rc = IFX_BAD_GEOMETRY;
   return ws;
 }
 
 int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,
-               const void *bias, int M, int N, int K, void *stream, void *ws, int64_t ws_bytes) {
+               const void *bias, int M, int N, int K, void *stream, void *ws, int64_t ws_bytes,
+               bool ordered) {
   const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
   if (rc != IFX_OK) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = out_dtype == IFX_OUT_F16;
-  const Route r = route(quant_type, M, K, N, f16, false);
+  const Route r = route(quant_type, M, K, N, f16, false, !ordered && mode == IFX_ACCUM);
   int wrc = IFX_OK;
   switch (r) {
   case Route::F16Gemm:
@@ -336,12 +356,12 @@ int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int o
   case Route::Lds:
     return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   case Route::Slot: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, wrc);
+    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s, w));
   }
   case Route::Dq: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, wrc);
+    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     // tiled weights: fp16 outputs split only through the workspace
     if (f16 && !w && !ifx::gemv_dq_f16_unsplit(quant_type, 1, &N, M, K)) return IFX_BAD_GEOMETRY;
@@ -358,7 +378,7 @@ int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int o
 
 int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y, const int *N,
                  const void *A_q8_1, int out_dtype, int mode, int M, int K, void *stream, void *ws,
-                 int64_t ws_bytes) {
+                 int64_t ws_bytes, bool ordered) {
   if (!W || !Y || !N) return IFX_NULL_POINTER;
   if (count < 1 || count > 3) return IFX_BAD_GEOMETRY;
   if (mode == IFX_BIAS) return IFX_BAD_GEOMETRY;
@@ -371,7 +391,7 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
   const bool f16 = out_dtype == IFX_OUT_F16;
   int n_total = 0;
   for (int i = 0; i < count; ++i) n_total += N[i];
-  const Route r = route(quant_type, M, K, n_total, f16, true);
+  const Route r = route(quant_type, M, K, n_total, f16, true, !ordered && mode == IFX_ACCUM);
   int wrc = IFX_OK;
   switch (r) {
   case Route::Gemv:
@@ -380,13 +400,13 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
   case Route::Lds:
     return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
   case Route::Slot: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, wrc);
+    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                            mode, s, w));
   }
   case Route::Dq: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, wrc);
+    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     if (f16 && !w && !ifx::gemv_dq_f16_unsplit(quant_type, count, N, M, K))  // tiled weights
       return IFX_BAD_GEOMETRY;
@@ -405,7 +425,7 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
   // batched decode and prefill: one launch per projection (each fills the chip)
   for (int i = 0; i < count; ++i) {
     const int rc = qgemv_impl(quant_type, W[i], A_q8_1, Y[i], out_dtype, mode, nullptr, M, N[i],
-                              K, stream, ws, ws_bytes);
+                              K, stream, ws, ws_bytes, ordered);
     if (rc != IFX_OK) return rc;
   }
   return IFX_OK;
@@ -565,30 +585,31 @@ int ifx_qgemv_packed(int quant_type, int count, const void *const *W, void *cons
 
 int ifx_qgemv(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype, int mode,
               const void *bias, int M, int N, int K, void *stream) {
-  return qgemv_impl(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream, nullptr, 0);
+  return qgemv_impl(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream, nullptr, 0,
+                    false);
 }
 
 int ifx_qgemv_ws(int quant_type, const void *W, const void *A_q8_1, void *Y, int out_dtype,
                  int mode, const void *bias, int M, int N, int K, void *workspace,
                  int64_t workspace_bytes, void *stream) {
-  if (!workspace) return IFX_NULL_POINTER;
+  if (!workspace && workspace_bytes != 0) return IFX_NULL_POINTER;
   return qgemv_impl(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K, stream, workspace,
-                    workspace_bytes);
+                    workspace_bytes, true);
 }
 
 int ifx_qgemv_grouped(int quant_type, int count, const void *const *W, void *const *Y,
                       const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                       void *stream) {
   return grouped_impl(quant_type, count, W, Y, N, A_q8_1, out_dtype, mode, M, K, stream, nullptr,
-                      0);
+                      0, false);
 }
 
 int ifx_qgemv_grouped_ws(int quant_type, int count, const void *const *W, void *const *Y,
                          const int *N, const void *A_q8_1, int out_dtype, int mode, int M, int K,
                          void *workspace, int64_t workspace_bytes, void *stream) {
-  if (!workspace) return IFX_NULL_POINTER;
+  if (!workspace && workspace_bytes != 0) return IFX_NULL_POINTER;
   return grouped_impl(quant_type, count, W, Y, N, A_q8_1, out_dtype, mode, M, K, stream,
-                      workspace, workspace_bytes);
+                      workspace, workspace_bytes, true);
 }
 
 int64_t ifx_qgemv_workspace_bytes(int quant_type, int count, const int *N, int out_dtype, int M,
@@ -945,7 +966,7 @@ int ifx_qgemv_mmq(int quant_type, const void *layout, const void *A_q8_1, void *
   const char *base = static_cast<const char *>(layout);
   if (M <= kMaxRowSplitM)
     return qgemv_impl(mmq_row_type(quant_type), base + ifx_mmq_layout_rows_offset(quant_type, N, K),
-                      A_q8_1, Y, out_dtype, mode, nullptr, M, N, K, stream, nullptr, 0);
+                      A_q8_1, Y, out_dtype, mode, nullptr, M, N, K, stream, nullptr, 0, false);
   // fp16 sums are split only through the workspace; fp32 ones on request
   void *ws = nullptr;
   int64_t wsb = 0;
@@ -955,7 +976,7 @@ int ifx_qgemv_mmq(int quant_type, const void *layout, const void *A_q8_1, void *
     if (wsb == 0) ws = nullptr;
   }
   return qgemv_impl(mmq_tiled_type(quant_type), layout, A_q8_1, Y, out_dtype, mode, nullptr, M, N,
-                    K, stream, ws, wsb);
+                    K, stream, ws, wsb, ordered || out_dtype == IFX_OUT_F16);
 }
 
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows, int K,

@@ -56,15 +56,20 @@ bool ViewCovers(const QuantizedWeightInfo &w, int N, int K) {
          w.num_elements >= static_cast<int64_t>(N) * static_cast<int64_t>(K);
 }
 
-// How a launch that splits K adds its splits' partial sums.  need: the
-// ordered workspace bytes of the launch (0: it does not split, so the plain
-// launch is already deterministic).  With deterministic_reductions the
-// ordered reduction is required (no large enough workspace: not handled);
-// without it, a caller-given reduction_workspace that fits (size and
-// 256-byte alignment) selects it too, and anything else takes fp32 atomics.
+// Which entry a launch takes.  need: the ordered workspace bytes of the
+// launch through the ordered entries (0: it does not split there).  With
+// deterministic_reductions the ordered entry is required (a split without a
+// large enough workspace: not handled); without it, a caller-given
+// reduction_workspace selects the ordered entry too when it fits (size and
+// 256-byte alignment) or is not needed, and anything else takes the plain
+// entry, whose K splits add with fp32 atomics (the plain entry may also
+// split launches the ordered entry runs unsplit: fp32 accumulate at
+// 9 <= M <= 16).
 enum class Reduction { kAtomic, kOrdered, kRefuse };
 Reduction SplitReduction(const NativeExecutionPolicy &p, int64_t need) {
-  if (need <= 0) return Reduction::kAtomic;
+  if (need <= 0)
+    return p.deterministic_reductions || p.reduction_workspace ? Reduction::kOrdered
+                                                               : Reduction::kAtomic;
   const bool fits = p.reduction_workspace && p.reduction_workspace_bytes >= need &&
                     reinterpret_cast<uintptr_t>(p.reduction_workspace) % 256 == 0;
   if (fits) return Reduction::kOrdered;
@@ -84,7 +89,8 @@ bool Launch(const QuantizedWeightInfo &w, const void *act, void *out, int out_dt
   case Reduction::kRefuse: return false;
   case Reduction::kOrdered:
     return ifx_qgemv_ws(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K,
-                        p.reduction_workspace, p.reduction_workspace_bytes, stream) == IFX_OK;
+                        p.reduction_workspace,
+                        p.reduction_workspace ? p.reduction_workspace_bytes : 0, stream) == IFX_OK;
   case Reduction::kAtomic: break;
   }
   return ifx_qgemv(w.quant_type, w.data, act, out, out_dtype, mode, bias, M, N, K, stream) ==
@@ -116,7 +122,8 @@ bool LaunchGroup(const std::array<PackedProjectionSpec, C> &p, const void *act, 
   case Reduction::kOrdered:
     return ifx_qgemv_grouped_ws(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,
                                 IFX_OUT_F16, IFX_STORE, M, K, pol.reduction_workspace,
-                                pol.reduction_workspace_bytes, stream) == IFX_OK;
+                                pol.reduction_workspace ? pol.reduction_workspace_bytes : 0,
+                                stream) == IFX_OK;
   case Reduction::kAtomic: break;
   }
   return ifx_qgemv_grouped(p[0].weight.quant_type, static_cast<int>(C), W, Y, N, act,

@@ -398,6 +398,32 @@ void TestDeterministicGemv(int qtype, int M, int N, int K) {
     HIP_OK(hipMemcpy(b.data(), y, b.size() * 4, hipMemcpyDeviceToHost));
     EXPECT(RowsClose(b, p.ye, M, N, 1e-3, false));
   }
+  if (wsb == 0) {
+    // accumulate into a fixed base: with the flag and no workspace, the
+    // same bits on every call; without a policy (the plain entry, whose
+    // fp32 accumulate launches at 9 <= M <= 16 split K with atomics) within
+    // the bar
+    std::vector<float> base(a.size());
+    std::vector<double> yb(p.ye);
+    for (size_t i = 0; i < base.size(); ++i) {
+      base[i] = 0.25f * static_cast<float>(i % 7) - 0.5f;
+      yb[i] += base[i];
+    }
+    auto run = [&](const NativeExecutionPolicy *pol, std::vector<float> &out) {
+      HIP_OK(hipMemcpy(y, base.data(), base.size() * 4, hipMemcpyHostToDevice));
+      EXPECT(FusedQuantGemm::GemvQ8_1AccumF32(w, da.p, y, M, N, K, nullptr, pol));
+      HIP_OK(hipDeviceSynchronize());
+      HIP_OK(hipMemcpy(out.data(), y, out.size() * 4, hipMemcpyDeviceToHost));
+    };
+    NativeExecutionPolicy det0;
+    det0.deterministic_reductions = true;
+    run(&det0, a);
+    run(&det0, b);
+    EXPECT(a == b);
+    EXPECT(RowsClose(a, yb, M, N, 1e-3, false));
+    run(nullptr, b);
+    EXPECT(RowsClose(b, yb, M, N, 1e-3, false));
+  }
 }
 
 // The producer-fused extensions against the oracle chain: RMSNorm + Q8_1
@@ -510,6 +536,7 @@ int main(int argc, char **argv) {
     TestDeterministicGemv(Q6_K, 8, 2048, 11008);  // slot GEMV, K split
     TestDeterministicGemv(Q4_K, 32, 5120, 5120);  // fp16-dequant GEMV, K split
     TestDeterministicGemv(Q4_K, 1, 2048, 2048);   // no split
+    TestDeterministicGemv(Q4_K, 16, 5120, 5120);  // accumulate: MMVQ, or the atomic split
     TestFusedProducers();
   } else {
     std::printf("usage: %s policy|gpu\n", argv[0]);

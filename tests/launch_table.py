@@ -68,9 +68,9 @@ LAUNCHES = [
     ("c3_q6_k_r_m1", "gemv", Q6_K_R, 1, (151936,), 2048, ["k_gemv<114,1,2,1,4,0,2>"]),
     # config 4: the 14B decode layer at M = 16 / 32, and its Q4_K launches at M = 1 / 8
     ("c4_qkv_m16", "grouped", Q4_K, 16, QKV14, 5120, ["k_mmvq<12,1,8,0>"]),
-    ("c4_o_m16", "gemv_accum", Q4_K, 16, (5120,), 5120, ["k_mmvq<12,1,8,0>"]),
+    ("c4_o_m16", "gemv_accum", Q4_K, 16, (5120,), 5120, ["k_gemv_dq<12,0,1>"]),
     ("c4_gate_up_m16", "grouped", Q4_K, 16, (13824, 13824), 5120, ["k_mmvq<12,1,2,0>"]),
-    ("c4_down_m16", "gemv_accum", Q6_K, 16, (5120,), 13824, ["k_mmvq<14,1,8,0>"]),
+    ("c4_down_m16", "gemv_accum", Q6_K, 16, (5120,), 13824, ["k_gemv_dq<14,0,1>"]),
     ("c4_qkv_m32", "grouped", Q4_K, 32, QKV14, 5120, ["k_fill_zero", "k_gemv_dq<12,0,1>"]),
     ("c4_o_m32", "gemv_accum", Q4_K, 32, (5120,), 5120, ["k_gemv_dq<12,0,1>"]),
     ("c4_gate_up_m32", "grouped", Q4_K, 32, (13824, 13824), 5120, ["k_gemv_dqr<12,0,0,0,4,2,8>"]),
@@ -102,6 +102,10 @@ LAUNCHES = [
      ["k_gemv_dqr<12,0,1,0,8,4,8>"]),
     ("c4t_down_m16", "gemv_accum_ws", Q6_K_T, 16, (5120,), 13824,
      ["k_gemv_slot<14,16,4,0,2,0,1>"]),
+    # plain accumulate launches at 9 <= M <= 16: the fp16-dequant GEMV's atomic split
+    ("c4tp_o_m16", "gemv_accum", Q4_K_T, 16, (5120,), 5120, ["k_gemv_dq<12,0,1,1>"]),
+    ("c4tp_down_m16", "gemv_accum", Q6_K_T, 16, (5120,), 13824, ["k_gemv_dq<14,0,1,1>"]),
+    ("c2tp_o_m12", "gemv_accum", Q4_K_T, 12, (2048,), 2048, ["k_gemv_dq<12,0,1,1>"]),
     ("c4t_gate_up_silu_m16", "gate_up_silu", Q4_K_T, 16, (13824,), 5120,
      ["k_gemv_dqr<12,0,1,1,8,4,8>"]),
     ("c4t_gate_up_silu_m32", "gate_up_silu", Q4_K_T, 32, (13824,), 5120,
