@@ -295,7 +295,11 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
 // hide the fp16 weight rounding behind).
 enum class Route { F16Gemm, Gemv, Lds, Slot, Dq, Skinny, Mmvq, Mfma, PerProjection };
 Route route(int qt, int M, int K, int n_total, bool f16, bool grouped, bool atomic_accum = false) {
-  if (atomic_accum && !f16 && M > kMaxSlotM && M <= 2 * kMaxSlotM && n_total >= 2048 &&
+  static const int acc_min_m = [] {  // IFX_ACCUM_DQ_MIN_M (tuning; read once)
+    const char *e = ifx::tuning_env("IFX_ACCUM_DQ_MIN_M");
+    return e && atoi(e) > 0 ? atoi(e) : kMaxSlotM + 1;
+  }();
+  if (atomic_accum && !f16 && M >= acc_min_m && M <= 2 * kMaxSlotM && n_total >= 2048 &&
       dq_env() < 0 &&
       (qt == IFX_TYPE_Q4_K || qt == IFX_TYPE_Q6_K || qt == IFX_TYPE_Q4_K_T ||
        qt == IFX_TYPE_Q6_K_T) &&
