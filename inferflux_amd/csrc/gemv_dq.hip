@@ -781,12 +781,11 @@ int dqr_min_groups() {
   return v;
 }
 
-// Whether a launch of `groups` row groups takes k_gemv_dqr.  Q8_0 up to
-// M = 16 stays on the K split (its deeper ring leaves one wave per SIMD,
-// measured slower on the 151936-row LM head).
+// Whether a launch of `groups` row groups takes k_gemv_dqr.
 bool dq_rolling(int qtype, int groups, int M, int splits_req) {
-  return dqr_min_groups() > 0 && groups >= dqr_min_groups() && splits_req == 0 &&
-         !(qtype % 100 == kTypeQ8_0 && M <= 16);
+  (void)qtype;
+  (void)M;
+  return dqr_min_groups() > 0 && groups >= dqr_min_groups() && splits_req == 0;
 }
 
 // Row groups and K splits of a launch (sets blk_begin and sb_per);
@@ -849,7 +848,11 @@ hipError_t launch_dqr(const DqArgs &args, int groups, hipStream_t s) {
     if (args.M > 16) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 4>(args, groups, s);
     return launch_dqr_c<QT, F16, TL, SW, 8, 8, 4>(args, groups, s);
   }
-  if (args.M > 16) {
+  // Q8_0 (40 registers a super-block) keeps the 4-super-block stage and a
+  // 2-deep ring at every M: with 8 and 4 it runs one wave per SIMD (LM head
+  // 151936 x 2048 at M = 16: 90.8 us, against 75.3 on this form and 82.9 on
+  // the K split)
+  if (args.M > 16 || QT == kTypeQ8_0) {
     if (QT != kTypeQ8_0 && dd == 4) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 8>(args, groups, s);
     return launch_dqr_c<QT, F16, TL, SW, 4, 2, 8>(args, groups, s);
   }

@@ -5,13 +5,12 @@ whole K of its rows, staging the activations through LDS in steps.
 Checked against the fp64 oracle on sampled rows (1e-3 * ||y_row||_2) over
 ragged K (a partial last stage step, a single super-block), ragged N, every
 quant type on raw and tiled rows, batch sizes on both stage widths (M <= 16:
-8 super-blocks a step, above: 4), the store / accumulate / bias epilogues
+8 super-blocks a step; above, and Q8_0 at every M: 4), the store / accumulate / bias epilogues
 (bit for bit against the stored result plus the base or bias), fp16 outputs
 without a workspace, and the fused gate/up/SiLU form bit for bit against
 the grouped launch followed by silu_mul_quantize_q8_1.  The form asks for
 no workspace, ignores one given, and repeats its bits call after call; the
-launches just below the row-group threshold, and Q8_0 up to M = 16, keep
-the K split."""
+launches just below the row-group threshold keep the K split."""
 import numpy as np
 import pytest
 
@@ -48,6 +47,7 @@ CASES = [
     (Q6_K, False, 24, 24600, 512),  # ragged N: the last group 24 rows
     (Q8_0, True, 20, 24576, 256),  # one super-block
     (Q8_0, False, 32, 24576, 512),
+    (Q8_0, True, 12, 24576, 768),  # Q8_0: the 4-super-block stage at every M
     (Q4_K, True, 9, 24576, 2304),  # 9 super-blocks: steps of 8 and 1
     (Q4_K, True, 16, 24700, 768),
     (Q6_K, True, 32, 24576, 2048),
@@ -65,8 +65,9 @@ def test_rolling_gemv(orc, dev, qtype, tiled, M, N, K):
     assert ops.qgemv_workspace_bytes(qt, [N], M, K) == 0
     with ops.launch_log() as lg:
         y1 = down(ops.qgemv(qt, W, A, M, N, K, out=torch.full((M, N), 7.0, device=dev)))
-    assert lg.kernels == [f"k_gemv_dqr<{qtype},0,{int(tiled)},0,{4 if M > 16 else 8},"
-                          f"{2 if M > 16 else 4},8>"], lg.kernels
+    wide = M > 16 or qtype == Q8_0  # the 4-super-block stage
+    assert lg.kernels == [f"k_gemv_dqr<{qtype},0,{int(tiled)},0,{4 if wide else 8},"
+                          f"{2 if wide else 4},8>"], lg.kernels
     idx = sample(N, M)
     ye = orc.gemv_exact(qtype, w[idx], a, M, len(idx), K)
     check_rows(y1[:, idx], ye)
@@ -135,7 +136,8 @@ def test_rolling_fused_ragged(orc, dev, qtype, tiled, M, N, K):
 
 
 def test_rolling_thresholds(dev):
-    """191 row groups, and Q8_0 at M = 16, keep the K split."""
+    """191 row groups keep the K split; Q8_0 takes the 4-super-block stage
+    at every M."""
     import torch
     from inferflux_amd import ops
     w = torch.zeros(24576 * 34 * 16, dtype=torch.uint8, device=dev)
@@ -143,5 +145,5 @@ def test_rolling_thresholds(dev):
     with ops.launch_log() as lg:
         ops.qgemv(Q4_K, w, a, 32, 24448, 512)
         ops.qgemv(Q8_0 + 200, w, a, 16, 24576, 512)
-    assert [k.split("<")[0] for k in lg.kernels] == ["k_fill_zero", "k_gemv_dq", "k_fill_zero",
-                                                    "k_gemv_dq"], lg.kernels
+    assert lg.kernels == ["k_fill_zero", "k_gemv_dq<12,0,1>", "k_gemv_dqr<8,0,1,0,4,2,8>"], \
+        lg.kernels
