@@ -834,28 +834,16 @@ hipError_t launch_dqr_c(const DqArgs &args, int groups, hipStream_t s) {
   return last_error();
 }
 
+// 8 waves (two per row slice: 26.9 against 28.2 us for one, fused 14B
+// gate/up at M = 32); C = 4 super-blocks a stage step above M = 16, 8 up to
+// it; D = C / 2 super-blocks in flight per wave (D = C measured the same,
+// with a longer prologue).  Q8_0 (40 registers a super-block) keeps C = 4
+// and D = 2 at every M: with 8 and 4 it runs one wave per SIMD (LM head
+// 151936 x 2048 at M = 16: 90.8 us, against 75.3 on this form and 82.9 on
+// the K split).
 template <int QT, bool F16, bool TL, bool SW>
 hipError_t launch_dqr(const DqArgs &args, int groups, hipStream_t s) {
-  static const int wv = [] {
-    const char *e = ifx::tuning_env("IFX_DQR_WV");
-    return e ? atoi(e) : 8;
-  }();
-  static const int dd = [] {
-    const char *e = ifx::tuning_env("IFX_DQR_D");
-    return e ? atoi(e) : 2;
-  }();
-  if (wv == 4) {
-    if (args.M > 16) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 4>(args, groups, s);
-    return launch_dqr_c<QT, F16, TL, SW, 8, 8, 4>(args, groups, s);
-  }
-  // Q8_0 (40 registers a super-block) keeps the 4-super-block stage and a
-  // 2-deep ring at every M: with 8 and 4 it runs one wave per SIMD (LM head
-  // 151936 x 2048 at M = 16: 90.8 us, against 75.3 on this form and 82.9 on
-  // the K split)
-  if (args.M > 16 || QT == kTypeQ8_0) {
-    if (QT != kTypeQ8_0 && dd == 4) return launch_dqr_c<QT, F16, TL, SW, 4, 4, 8>(args, groups, s);
-    return launch_dqr_c<QT, F16, TL, SW, 4, 2, 8>(args, groups, s);
-  }
+  if (args.M > 16 || QT == kTypeQ8_0) return launch_dqr_c<QT, F16, TL, SW, 4, 2, 8>(args, groups, s);
   return launch_dqr_c<QT, F16, TL, SW, 8, 4, 8>(args, groups, s);
 }
 
