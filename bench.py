@@ -639,6 +639,17 @@ def main():
                                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                     "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
             del ws
+            # the ordered K split (ifx_qgemm_prefill_ordered), where the shape splits
+            nbo = ops.prefill_ordered_workspace_bytes(qt, M, N, K)
+            if nbo > ops.prefill_workspace_bytes(qt, M, N, K):
+                ws = torch.empty(nbo, dtype=torch.uint8, device=dev)
+                us = time_loop(lambda i: ops.qgemm_prefill_ordered(qt, w, A, M, N, K, ws, out=Y),
+                               max(10, args.steps // 10), 3)
+                tops = 2.0 * M * N * K / us / 1e6
+                res["f16_ordered"] = {"us": round(us, 1), "TOPS": round(tops, 1),
+                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                      "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
+                del ws
             res["default"] = "f16" if ops.kernel_family(qt, M, N, K) == 4 else "int8"
             # The reference's prefill path recreated on this GPU: dequantize W
             # to an FP16 scratch copy (ifx_dequantize, the counterpart of

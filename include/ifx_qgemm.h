@@ -278,6 +278,24 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
                          int out_dtype, int mode, const void *bias, int M, int N, int K,
                          void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Deterministic prefill: ifx_qgemm_prefill_ws whose K split (fp32 outputs
+ * of shapes with too few output tiles to fill the GPU, e.g. Q6_K
+ * 5120 x 27648 at M = 512: six splits) stores each split's fp32 tile in its
+ * own workspace slot and adds the slots in split order in a second launch,
+ * with no zero fill and no fp32 atomics: the same bits on every call.
+ * Workspace: at least ifx_qgemm_prefill_ordered_workspace_bytes bytes,
+ * 256-byte aligned (the fp16 activation copy where the shape uses one, then
+ * splits x M x N fp32 slots); it needs no clearing, and calls sharing one
+ * must not overlap.  Shapes that do not split run exactly
+ * ifx_qgemm_prefill_ws.  No reference counterpart (the reference's prefill
+ * GEMM, cublasGemmEx at transformer_forward.cu:1479, does not split K
+ * across launches of its own). */
+int64_t ifx_qgemm_prefill_ordered_workspace_bytes(int quant_type, int out_dtype, int M, int N,
+                                                  int K);
+int ifx_qgemm_prefill_ordered(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                              int out_dtype, int mode, const void *bias, int M, int N, int K,
+                              void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Size of the library's static device scratch (per GPU, held until the
  * process ends) that ifx_qgemm_prefill_noalloc uses as its workspace. */
 #define IFX_NOALLOC_SCRATCH_BYTES (16 << 20)

@@ -33,6 +33,9 @@ SIGNATURES = {
     "ifx_qgemv_gate_up_silu_rmsnorm": ([_i32, _vp, _vp, _vp, _i32, _vp, ctypes.c_float, _vp, _i32, _vp, _i32,
                                         _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_noalloc": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "ifx_qgemm_prefill_ordered_workspace_bytes": ([_i32, _i32, _i32, _i32, _i32], _i64),
+    "ifx_qgemm_prefill_ordered": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _i64,
+                                   _vp], _i32),
     "ifx_qgemm_prefill": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _vp], _i32),
     "ifx_qgemm_prefill_kernel": ([_i32, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp], _i32),
     "ifx_repacked_bytes": ([_i32, _i64, _i32], _i64),

@@ -51,7 +51,8 @@ bool gemm_f16_fits(int qtype, int K);
 int64_t gemm_f16_workspace_bytes(int M, int K);
 hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *A16, void *Y, const void *bias,
                            bool f16, int M, int N, int K, int mode, int splits_req,
-                           hipStream_t stream);
+                           hipStream_t stream, float *slots = nullptr);
+int64_t gemm_f16_slot_bytes(bool f16, int M, int N, int K);
 hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, const int *N,
                                const void *x, bool x_f16, const uint16_t *norm_w, float eps,
                                bool f16, int M, int K, int mode, hipStream_t stream);
@@ -804,6 +805,47 @@ int ifx_qgemm_prefill_ws(int quant_type, const void *W, const void *A_q8_1, void
   return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, workspace, Y, bias,
                                         out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
                                         static_cast<hipStream_t>(stream)));
+}
+
+// The ordered prefill's workspace: the fp16 activation copy of
+// ifx_qgemm_prefill_ws (when the shape uses one), 256-byte aligned, then
+// the K splits' slots (when the launch splits K).
+int64_t ordered_a16_bytes(int quant_type, int M, int N, int K) {
+  return (ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K) + 255) / 256 * 256;
+}
+int64_t ordered_slot_bytes(int quant_type, int out_dtype, int M, int N, int K) {
+  if (!is_weight_type(quant_type) || gemv_only(quant_type) || repacked(quant_type) || M <= 0 ||
+      N <= 0 || K <= 0 || !use_f16_gemm(quant_type, M, K) || !ifx::gemm_f16_fits(quant_type, K))
+    return 0;
+  return ifx::gemm_f16_slot_bytes(out_dtype == IFX_OUT_F16, M, N, K);
+}
+
+int64_t ifx_qgemm_prefill_ordered_workspace_bytes(int quant_type, int out_dtype, int M, int N,
+                                                  int K) {
+  const int64_t slots = ordered_slot_bytes(quant_type, out_dtype, M, N, K);
+  const int64_t a16 = ifx_qgemm_prefill_workspace_bytes(quant_type, M, N, K);
+  return slots ? ordered_a16_bytes(quant_type, M, N, K) + slots : a16;
+}
+
+int ifx_qgemm_prefill_ordered(int quant_type, const void *W, const void *A_q8_1, void *Y,
+                              int out_dtype, int mode, const void *bias, int M, int N, int K,
+                              void *workspace, int64_t workspace_bytes, void *stream) {
+  const int rc = check_gemm_args(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K);
+  if (rc != IFX_OK) return rc;
+  if (gemv_only(quant_type) || repacked(quant_type)) return IFX_UNSUPPORTED_TYPE;
+  const int64_t slots = ordered_slot_bytes(quant_type, out_dtype, M, N, K);
+  if (slots == 0)  // no K split: the workspace entry is already deterministic
+    return ifx_qgemm_prefill_ws(quant_type, W, A_q8_1, Y, out_dtype, mode, bias, M, N, K,
+                                workspace, workspace_bytes, stream);
+  if (!workspace) return IFX_NULL_POINTER;
+  const int64_t a16 = ordered_a16_bytes(quant_type, M, N, K);
+  if (workspace_bytes < a16 + slots || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return IFX_BAD_GEOMETRY;
+  uint8_t *base = static_cast<uint8_t *>(workspace);
+  return status_of(ifx::launch_gemm_f16(quant_type, W, A_q8_1, a16 ? base : nullptr, Y, bias,
+                                        out_dtype == IFX_OUT_F16, M, N, K, mode, 0,
+                                        static_cast<hipStream_t>(stream),
+                                        reinterpret_cast<float *>(base + a16)));
 }
 
 int ifx_qgemm_prefill_noalloc(int quant_type, const void *W, const void *A_q8_1, void *Y,

@@ -302,7 +302,10 @@ __device__ __forceinline__ void commit(Smem &sm, int buf, const Raw<QT> &r, int 
 // a third less LDS operand traffic per MFMA and twice the conversion work
 // per thread.
 // Each workgroup covers K stages [split * cps, min(nst, (split + 1) * cps)).
-template <int QT, int WV, bool F16OUT, bool ATOMIC, bool AH>
+// SPL: 0 one split; 1 K splits added into Y with fp32 atomics; 2 K splits
+// stored to their own slots (Y = the slots, split s at Y + s * M * N, no
+// epilogue; k_split_sum adds them in split order).
+template <int QT, int WV, bool F16OUT, int SPL, bool AH>
 __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restrict__ W,
                                                          const uint8_t *__restrict__ A,
                                                          void *__restrict__ Y,
@@ -434,7 +437,9 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemm_f16(const uint8_t *__restri
         if (m >= M) continue;
         const int64_t o = static_cast<int64_t>(m) * N + n;
         float y = acc[i][j][e];
-        if constexpr (ATOMIC) {
+        if constexpr (SPL == 2) {
+          static_cast<float *>(Y)[static_cast<int64_t>(split) * M * N + o] = y;
+        } else if constexpr (SPL == 1) {
           if (mode == 2 && split == 0) y += static_cast<const float *>(bias)[n];
           atomicAdd(static_cast<float *>(Y) + o, y);
         } else if constexpr (F16OUT) {
@@ -472,13 +477,43 @@ __global__ __launch_bounds__(256) void k_q8_1_to_f16(const uint8_t *__restrict__
   out[t] = u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// The ordered reduction of the SPL = 2 GEMM: y = ((s_0 + s_1) + ...) over
+// the splits' slots in split order, then the epilogue (mode 1: + Y, 2:
+// + bias[n]).  Four consecutive outputs per thread (16-byte accesses when
+// M * N % 4 == 0 and Y is 16-byte aligned).
+__global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ slots,
+                                                   float *__restrict__ Y,
+                                                   const float *__restrict__ bias, int64_t mn,
+                                                   int N, int splits, int mode) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  if ((mn & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+    f32x4 t = *reinterpret_cast<const f32x4 *>(slots + i);
+    for (int sp = 1; sp < splits; ++sp) t += *reinterpret_cast<const f32x4 *>(slots + sp * mn + i);
+    if (mode == 1) t += *reinterpret_cast<const f32x4 *>(Y + i);
+    if (mode == 2) {
+      const int n = static_cast<int>(i % N);
+      t += f32x4{bias[n], bias[(n + 1) % N], bias[(n + 2) % N], bias[(n + 3) % N]};
+    }
+    *reinterpret_cast<f32x4 *>(Y + i) = t;
+    return;
+  }
+  for (int64_t k = i; k < mn && k < i + 4; ++k) {
+    float t = slots[k];
+    for (int sp = 1; sp < splits; ++sp) t += slots[sp * mn + k];
+    if (mode == 1) t += Y[k];
+    if (mode == 2) t += bias[k % N];
+    Y[k] = t;
+  }
+}
+
 namespace {
 
-template <int QT, bool F16OUT, bool ATOMIC, bool AH, int WV = IFX_F16_WAVES>
+template <int QT, bool F16OUT, int SPL, bool AH, int WV = IFX_F16_WAVES>
 hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bias, int M, int N,
                     int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
                     hipStream_t s) {
-  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, ATOMIC, AH>);
+  const void *fn = reinterpret_cast<const void *>(&k_gemm_f16<QT, WV, F16OUT, SPL, AH>);
   // set once per instantiation (a function-local static: thread-safe)
   if (!dry_run()) {
     static const hipError_t attr = hipFuncSetAttribute(
@@ -486,36 +521,35 @@ hipError_t launch_k(const uint8_t *W, const uint8_t *A, void *Y, const void *bia
     if (attr != hipSuccess) return attr;
   }
   const dim3 grid(static_cast<unsigned>(m_tiles * n_tiles * splits));
-  IFX_LAUNCH(k_gemm_f16, (QT, WV, F16OUT, ATOMIC, AH), grid, dim3(64 * WV), sizeof(Smem), s,
+  IFX_LAUNCH(k_gemm_f16, (QT, WV, F16OUT, SPL, AH), grid, dim3(64 * WV), sizeof(Smem), s,
                      W, A, Y, bias, M, N, K, mode, m_tiles, splits, cps);
   return last_error();
 }
 
-template <int QT, bool F16OUT, bool ATOMIC>
+template <int QT, bool F16OUT, int SPL>
 hipError_t launch_a(const uint8_t *W, const uint8_t *A, void *A16, void *Y, const void *bias,
                     int M, int N, int K, int mode, int m_tiles, int n_tiles, int splits, int cps,
                     hipStream_t s) {
   if (!A16)
-    return launch_k<QT, F16OUT, ATOMIC, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles,
-                                               splits, cps, s);
+    return launch_k<QT, F16OUT, SPL, false>(W, A, Y, bias, M, N, K, mode, m_tiles, n_tiles,
+                                            splits, cps, s);
   const int64_t nchunks = static_cast<int64_t>(M) * (K >> 5) * 4;
   IFX_LAUNCH0(k_q8_1_to_f16, dim3(static_cast<unsigned>((nchunks + 255) / 256)), dim3(256),
                      0, s, A, static_cast<u32x4 *>(A16), nchunks);
   const hipError_t e = last_error();
   if (e != hipSuccess) return e;
-  return launch_k<QT, F16OUT, ATOMIC, true>(W, static_cast<const uint8_t *>(A16), Y, bias, M, N,
-                                            K, mode, m_tiles, n_tiles, splits, cps, s);
+  return launch_k<QT, F16OUT, SPL, true>(W, static_cast<const uint8_t *>(A16), Y, bias, M, N, K,
+                                         mode, m_tiles, n_tiles, splits, cps, s);
 }
 
-template <int QT>
-hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, const void *bias,
-                     bool f16, int M, int N, int K, int mode, int splits_req, hipStream_t s) {
+// K splits of a launch: only for fp32 outputs, when the tile grid fills
+// less than 3/4 of the 256 CUs (one 512-thread workgroup per CU): as many
+// splits as fit in one pass over the CUs, keeping >= 8 stages per workgroup
+// (measured, N = 5120, K = 27648, M = 512: 5 splits 273 us, 6 splits 230
+// us).  Sets cps (stages per split).
+int f16_splits(bool f16, int M, int N, int K, int splits_req, int &cps) {
   const int m_tiles = (M + kBM - 1) / kBM, n_tiles = (N + kBN - 1) / kBN;
   const int nst = K / kBK;
-  // Split K only for fp32 outputs, when the tile grid fills less than 3/4
-  // of the 256 CUs (one 512-thread workgroup per CU): as many splits as fit
-  // in one pass over the CUs, keeping >= 8 stages per workgroup (measured,
-  // N = 5120, K = 27648, M = 512: 5 splits 273 us, 6 splits 230 us).
   int splits = 1;
   if (splits_req > 0) {
     splits = splits_req;
@@ -525,8 +559,29 @@ hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, con
   }
   if (f16) splits = 1;
   if (splits > nst) splits = nst;
-  const int cps = (nst + splits - 1) / splits;
-  splits = (nst + cps - 1) / cps;
+  cps = (nst + splits - 1) / splits;
+  return (nst + cps - 1) / cps;
+}
+
+// slots: NULL, or the ordered reduction's slots (splits x M x N fp32) for a
+// launch that splits K.
+template <int QT>
+hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, const void *bias,
+                     bool f16, int M, int N, int K, int mode, int splits_req, float *slots,
+                     hipStream_t s) {
+  const int m_tiles = (M + kBM - 1) / kBM, n_tiles = (N + kBN - 1) / kBN;
+  int cps = 0;
+  const int splits = f16_splits(f16, M, N, K, splits_req, cps);
+  if (splits > 1 && slots) {
+    const hipError_t e = launch_a<QT, false, 2>(W, A, A16, slots, nullptr, M, N, K, mode, m_tiles,
+                                                n_tiles, splits, cps, s);
+    if (e != hipSuccess) return e;
+    const int64_t mn = static_cast<int64_t>(M) * N;
+    IFX_LAUNCH0(k_split_sum, dim3(static_cast<unsigned>((mn + 1023) / 1024)), dim3(256), 0, s,
+                slots, static_cast<float *>(Y), static_cast<const float *>(bias), mn, N, splits,
+                mode);
+    return last_error();
+  }
   if (splits > 1) {
     if (mode != 1) {  // store / bias: the workgroups add into a zeroed Y
       FillArgs f{};
@@ -534,12 +589,12 @@ hipError_t launch_qt(const uint8_t *W, const uint8_t *A, void *A16, void *Y, con
       f.n[0] = static_cast<int64_t>(M) * N;
       if (launch_fill_zero(f, 1, s) != hipSuccess) return last_error();
     }
-    return launch_a<QT, false, true>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits,
-                                     cps, s);
+    return launch_a<QT, false, 1>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, splits,
+                                  cps, s);
   }
   if (f16)
-    return launch_a<QT, true, false>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
-  return launch_a<QT, false, false>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
+    return launch_a<QT, true, 0>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
+  return launch_a<QT, false, 0>(W, A, A16, Y, bias, M, N, K, mode, m_tiles, n_tiles, 1, cps, s);
 }
 
 }  // namespace
@@ -557,21 +612,31 @@ int64_t gemm_f16_workspace_bytes(int M, int K) {
   return b < (int64_t{1} << 32) ? b : 0;
 }
 
+// Bytes of the ordered reduction's slots (splits x M x N fp32), or 0 when
+// the launch does not split K.
+int64_t gemm_f16_slot_bytes(bool f16, int M, int N, int K) {
+  int cps = 0;
+  const int splits = f16_splits(f16, M, N, K, 0, cps);
+  return splits > 1 ? static_cast<int64_t>(splits) * M * N * 4 : 0;
+}
+
 // splits_req: 0 = chosen from the tile grid, else forced (tests).  A16:
 // caller-owned workspace of gemm_f16_workspace_bytes(M, K) bytes (16-byte
 // aligned) for the fp16 activations, converted once before the GEMM; NULL:
 // each workgroup converts its Q8_1 activation tiles itself.  Same results.
+// slots: NULL (K splits add with fp32 atomics into a zeroed Y), or
+// gemm_f16_slot_bytes of 16-byte aligned memory for the ordered reduction.
 hipError_t launch_gemm_f16(int qtype, const void *W, const void *A, void *A16, void *Y,
                            const void *bias, bool f16, int M, int N, int K, int mode,
-                           int splits_req, hipStream_t stream) {
+                           int splits_req, hipStream_t stream, float *slots) {
   const uint8_t *w = static_cast<const uint8_t *>(W);
   const uint8_t *a = static_cast<const uint8_t *>(A);
   if (!gemm_f16_fits(qtype, K)) return hipErrorInvalidValue;
   if (A16 && gemm_f16_workspace_bytes(M, K) == 0) A16 = nullptr;
   switch (qtype) {
-  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
-  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
-  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, stream);
+  case kTypeQ4_K: return launch_qt<kTypeQ4_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, slots, stream);
+  case kTypeQ6_K: return launch_qt<kTypeQ6_K>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, slots, stream);
+  case kTypeQ8_0: return launch_qt<kTypeQ8_0>(w, a, A16, Y, bias, f16, M, N, K, mode, splits_req, slots, stream);
   default: return hipErrorInvalidValue;
   }
 }

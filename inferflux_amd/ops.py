@@ -241,6 +241,32 @@ def qgemm_prefill_ws(qtype, W, A, M, N, K, workspace, out=None, out_dtype=torch.
     return out
 
 
+def prefill_ordered_workspace_bytes(qtype, M, N, K, out_dtype=torch.float32):
+    """Bytes of workspace qgemm_prefill_ordered needs at this shape."""
+    od = OUT_F16 if out_dtype == torch.float16 else OUT_F32
+    return int(_lib.load().ifx_qgemm_prefill_ordered_workspace_bytes(qtype, od, M, N, K))
+
+
+def qgemm_prefill_ordered(qtype, W, A, M, N, K, workspace, out=None, out_dtype=torch.float32,
+                          mode=STORE, bias=None, stream=None):
+    """The prefill GEMM with its K split reduced in split order through the
+    workspace (a device tensor of at least prefill_ordered_workspace_bytes
+    bytes, 256-byte aligned): the same bits on every call."""
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=W.device)
+    od = OUT_F16 if out.dtype == torch.float16 else OUT_F32
+    if W.numel() < weight_bytes(qtype, N, K) or A.numel() < M * (K // 32) * 36 or out.numel() < M * N:
+        raise ValueError("W, A or out is smaller than the shape")
+    nbytes = workspace.numel() * workspace.element_size()
+    bptr = _dev(bias, "bias") if bias is not None else None
+    rc = _lib.load().ifx_qgemm_prefill_ordered(qtype, _dev(W, "W"), _dev(A, "A"), _dev(out, "out"),
+                                               od, mode, bptr, M, N, K,
+                                               _dev(workspace, "workspace"), nbytes,
+                                               _stream(stream))
+    _check(rc, "ifx_qgemm_prefill_ordered")
+    return out
+
+
 def qgemm_prefill_noalloc(qtype, W, A, M, N, K, out=None, out_dtype=torch.float32, mode=STORE,
                           bias=None, stream=None):
     """qgemm_prefill_ws with the library's static device scratch as the
