@@ -755,15 +755,19 @@ namespace {
 // Largest K range (super-blocks) whose fp16 activation stage fits kLdsBytes.
 int dq_sb_max(int M) { return max(1, (kLdsBytes / 2 / (M + 1) - 8) / 256); }
 
-// Super-block splits: at least what the activation stage needs, and enough
-// workgroups for two per CU on 256 CUs; fp16 outputs without the ordered-
-// split workspace (no_split) take the fewest the stage allows.  IFX_DQ_WGS
-// sets the workgroup target (tuning; read once).
+// Super-block splits: at least what the activation stage needs, and about
+// 512 workgroups (two per CU on 256 CUs) up to M = 16, 320 above (fewer
+// partial sums: 14B Q/K/V at M = 32 13.8 -> 13.05 us, ordered 15.6 -> 13.9,
+// O 9.55 -> 9.05, ordered 13.1 -> 13.85; at M = 16 the 14B O / down lose
+// 0.9 / 2.8 us with it); fp16 outputs without the ordered-split workspace
+// (no_split) take the fewest the stage allows.  IFX_DQ_WGS sets the
+// workgroup target (tuning; read once).
 int dq_splits(int groups, int nsb, int M, bool no_split) {
-  static const int target = [] {
+  static const int env = [] {
     const char *e = ifx::tuning_env("IFX_DQ_WGS");
-    return e && atoi(e) > 0 ? atoi(e) : 512;
+    return e && atoi(e) > 0 ? atoi(e) : 0;
   }();
+  const int target = env ? env : M > 16 ? 320 : 512;
   const int need = (nsb + dq_sb_max(M) - 1) / dq_sb_max(M);
   if (no_split) return need;
   return max(need, min(nsb, (target + groups - 1) / groups));
