@@ -58,22 +58,22 @@ hipError_t launch_gemv_rmsnorm(int count, const void *const *W, void *const *Y, 
                                bool f16, int M, int K, int mode, hipStream_t stream);
 bool gemv_dq_fits(int qtype, int M, int K);
 bool gemv_dq_fits_f16(int M, int K);
-bool gemv_dq_f16_unsplit(int qtype, int count, const int *N, int M, int K);
+bool gemv_dq_f16_unsplit(int count, const int *N, int M, int K);
 hipError_t launch_gemv_dq(int qtype, int count, const void *const *W, void *const *Y,
                           const int *N, const void *bias, const void *A, bool f16, int M, int K,
                           int mode, int splits_req, hipStream_t stream, void *ws = nullptr);
-int64_t gemv_dq_workspace_bytes(int qtype, int count, const int *N, bool f16, int M, int K);
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K);
 hipError_t scratch_address(void **out);
 hipError_t launch_repack(int qtype, const void *W, void *out, int64_t n_rows, int K,
                          hipStream_t stream);
 hipError_t launch_repack_tiled(int qtype, const void *W, void *out, int64_t n_rows, int K,
                                hipStream_t stream);
 bool gemv_slot_fits(int qtype, int M, int K);
-int gemv_dq_swiglu_splits(int qtype, int M, int N, int K);
+int gemv_dq_swiglu_splits(int M, int N, int K);
 hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
                                  void *H, bool h_f16, void *Q, int M, int N, int K, void *ws,
                                  hipStream_t stream);
-int64_t gemv_dq_workspace_bytes(int qtype, int count, const int *N, bool f16, int M, int K);
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K);
 hipError_t launch_gemv_slot_swiglu(int qtype, const void *Wg, const void *Wu, const void *A,
                                    void *H, bool f16h, void *Q, int M, int N, int K,
                                    hipStream_t stream);
@@ -333,12 +333,12 @@ Route route(int qt, int M, int K, int n_total, bool f16, bool grouped, bool atom
 // the caller's workspace is too small or not 256-byte aligned.
 // ordered: an ordered entry (ifx_qgemv_ws / _grouped_ws), whose launches
 // that split need the workspace (none given: IFX_BAD_GEOMETRY).
-void *split_ws(Route r, int qtype, void *ws, int64_t ws_bytes, int count, const int *N, bool f16,
+void *split_ws(Route r, void *ws, int64_t ws_bytes, int count, const int *N, bool f16,
                int M, int K, bool ordered, int &rc) {
   rc = IFX_OK;
   if (!ws && !ordered) return nullptr;
   const int64_t need = r == Route::Slot ? ifx::gemv_slot_workspace_bytes(count, N, f16, M, K)
-                                        : ifx::gemv_dq_workspace_bytes(qtype, count, N, f16, M, K);
+                                        : ifx::gemv_dq_workspace_bytes(count, N, f16, M, K);
   if (need == 0) return nullptr;
   if (!ws || ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) rc = IFX_BAD_GEOMETRY;
   return ws;
@@ -361,15 +361,15 @@ int qgemv_impl(int quant_type, const void *W, const void *A_q8_1, void *Y, int o
   case Route::Lds:
     return status_of(ifx::launch_gemv_lds(1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s));
   case Route::Slot: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
+    void *w = split_ws(r, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     return status_of(ifx::launch_gemv_slot(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, s, w));
   }
   case Route::Dq: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
+    void *w = split_ws(r, ws, ws_bytes, 1, &N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     // tiled weights: fp16 outputs split only through the workspace
-    if (f16 && !w && !ifx::gemv_dq_f16_unsplit(quant_type, 1, &N, M, K)) return IFX_BAD_GEOMETRY;
+    if (f16 && !w && !ifx::gemv_dq_f16_unsplit(1, &N, M, K)) return IFX_BAD_GEOMETRY;
     return status_of(ifx::launch_gemv_dq(quant_type, 1, &W, &Y, &N, bias, A_q8_1, f16, M, K, mode, 0, s, w));
   }
   case Route::Skinny:
@@ -405,15 +405,15 @@ int grouped_impl(int quant_type, int count, const void *const *W, void *const *Y
   case Route::Lds:
     return status_of(ifx::launch_gemv_lds(count, W, Y, N, nullptr, A_q8_1, f16, M, K, mode, s));
   case Route::Slot: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
+    void *w = split_ws(r, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
     return status_of(ifx::launch_gemv_slot(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                            mode, s, w));
   }
   case Route::Dq: {
-    void *w = split_ws(r, quant_type, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
+    void *w = split_ws(r, ws, ws_bytes, count, N, f16, M, K, ordered, wrc);
     if (wrc != IFX_OK) return wrc;
-    if (f16 && !w && !ifx::gemv_dq_f16_unsplit(quant_type, count, N, M, K))  // tiled weights
+    if (f16 && !w && !ifx::gemv_dq_f16_unsplit(count, N, M, K))  // tiled weights
       return IFX_BAD_GEOMETRY;
     return status_of(ifx::launch_gemv_dq(quant_type, count, W, Y, N, nullptr, A_q8_1, f16, M, K,
                                          mode, 0, s, w));
@@ -630,7 +630,7 @@ int64_t ifx_qgemv_workspace_bytes(int quant_type, int count, const int *N, int o
   const bool f16 = out_dtype == IFX_OUT_F16;
   switch (route(quant_type, M, K, n_total, f16, count > 1)) {
   case Route::Slot: return ifx::gemv_slot_workspace_bytes(count, N, f16, M, K);
-  case Route::Dq: return ifx::gemv_dq_workspace_bytes(quant_type, count, N, f16, M, K);
+  case Route::Dq: return ifx::gemv_dq_workspace_bytes(count, N, f16, M, K);
   default: return 0;
   }
 }
@@ -702,10 +702,10 @@ int gate_up_silu_impl(int quant_type, const void *W_gate, const void *W_up, cons
     return status_of(ifx::launch_gemv_slot_swiglu(quant_type, W_gate, W_up, A_q8_1, H,
                                                   h_dtype == IFX_OUT_F16, q8_1_out, M, N, K, s));
   if (dq) {
-    if (ifx::gemv_dq_swiglu_splits(quant_type, M, N, K) > 1) {
+    if (ifx::gemv_dq_swiglu_splits(M, N, K) > 1) {
       const int NN[2] = {N, N};
       if (!ws) return IFX_BAD_GEOMETRY;  // not handled without the workspace
-      if (ws_bytes < ifx::gemv_dq_workspace_bytes(quant_type, 2, NN, false, M, K)) return IFX_BAD_GEOMETRY;
+      if (ws_bytes < ifx::gemv_dq_workspace_bytes(2, NN, false, M, K)) return IFX_BAD_GEOMETRY;
     } else {
       ws = nullptr;
     }
@@ -729,9 +729,9 @@ int ifx_qgemv_gate_up_silu(int quant_type, const void *W_gate, const void *W_up,
 int64_t ifx_qgemv_gate_up_silu_workspace_bytes(int quant_type, int M, int N, int K) {
   if (!is_weight_type(quant_type) || row_split(quant_type) || M < 1 || N < 1 || K < 1) return 0;
   if (swiglu_kernel(quant_type, M, N, K) != SwKernel::Dq) return 0;
-  if (ifx::gemv_dq_swiglu_splits(quant_type, M, N, K) <= 1) return 0;
+  if (ifx::gemv_dq_swiglu_splits(M, N, K) <= 1) return 0;
   const int NN[2] = {N, N};
-  return ifx::gemv_dq_workspace_bytes(quant_type, 2, NN, false, M, K);
+  return ifx::gemv_dq_workspace_bytes(2, NN, false, M, K);
 }
 
 int ifx_qgemv_gate_up_silu_ws(int quant_type, const void *W_gate, const void *W_up,

@@ -786,22 +786,20 @@ int dqr_min_groups() {
 }
 
 // Whether a launch of `groups` row groups takes k_gemv_dqr.
-bool dq_rolling(int qtype, int groups, int M, int splits_req) {
-  (void)qtype;
-  (void)M;
+bool dq_rolling(int groups, int splits_req) {
   return dqr_min_groups() > 0 && groups >= dqr_min_groups() && splits_req == 0;
 }
 
 // Row groups and K splits of a launch (sets blk_begin and sb_per);
 // rolling: the launch takes k_gemv_dqr (ks = 1, sb_per unused).
-void dq_plan(DqArgs &args, int qtype, bool no_split, int splits_req, int &groups, int &ks,
+void dq_plan(DqArgs &args, bool no_split, int splits_req, int &groups, int &ks,
              bool *rolling = nullptr) {
   groups = 0;
   for (int i = 0; i < args.nseg; ++i) {
     args.seg[i].blk_begin = groups;
     groups += (args.seg[i].N + kRowsPerWg - 1) / kRowsPerWg;
   }
-  const bool roll = dq_rolling(qtype, groups, args.M, splits_req);
+  const bool roll = dq_rolling(groups, splits_req);
   if (rolling) *rolling = roll;
   if (roll) {
     ks = 1;
@@ -857,7 +855,7 @@ hipError_t launch_qt(DqArgs args, bool f16, int splits_req, hipStream_t s) {
   const bool ordered = args.ws.cnt != nullptr;
   int groups = 0, ks = 1;
   bool rolling = false;
-  dq_plan(args, QT, f16 && !ordered, splits_req, groups, ks, &rolling);
+  dq_plan(args, f16 && !ordered, splits_req, groups, ks, &rolling);
   if (rolling) {
     if (f16) return launch_dqr<QT, true, TL, false>(args, groups, s);
     return launch_dqr<QT, false, TL, false>(args, groups, s);
@@ -909,10 +907,10 @@ hipError_t launch_sw(const DqArgs &args, int groups, int ks, hipStream_t s) {
 
 // The pair plan (gate and up as one grouped launch of two projections):
 // row groups, K splits and sb_per as the grouped launch chooses them.
-void sw_plan(DqArgs &args, int qtype, int N, int &pair_groups, int &ks, bool *rolling = nullptr) {
+void sw_plan(DqArgs &args, int N, int &pair_groups, int &ks, bool *rolling = nullptr) {
   args.seg[0].N = args.seg[1].N = N;
   args.nseg = 2;
-  dq_plan(args, qtype, false, 0, pair_groups, ks, rolling);
+  dq_plan(args, false, 0, pair_groups, ks, rolling);
 }
 
 }  // namespace
@@ -920,12 +918,12 @@ void sw_plan(DqArgs &args, int qtype, int N, int &pair_groups, int &ks, bool *ro
 bool gemv_dq_fits(int qtype, int M, int K);
 
 // K splits of the fused gate/up/SiLU launch (1: no workspace needed).
-int gemv_dq_swiglu_splits(int qtype, int M, int N, int K) {
+int gemv_dq_swiglu_splits(int M, int N, int K) {
   DqArgs args{};
   args.M = M;
   args.K = K;
   int pg = 0, ks = 1;
-  sw_plan(args, qtype, N, pg, ks);
+  sw_plan(args, N, pg, ks);
   return ks;
 }
 
@@ -948,7 +946,7 @@ hipError_t launch_gemv_dq_swiglu(int qtype, const void *Wg, const void *Wu, cons
   args.h_f16 = h_f16 ? 1 : 0;
   int pair_groups = 0, ks = 1;
   bool rolling = false;
-  sw_plan(args, qtype, N, pair_groups, ks, &rolling);
+  sw_plan(args, N, pair_groups, ks, &rolling);
   const int groups = (N + 63) / 64;
   if (rolling) {
     switch (qtype) {
@@ -990,17 +988,17 @@ bool gemv_dq_fits(int qtype, int M, int K) {
 // holds K.
 bool gemv_dq_fits_f16(int M, int K) { return M <= kMaxM && K / 256 <= dq_sb_max(M); }
 // ... or the launch (count projections of N rows) takes the no-split form.
-bool gemv_dq_f16_unsplit(int qtype, int count, const int *N, int M, int K) {
+bool gemv_dq_f16_unsplit(int count, const int *N, int M, int K) {
   int groups = 0;
   for (int i = 0; i < count; ++i) groups += (N[i] + kRowsPerWg - 1) / kRowsPerWg;
-  return M <= kMaxM && (K / 256 <= dq_sb_max(M) || dq_rolling(qtype, groups, M, 0));
+  return M <= kMaxM && (K / 256 <= dq_sb_max(M) || dq_rolling(groups, 0));
 }
 
 // count projections (1..3) of one quant type share A; bias only with
 // count == 1.  splits_req: 0 = chosen from the shape.
 // Workspace bytes of the ordered split (0: the launch does not split):
 // counters (256-byte aligned) then one 16 KB slot per (row group, split).
-int64_t gemv_dq_workspace_bytes(int qtype, int count, const int *N, bool f16, int M, int K) {
+int64_t gemv_dq_workspace_bytes(int count, const int *N, bool f16, int M, int K) {
   DqArgs args{};
   for (int i = 0; i < count; ++i) args.seg[i].N = N[i];
   args.nseg = count;
@@ -1008,7 +1006,7 @@ int64_t gemv_dq_workspace_bytes(int qtype, int count, const int *N, bool f16, in
   args.K = K;
   int groups = 0, ks = 1;
   (void)f16;  // fp16 outputs split as fp32 ones when the workspace is given
-  dq_plan(args, qtype, false, 0, groups, ks);
+  dq_plan(args, false, 0, groups, ks);
   if (ks <= 1) return 0;
   return (static_cast<int64_t>(groups) * 4 + 255) / 256 * 256 +
          static_cast<int64_t>(groups) * ks * kWaves * 64 * 16 * 4;
