@@ -262,6 +262,15 @@ uint64_t weight_bytes(int t, int N, int K) {
   return rows * ifx::row_bytes(t, K);
 }
 
+// Kernels address W and A with 32-bit byte offsets (buffer loads) and read
+// zeros at ifx::kOobOffset, past every accepted tensor.
+bool buffers_fit(int quant_type, int M, int N, int K) {
+  if (N > (1 << 30) || M > (1 << 24) || K > (1 << 24)) return false;
+  const uint64_t w_bytes = weight_bytes(quant_type, N, K);
+  const uint64_t a_bytes = static_cast<uint64_t>(M) * (K / 32) * 36;
+  return w_bytes < ifx::kMaxBufferBytes && a_bytes < ifx::kMaxBufferBytes;
+}
+
 int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int out_dtype,
                     int mode, const void *bias, int M, int N, int K) {
   if (!W || !A || !Y) return IFX_NULL_POINTER;
@@ -274,11 +283,7 @@ int check_gemm_args(int quant_type, const void *W, const void *A, void *Y, int o
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return IFX_BAD_GEOMETRY;
   if (row_split(quant_type) && M > kMaxRowSplitM) return IFX_BAD_GEOMETRY;
   if (tiled(quant_type) && M > kMaxTiledM) return IFX_BAD_GEOMETRY;
-  // Kernels address W and A with 32-bit byte offsets (buffer loads).
-  if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return IFX_BAD_GEOMETRY;
-  const uint64_t w_bytes = weight_bytes(quant_type, N, K);
-  const uint64_t a_bytes = static_cast<uint64_t>(M) * (K / 32) * 36;
-  if (w_bytes >= (1ull << 32) || a_bytes >= (1ull << 32)) return IFX_BAD_GEOMETRY;
+  if (!buffers_fit(quant_type, M, N, K)) return IFX_BAD_GEOMETRY;
   return IFX_OK;
 }
 
@@ -485,10 +490,7 @@ int ifx_supports(int quant_type, int M, int N, int K) {
   if (gemv_only(quant_type) && M > kMaxGemvOnlyM) return 0;
   if (row_split(quant_type) && M > kMaxRowSplitM) return 0;
   if (tiled(quant_type) && M > kMaxTiledM) return 0;
-  if (N > (1 << 30) || M > (1 << 24) || K > (1 << 28)) return 0;
-  const uint64_t w_bytes = weight_bytes(quant_type, N, K);
-  if (w_bytes >= (1ull << 32) || static_cast<uint64_t>(M) * (K / 32) * 36 >= (1ull << 32)) return 0;
-  return 1;
+  return buffers_fit(quant_type, M, N, K) ? 1 : 0;
 }
 
 int ifx_kernel_family(int quant_type, int M, int N, int K) {

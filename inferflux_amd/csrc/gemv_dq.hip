@@ -626,7 +626,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_gemv_dqr(const DqArgs args) {
   // out of range, zeros, no reads
   auto fetch = [&](RawW<QT> &r, int i) {
     const int t = i * kHalves + half;
-    fetch_w<QT, TL>(r, Wr, t < nsb ? row_off : 0xF0000000u, min(t, nsb - 1), h, l32);
+    fetch_w<QT, TL>(r, Wr, t < nsb ? row_off : kOobOffset, t < nsb ? t : 0, h, l32);
   };
 
   f32x16 acc0, acc1;

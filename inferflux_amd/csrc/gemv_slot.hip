@@ -252,7 +252,6 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
   constexpr int kSbStep = TL ? kTile : kSbBytes;  // bytes between a row's super-blocks
   // activation operand: MFMA row r = c32 = batch row (r % MP) of slot r / MP
   const int am = c32 % MP, aslot = c32 / MP;
-  constexpr uint32_t kOob = 0x80000000u;  // past any A range: loads zeros
   bool a_valid = true;
   int tsel = aslot;  // MFMA within a chain that this lane feeds
   if constexpr (QT == kTypeQ6_K) {
@@ -263,7 +262,7 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
 #pragma unroll
   for (int c = 0; c < G::kCh; ++c) {
     const int j = c * G::kTpc + tsel;
-    a_off[c] = a_valid ? static_cast<uint32_t>(am) * a_row + j * kQ8_1Bytes + 4 + 16 * h : kOob;
+    a_off[c] = a_valid ? static_cast<uint32_t>(am) * a_row + j * kQ8_1Bytes + 4 + 16 * h : kOobOffset;
   }
   uint32_t ds_off[MP / 8];
 #pragma unroll

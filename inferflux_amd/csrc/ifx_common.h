@@ -201,6 +201,14 @@ __device__ __forceinline__ T ldg(const void *p) {
 // the gfx9-family default (raw buffer, 32-bit dword format).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
+// An offset past every W and A range the entry points accept (they refuse
+// tensors of kMaxBufferBytes or more): a load there reads zeros and touches
+// no memory.  Kernels add at most one weight tile or one Q8_1 row (K <=
+// 2^24: 18.9 MB) to it, which stays below 2^32 whether or not the range
+// check counts the scalar offset.
+constexpr uint32_t kOobOffset = 0xF0000000u;
+constexpr uint64_t kMaxBufferBytes = kOobOffset;
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes),
                                            0x00020000);

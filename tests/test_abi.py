@@ -73,6 +73,14 @@ def test_supports(lib):
     assert lib.ifx_supports(13, 1, 16, 128) == 0
     assert lib.ifx_supports(11, 1, 16, 256) == 0      # Q3_K: no kernel
     assert lib.ifx_supports(12, 0, 16, 256) == 0
+    # W and A stay below 0xF0000000 bytes, the offset at which the kernels'
+    # loads that must read zeros are placed; K up to 2^24
+    assert lib.ifx_supports(8, 16, 151936, 24832) == 1  # Q8_0 W 4.009e9 B
+    assert lib.ifx_supports(8, 16, 151936, 24960) == 0  # 4.029e9 B >= 0xF0000000
+    assert lib.ifx_supports(12, 1, 1, 1 << 24) == 1
+    assert lib.ifx_supports(12, 1, 1, (1 << 24) + 256) == 0
+    assert lib.ifx_supports(12, 213, 1, 1 << 24) == 1    # A 4.020e9 B
+    assert lib.ifx_supports(12, 214, 1, 1 << 24) == 0    # A 4.039e9 B
 
 
 def test_validation_without_launch(lib):
