@@ -39,10 +39,10 @@ LAUNCHES = [
     ("c1_m8", "gemv", Q4_K, 8, (11008,), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
     # config 2: the 3B decode layer as the reference launches it
     ("c2_qkv_m1", "grouped", Q4_K, 1, QKV3, 2048, ["k_gemv<12,1,1,1,4,0,2>"]),
-    ("c2_o_m1", "gemv_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2>"]),
+    ("c2_o_m1", "gemv_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2,0,1>"]),
     ("c2_gate_up_m1", "grouped", Q4_K, 1, (11008, 11008), 2048, ["k_gemv<12,1,2,1,4,0,2>"]),
-    ("c2_down_m1", "gemv_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<14,1,2,3,1,0,1>"]),
-    ("c2_down_r_m1", "gemv_accum", Q6_K_R, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1>"]),
+    ("c2_down_m1", "gemv_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<14,1,2,3,1,0,1,0,1>"]),
+    ("c2_down_r_m1", "gemv_accum", Q6_K_R, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1,0,1>"]),
     ("c2_qkv_m4", "grouped", Q4_K, 4, QKV3, 2048, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c2_o_m4", "gemv_accum", Q4_K, 4, (2048,), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c2_gate_up_m4", "grouped", Q4_K, 4, (11008, 11008), 2048, ["k_gemv_lds<4,2,2,8,0>"]),
@@ -56,7 +56,7 @@ LAUNCHES = [
     ("c2s_gate_up_m8", "gate_up_silu", Q4_K, 8, (11008,), 2048, ["k_gemv_slot<12,8,4,0,0,1>"]),
     # config 2, the fused layer form the benchmark's step uses at M = 1
     ("c2f_qkv_m1", "grouped_rmsnorm", Q4_K, 1, QKV3, 2048, ["k_gemv<12,1,2,1,4,0,2,1>"]),
-    ("c2f_o_m1", "quantize_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2,3>"]),
+    ("c2f_o_m1", "quantize_accum", Q4_K, 1, (2048,), 2048, ["k_gemv<12,1,1,1,4,0,2,3,1>"]),
     ("c2f_gate_up_m1", "gate_up_silu_rmsnorm", Q4_K, 1, (11008,), 2048,
      ["k_gemv_swiglu_wide<1,0,1,8>"]),
     # config 3: LM head 151936 x 2048
@@ -76,7 +76,7 @@ LAUNCHES = [
     ("c4_gate_up_m32", "grouped", Q4_K, 32, (13824, 13824), 5120, ["k_gemv_dqr<12,0,0,0,4,2,8>"]),
     ("c4_down_m32", "gemv_accum", Q6_K, 32, (5120,), 13824, ["k_gemv_dq<14,0,1>"]),
     ("c4_qkv_m1", "grouped", Q4_K, 1, QKV14, 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
-    ("c4_o_m1", "gemv_accum", Q4_K, 1, (5120,), 5120, ["k_gemv<12,1,1,1,4,0,4>"]),
+    ("c4_o_m1", "gemv_accum", Q4_K, 1, (5120,), 5120, ["k_gemv<12,1,1,1,4,0,4,0,1>"]),
     ("c4_gate_up_m1", "grouped", Q4_K, 1, (13824, 13824), 5120, ["k_gemv<12,1,2,1,4,0,4>"]),
     ("c4_qkv_m8", "grouped", Q4_K, 8, QKV14, 5120, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c4_o_m8", "gemv_accum", Q4_K, 8, (5120,), 5120, ["k_gemv_slot<12,8,8,0,0>"]),
@@ -117,7 +117,7 @@ LAUNCHES = [
     ("c4t_down_m32", "gemv_accum_ws", Q6_K_T, 32, (5120,), 13824, ["k_gemv_dq<14,0,2,1>"]),
     # the down projections on the MMQ layout (FusedQuantGemm::DownProjMmq):
     # row-split rows at M <= 2, tiles above, ordered K splits
-    ("c2m_down_m1", "mmq_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1>"]),
+    ("c2m_down_m1", "mmq_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1,0,1>"]),
     ("c2m_down_m4", "mmq_accum_ws", Q6_K, 4, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
     ("c2m_down_m8", "mmq_accum_ws", Q6_K, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
     ("c4m_down_m16", "mmq_accum_ws", Q6_K, 16, (5120,), 13824,
