@@ -217,7 +217,11 @@ constexpr int slot_lds_bytes() {
 // sums in another order).
 // SPLIT: 0 one workgroup per row group; 1 K split over gridDim.y with fp32
 // atomics into Y (zeroed first in store / bias mode); 2 K split with the
-// ordered reduction through args.ws (split_arrive_last, ifx_common.h).
+// ordered reduction through args.ws (split_arrive_last, ifx_common.h);
+// 3 as 0, for accumulate and bias launches: the term each output adds (Y
+// before the launch, or the bias) is loaded ahead of the weights, so the
+// epilogue waits on no dependent load (nothing else writes those outputs
+// during the launch: the same bits as 0).
 template <int QT, int MP, int KW, bool F16OUT, int SPLIT, bool SW = false, bool TL = false>
 __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const SlotArgs args) {
   using G = SlotGeo<QT, MP>;
@@ -279,9 +283,30 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
 #pragma unroll
   for (int i = 0; i < NM; ++i) acc[i] = 0.0f;
 
+  float early[SPLIT == 3 ? NM : 1];  // SPLIT == 3: the added term, branch-free
+  if constexpr (SPLIT == 3) {
+    const int nc = min(n0 + c32, N - 1);
+    const bool bias_mode = args.mode == 2;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int m = min(2 * (mi & ~3) + 4 * h + (mi & 3), M - 1);
+      const int64_t o = static_cast<int64_t>(m) * N + nc;
+      if constexpr (F16OUT) {
+        const uint16_t *p = bias_mode ? static_cast<const uint16_t *>(sg.bias) + nc
+                                      : static_cast<const uint16_t *>(sg.Y) + o;
+        early[mi] = h2f(*p);
+      } else {
+        const float *p = bias_mode ? static_cast<const float *>(sg.bias) + nc
+                                   : static_cast<const float *>(sg.Y) + o;
+        early[mi] = *p;
+      }
+    }
+  }
+
   // this wave's super-blocks: wave index over the split, stride KS * KW
-  const int step = SPLIT ? KW * static_cast<int>(gridDim.y) : KW;
-  int sb = (SPLIT ? static_cast<int>(blockIdx.y) * KW : 0) + wave;
+  constexpr bool kSplitK = SPLIT == 1 || SPLIT == 2;
+  const int step = kSplitK ? KW * static_cast<int>(gridDim.y) : KW;
+  int sb = (kSplitK ? static_cast<int>(blockIdx.y) * KW : 0) + wave;
   WSb<QT> wc;
   ASb<QT, MP> ac;
   if (sb < nsb) {
@@ -520,6 +545,10 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
       // Y was zeroed (store/bias) or holds the accumulate base
       if (mode == 2 && blockIdx.y == 0) y += static_cast<const float *>(sg.bias)[n];
       atomicAdd(static_cast<float *>(sg.Y) + o, y);
+    } else if constexpr (SPLIT == 3) {
+      if (mode == 1 || mode == 2) y += early[mi];
+      if constexpr (F16OUT) static_cast<uint16_t *>(sg.Y)[o] = static_cast<uint16_t>(f2h_bits(y));
+      else static_cast<float *>(sg.Y)[o] = y;
     } else if constexpr (F16OUT) {
       uint16_t *Yh = static_cast<uint16_t *>(sg.Y);
       if (mode == 1) y += h2f(Yh[o]);
@@ -584,11 +613,14 @@ void slot_launch(const SlotArgs &args, int blocks, int ks, hipStream_t s) {
 
 template <int QT, int MP, int KW, bool TL>
 void slot_split(const SlotArgs &args, int blocks, int ks, bool f16, hipStream_t s) {
+  const bool adds = args.mode != 0;  // accumulate / bias: the term loaded early
   if (f16) {  // a split fp16 launch is ordered (choose_slot_work)
     if (ks > 1) slot_launch<QT, MP, KW, true, 2, TL>(args, blocks, ks, s);
+    else if (adds) slot_launch<QT, MP, KW, true, 3, TL>(args, blocks, 1, s);
     else slot_launch<QT, MP, KW, true, 0, TL>(args, blocks, 1, s);
   } else if (ks == 1) {
-    slot_launch<QT, MP, KW, false, 0, TL>(args, blocks, 1, s);
+    if (adds) slot_launch<QT, MP, KW, false, 3, TL>(args, blocks, 1, s);
+    else slot_launch<QT, MP, KW, false, 0, TL>(args, blocks, 1, s);
   } else if (args.ws.cnt) {
     slot_launch<QT, MP, KW, false, 2, TL>(args, blocks, ks, s);
   } else {

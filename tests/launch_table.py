@@ -44,11 +44,11 @@ LAUNCHES = [
     ("c2_down_m1", "gemv_accum", Q6_K, 1, (2048,), 11008, ["k_gemv<14,1,2,3,1,0,1,0,1>"]),
     ("c2_down_r_m1", "gemv_accum", Q6_K_R, 1, (2048,), 11008, ["k_gemv<114,1,2,3,1,0,1,0,1>"]),
     ("c2_qkv_m4", "grouped", Q4_K, 4, QKV3, 2048, ["k_gemv_slot<12,8,8,0,0>"]),
-    ("c2_o_m4", "gemv_accum", Q4_K, 4, (2048,), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
+    ("c2_o_m4", "gemv_accum", Q4_K, 4, (2048,), 2048, ["k_gemv_slot<12,8,8,0,3>"]),
     ("c2_gate_up_m4", "grouped", Q4_K, 4, (11008, 11008), 2048, ["k_gemv_lds<4,2,2,8,0>"]),
     ("c2_down_m4", "gemv_accum", Q6_K, 4, (2048,), 11008, ["k_gemv_slot<14,8,4,0,1>"]),
     ("c2_qkv_m8", "grouped", Q4_K, 8, QKV3, 2048, ["k_gemv_slot<12,8,8,0,0>"]),
-    ("c2_o_m8", "gemv_accum", Q4_K, 8, (2048,), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
+    ("c2_o_m8", "gemv_accum", Q4_K, 8, (2048,), 2048, ["k_gemv_slot<12,8,8,0,3>"]),
     ("c2_gate_up_m8", "grouped", Q4_K, 8, (11008, 11008), 2048, ["k_gemv_slot<12,8,8,0,0>"]),
     ("c2_down_m8", "gemv_accum", Q6_K, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,1>"]),
     # config 2 at M = 4 / 8 with SiLU * up + Q8_1 in the gate/up epilogue
@@ -79,25 +79,25 @@ LAUNCHES = [
     ("c4_o_m1", "gemv_accum", Q4_K, 1, (5120,), 5120, ["k_gemv<12,1,1,1,4,0,4,0,1>"]),
     ("c4_gate_up_m1", "grouped", Q4_K, 1, (13824, 13824), 5120, ["k_gemv<12,1,2,1,4,0,4>"]),
     ("c4_qkv_m8", "grouped", Q4_K, 8, QKV14, 5120, ["k_gemv_slot<12,8,8,0,0>"]),
-    ("c4_o_m8", "gemv_accum", Q4_K, 8, (5120,), 5120, ["k_gemv_slot<12,8,8,0,0>"]),
+    ("c4_o_m8", "gemv_accum", Q4_K, 8, (5120,), 5120, ["k_gemv_slot<12,8,8,0,3>"]),
     ("c4_gate_up_m8", "grouped", Q4_K, 8, (13824, 13824), 5120, ["k_gemv_slot<12,8,8,0,0>"]),
     # the benchmark's tiled forms: config 1 at M = 8, the 3B layer at M = 4 / 8
     # and the 14B layer at M = 16 / 32 with ordered K splits, the LM head at M = 8
     ("c1_m8_tiled", "gemv", Q4_K_T, 8, (11008,), 2048, ["k_gemv_slot<12,8,8,0,0,0,1>"]),
     ("c2t_qkv_m4", "grouped_ws", Q4_K_T, 4, QKV3, 2048, ["k_gemv_slot<12,8,8,0,0,0,1>"]),
-    ("c2t_o_m4", "gemv_accum_ws", Q4_K_T, 4, (2048,), 2048, ["k_gemv_slot<12,8,8,0,0,0,1>"]),
+    ("c2t_o_m4", "gemv_accum_ws", Q4_K_T, 4, (2048,), 2048, ["k_gemv_slot<12,8,8,0,3,0,1>"]),
     ("c2t_gate_up_m4", "gate_up_silu", Q4_K_T, 4, (11008,), 2048,
      ["k_gemv_slot<12,8,4,0,0,1,1>"]),
     ("c2t_down_m4", "gemv_accum_ws", Q6_K_T, 4, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
     ("c2t_qkv_m8", "grouped_ws", Q4_K_T, 8, QKV3, 2048, ["k_gemv_slot<12,8,8,0,0,0,1>"]),
-    ("c2t_o_m8", "gemv_accum_ws", Q4_K_T, 8, (2048,), 2048, ["k_gemv_slot<12,8,8,0,0,0,1>"]),
+    ("c2t_o_m8", "gemv_accum_ws", Q4_K_T, 8, (2048,), 2048, ["k_gemv_slot<12,8,8,0,3,0,1>"]),
     ("c2t_gate_up_m8", "gate_up_silu", Q4_K_T, 8, (11008,), 2048,
      ["k_gemv_slot<12,8,4,0,0,1,1>"]),
     ("c2t_down_m8", "gemv_accum_ws", Q6_K_T, 8, (2048,), 11008, ["k_gemv_slot<14,8,4,0,2,0,1>"]),
     ("c3_q8_0_t_m8", "gemv", Q8_0_T, 8, (151936,), 2048, ["k_gemv_slot<8,8,1,0,0,0,1>"]),
     ("c3_q6_k_t_m8", "gemv", Q6_K_T, 8, (151936,), 2048, ["k_gemv_slot<14,8,1,0,0,0,1>"]),
     ("c4t_qkv_m16", "grouped_ws", Q4_K_T, 16, QKV14, 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
-    ("c4t_o_m16", "gemv_accum_ws", Q4_K_T, 16, (5120,), 5120, ["k_gemv_slot<12,16,8,0,0,0,1>"]),
+    ("c4t_o_m16", "gemv_accum_ws", Q4_K_T, 16, (5120,), 5120, ["k_gemv_slot<12,16,8,0,3,0,1>"]),
     ("c4t_gate_up_m16", "grouped_ws", Q4_K_T, 16, (13824, 13824), 5120,
      ["k_gemv_dqr<12,0,1,0,8,4,8>"]),
     ("c4t_down_m16", "gemv_accum_ws", Q6_K_T, 16, (5120,), 13824,
