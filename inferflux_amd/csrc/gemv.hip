@@ -459,7 +459,8 @@ static void launch_g(const GemvArgs &args, bool f16, hipStream_t s) {
 //    -> 2, N = 151936 -> 4;
 //  * wide Q4_K slices: half-wave R = 1 for N < 8192, else 2 (4 rows a
 //    wave); full-wave R = M for N < 8192, else 2M;
-//  * wide Q6_K slices: R = 2; row-split Q8_0 at M = 1, N >= 65536: 1.
+//  * wide Q6_K slices: R = 2 below N = 4096, else 4; row-split Q8_0 at
+//    M = 1, N >= 65536: 1.
 // IFX_GEMV_ROWS in {1, 2, 4, 8} overrides it (tuning; read once).
 static int rows_env() {
   static const int env = [] {
@@ -473,7 +474,11 @@ static int rows_env() {
 template <int QT, int MC>
 static int rows_per_wave(int N, int K) {
   if (rows_env()) return rows_env();
-  if constexpr (kWide<QT, MC> && (QT == kTypeQ6_K || QT == kTypeQ6_KR)) return 2;
+  // wide Q6_K (activation loads issued with the weights): 4 rows a wave
+  // from N = 4096 (LM head 151936 x 2048: 56 -> 50 us raw, 46 -> 44.4
+  // row-split; 14B down 5120 x 13824: 16.4 -> 15.6 us), 2 below (3B down
+  // 2048 x 11008: 6.6 against 6.9 at 4)
+  if constexpr (kWide<QT, MC> && (QT == kTypeQ6_K || QT == kTypeQ6_KR)) return N >= 4096 ? 4 : 2;
   // row-split Q8_0, one column, LM-head sized launches: the aligned rows
   // stream best one per wave (151936 x 2048: 51.5 against 54.2 us at 4)
   if constexpr (QT == kTypeQ8_0R && MC == 1)

@@ -62,14 +62,15 @@ LAUNCHES = [
     # config 3: LM head 151936 x 2048
     ("c3_q8_0_m1", "gemv", Q8_0, 1, (151936,), 2048, ["k_gemv<8,1,4,1,4,0,1>"]),
     ("c3_q8_0_m8", "gemv", Q8_0, 8, (151936,), 2048, ["k_mmvq<8,1,1,0>"]),
-    ("c3_q6_k_m1", "gemv", Q6_K, 1, (151936,), 2048, ["k_gemv<14,1,2,1,4,0,2>"]),
+    ("c3_q6_k_m1", "gemv", Q6_K, 1, (151936,), 2048, ["k_gemv<14,1,4,1,4,0,2>"]),
     ("c3_q6_k_m8", "gemv", Q6_K, 8, (151936,), 2048, ["k_gemv_slot<14,8,1,0,0>"]),
     ("c3_q8_0_r_m1", "gemv", Q8_0_R, 1, (151936,), 2048, ["k_gemv<108,1,1,1,4,0,1>"]),
-    ("c3_q6_k_r_m1", "gemv", Q6_K_R, 1, (151936,), 2048, ["k_gemv<114,1,2,1,4,0,2>"]),
+    ("c3_q6_k_r_m1", "gemv", Q6_K_R, 1, (151936,), 2048, ["k_gemv<114,1,4,1,4,0,2>"]),
     # config 4: the 14B decode layer at M = 16 / 32, and its Q4_K launches at M = 1 / 8
     ("c4_qkv_m16", "grouped", Q4_K, 16, QKV14, 5120, ["k_mmvq<12,1,8,0>"]),
     ("c4_o_m16", "gemv_accum", Q4_K, 16, (5120,), 5120, ["k_gemv_dq<12,0,1>"]),
     ("c4_gate_up_m16", "grouped", Q4_K, 16, (13824, 13824), 5120, ["k_mmvq<12,1,2,0>"]),
+    ("c4_down_m1", "gemv_accum", Q6_K, 1, (5120,), 13824, ["k_gemv<14,1,4,4,1,0,1,0,1>"]),
     ("c4_down_m16", "gemv_accum", Q6_K, 16, (5120,), 13824, ["k_gemv_dq<14,0,1>"]),
     ("c4_qkv_m32", "grouped", Q4_K, 32, QKV14, 5120, ["k_fill_zero", "k_gemv_dq<12,0,1>"]),
     ("c4_o_m32", "gemv_accum", Q4_K, 32, (5120,), 5120, ["k_gemv_dq<12,0,1>"]),
