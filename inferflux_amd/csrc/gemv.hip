@@ -227,15 +227,11 @@ __global__ __launch_bounds__(64 * G * P) void k_gemv(const GemvArgs args) {
     for (int idx = 0; idx < V; ++idx) {
       const int row = min(row0 + idx / MC, N - 1);
       const int64_t o = static_cast<int64_t>(col0 + min(idx % MC, mvalid - 1)) * N + row;
-      if constexpr (F16OUT) {
-        const uint16_t *p = bias_mode ? static_cast<const uint16_t *>(sg.bias) + row
-                                      : static_cast<const uint16_t *>(sg.Y) + o;
-        base[idx] = h2f(*p);
-      } else {
-        const float *p = bias_mode ? static_cast<const float *>(sg.bias) + row
-                                   : static_cast<const float *>(sg.Y) + o;
-        base[idx] = *p;
-      }
+      const int64_t at = bias_mode ? row : o;  // no offset from a null bias
+      if constexpr (F16OUT)
+        base[idx] = h2f(static_cast<const uint16_t *>(bias_mode ? sg.bias : sg.Y)[at]);
+      else
+        base[idx] = static_cast<const float *>(bias_mode ? sg.bias : sg.Y)[at];
     }
   }
 

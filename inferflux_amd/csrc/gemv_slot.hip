@@ -291,15 +291,11 @@ __global__ __launch_bounds__(64 * KW * (SW ? 2 : 1)) void k_gemv_slot(const Slot
     for (int mi = 0; mi < NM; ++mi) {
       const int m = min(2 * (mi & ~3) + 4 * h + (mi & 3), M - 1);
       const int64_t o = static_cast<int64_t>(m) * N + nc;
-      if constexpr (F16OUT) {
-        const uint16_t *p = bias_mode ? static_cast<const uint16_t *>(sg.bias) + nc
-                                      : static_cast<const uint16_t *>(sg.Y) + o;
-        early[mi] = h2f(*p);
-      } else {
-        const float *p = bias_mode ? static_cast<const float *>(sg.bias) + nc
-                                   : static_cast<const float *>(sg.Y) + o;
-        early[mi] = *p;
-      }
+      const int64_t at = bias_mode ? nc : o;  // no offset from a null bias
+      if constexpr (F16OUT)
+        early[mi] = h2f(static_cast<const uint16_t *>(bias_mode ? sg.bias : sg.Y)[at]);
+      else
+        early[mi] = static_cast<const float *>(bias_mode ? sg.bias : sg.Y)[at];
     }
   }
 
