@@ -412,7 +412,10 @@ int ifx_qgemv_mmq(int quant_type, const void *layout, const void *A_q8_1, void *
 int ifx_dequantize(int quant_type, const void *W, void *out, int out_dtype, int64_t n_rows,
                    int K, void *stream);
 
-/* 1 if ifx_qgemv handles (quant_type, M, N, K), else 0.
+/* 1 if ifx_qgemv handles (quant_type, M, N, K), else 0.  The weights and
+ * the Q8_1 activations must each stay below 0xF0000000 bytes and K at most
+ * 2^24 (the kernels' 32-bit buffer offsets; every GEMV / GEMM entry returns
+ * IFX_BAD_GEOMETRY beyond them).
  * Replaces FusedQuantGemm::SupportsQ8_1Activations (fused_quant_gemm.h:333)
  * combined with ShouldUseFusedPath (fused_quant_gemm.h:388-391). */
 int ifx_supports(int quant_type, int M, int N, int K);
