@@ -220,7 +220,8 @@ def test_epilogues(orc, dev, qtype, M):
 ])
 def test_slot_epilogues(orc, dev, qtype, M, N, K):
     """Store, accumulate and bias modes of the slot-packed MFMA GEMV, with
-    and without the workgroup split of K; fp16 outputs (never split)."""
+    and without the workgroup split of K; fp16 outputs (never split), stored
+    and accumulated."""
     import torch
     from inferflux_amd import ops, synth
     note(f"slot epilogue type={qtype} M={M} N={N} K={K}")
@@ -239,6 +240,10 @@ def test_slot_epilogues(orc, dev, qtype, M, N, K):
     check_rows(down(y), ye + bias[None, :])
     y16 = ops.qgemv(qtype, W, A, M, N, K, out_dtype=torch.float16)
     check_rows(down(y16).astype(np.float64), ye, tol=2e-3)
+    # fp16 accumulate: unsplit, the added term loaded ahead of the weights
+    b16 = base.astype(np.float16)
+    y16 = ops.qgemv(qtype, W, A, M, N, K, out=up(b16, dev), mode=ops.ACCUM)
+    check_rows(down(y16).astype(np.float64), ye + b16.astype(np.float64), tol=2e-3)
 
 
 # ------------------------------------------------------------ MFMA GEMM
