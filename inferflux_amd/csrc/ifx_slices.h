@@ -490,15 +490,6 @@ __device__ __forceinline__ void q6k_wide_math(const Q6Wide<R> &wt, const Q6WideA
   }
 }
 
-
-template <int MC, int R, typename AS>
-__device__ __forceinline__ void q6k_wide_compute(const Q6Wide<R> &wt, const AS &as, int mvalid,
-                                                 int s, float (&acc)[R][MC]) {
-  Q6WideAct<MC> a;
-  q6k_wide_act<MC>(a, as, mvalid, s);
-  q6k_wide_math<MC, R>(wt, a, s, acc);
-}
-
 template <int MC, int R, bool RS = false>
 __device__ __forceinline__ void q6k_wide(const rsrc_t Wr, rsrc_t Ar, const uint32_t (&voff)[R],
                                          const uint32_t (&soff)[R], uint32_t a_row, int mvalid,
